@@ -1,0 +1,278 @@
+"""Benchmark of the MI355X FP8 attention hot path (one JSON line on stdout).
+
+Default workload: BASELINE config 3, Wan-2.2 self-attention
+(B=1, H=40, S=75600, D=128, non-causal), bf16 inputs resident in HBM.
+One step = the whole hot path on one batch: per-(B,H) amax scale + e4m3fn
+quantization of Q, K and V (V written transposed) followed by the FP8
+flash-attention forward writing bf16 output -- the work of the reference's
+``fp8_flash_attention`` call.
+
+``value`` is whole-step throughput in TFLOP/s (algorithmic FLOPs
+4*B*H*S^2*D per step / step time).  ``roofline`` is the attention kernel's
+own MFMA roofline, its average launch time measured with HIP events on the
+stream the kernel runs on.  ``quantize`` reports the quantizer's HBM rate
+(5 bytes per element).  ``cpu_baseline`` times the reference's CPU
+attention path (torch SDPA on CPU, bf16) on a bounded sample.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config NAME]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+FP8_PEAK_TFLOPS = 5000.0  # MI355X dense FP8 MFMA, published
+HBM_PEAK_GBPS = 8000.0    # MI355X HBM3E, published
+
+
+def log(*a: object) -> None:
+    print(*a, file=sys.stderr, flush=True)
+
+
+def _traffic_from_profiles(kernel: str, workload: str) -> float | None:
+    """HBM bytes per launch recorded by the rocprofv3 counter runs under profiles/."""
+    f = ROOT / "profiles" / "traffic.json"
+    if not f.exists():
+        return None
+    try:
+        data = json.loads(f.read_text())
+        return float(data[workload][kernel]["hbm_bytes_per_launch"])
+    except (KeyError, ValueError, TypeError, json.JSONDecodeError):
+        return None
+
+
+def cpu_baseline(cfg, budget_s: float) -> dict:
+    """Reference CPU attention (torch SDPA, bf16, all host cores) on one head,
+    a row slice of the queries against all keys, extrapolated to the config."""
+    import torch
+
+    from oracle.cpu_sdpa import cpu_model, cpu_threads, sdpa_cpu
+
+    threads = cpu_threads()
+    gen = torch.Generator().manual_seed(cfg.seed)
+    k = torch.randn(1, 1, cfg.Skv, cfg.D, generator=gen).to(torch.bfloat16)
+    v = torch.randn(1, 1, cfg.Skv, cfg.D, generator=gen).to(torch.bfloat16)
+
+    def run(rows: int) -> float:
+        q = torch.randn(1, 1, rows, cfg.D, generator=gen).to(torch.bfloat16)
+        t0 = time.perf_counter()
+        sdpa_cpu(q, k, v)
+        return time.perf_counter() - t0
+
+    rows = min(256, cfg.Sq)
+    run(rows)  # warm-up (thread pool, allocator)
+    t = run(rows)
+    # grow the slice to fill about budget_s of CPU work
+    while rows < cfg.Sq and t < budget_s / 4:
+        rows = min(cfg.Sq, rows * 4)
+        t = run(rows)
+    flops_sample = 4.0 * rows * cfg.Skv * cfg.D
+    tflops = flops_sample / t / 1e12
+    return {
+        "value": round(tflops, 4),
+        "unit": "TFLOP/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": (f"torch SDPA on CPU (bf16, {threads} threads, {cpu_model()}): 1 head, "
+                   f"{rows} query rows x {cfg.Skv} keys x D={cfg.D} in {t:.2f} s; "
+                   f"full {cfg.name} extrapolates to "
+                   f"{cfg.flops / (tflops * 1e12):.0f} s"),
+    }
+
+
+def bench_attention(args, cfg) -> dict:
+    import torch
+
+    from repercep_runtime_amd import ops
+    from repercep_runtime_amd.workloads import QUANT_BYTES_PER_ELEM, attn_inputs
+
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    log(f"[bench] generating {cfg.name} inputs on {dev}")
+    q, k, v = attn_inputs(cfg, device=dev)
+    sm = cfg.D ** -0.5
+    prefix = cfg.prefix
+    out = torch.empty_like(q)
+    st = torch.cuda.current_stream(dev)
+
+    def step(ev=None):
+        if ev is not None:
+            ev[0].record(st)
+        qs, q8 = ops.scale_quantize(q, "bh", "bhsd")
+        ks, k8 = ops.scale_quantize(k, "bh", "bhsd")
+        vs, vt8 = ops.scale_quantize(v, "bh", "bhds")
+        if ev is not None:
+            ev[1].record(st)
+        ops.attention_fp8(q8.view(torch.uint8), k8.view(torch.uint8), vt8.view(torch.uint8),
+                          qs, ks, vs, sm, out=out, causal=cfg.causal, prefix_len=prefix,
+                          suffix_len=cfg.suffix)
+        if ev is not None:
+            ev[2].record(st)
+
+    log(f"[bench] warmup {args.warmup}")
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+
+    # whole-step timing
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0.record(st)
+    for _ in range(args.steps):
+        step()
+    t1.record(st)
+    torch.cuda.synchronize()
+    ms_per_step = t0.elapsed_time(t1) / args.steps
+    log(f"[bench] {args.steps} steps: {ms_per_step:.3f} ms/step")
+
+    # per-kernel split (same stream, separate pass so the events do not perturb the above)
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps)]
+    for e in evs:
+        step(e)
+    torch.cuda.synchronize()
+    quant_ms = sum(e[0].elapsed_time(e[1]) for e in evs) / len(evs)
+    attn_ms = sum(e[1].elapsed_time(e[2]) for e in evs) / len(evs)
+    log(f"[bench] split: quantize {quant_ms:.3f} ms, attention kernel {attn_ms:.3f} ms")
+
+    tflops_step = cfg.flops / (ms_per_step * 1e-3) / 1e12
+    tflops_attn = cfg.flops / (attn_ms * 1e-3) / 1e12
+    qbytes = QUANT_BYTES_PER_ELEM * cfg.quant_elems
+    q_gbps = qbytes / (quant_ms * 1e-3) / 1e9
+    res = {
+        "metric": "FP8 attn TFLOP/s + % FP8-MFMA peak (Wan-2.2 S=75600); quantize GB/s",
+        "value": round(tflops_step, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp8_e4m3fn (fp32 accumulate, bf16 out)",
+        "data": "synthetic: seeded N(0,1) bf16 Q/K/V generated on the GPU",
+        "config": {"workload": cfg.name, "B": cfg.B, "H": cfg.H, "Sq": cfg.Sq, "Skv": cfg.Skv,
+                   "D": cfg.D, "causal": cfg.causal, "scale_granularity": "per (b,h)",
+                   "flops_per_step": cfg.flops},
+        "roofline": {
+            "bound": "mfma",
+            "achieved": round(tflops_attn, 2),
+            "peak": FP8_PEAK_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(tflops_attn / FP8_PEAK_TFLOPS, 4),
+            "traffic": _traffic_from_profiles("attn_fwd_kernel", cfg.name),
+            "kernel": "attn_fwd_kernel",
+            "kernel_ms": round(attn_ms, 4),
+        },
+        "quantize": {
+            "achieved_GBps": round(q_gbps, 1),
+            "peak_GBps": HBM_PEAK_GBPS,
+            "frac": round(q_gbps / HBM_PEAK_GBPS, 4),
+            "ms": round(quant_ms, 4),
+            "bytes": qbytes,
+            "note": "Q, K, V: amax pass + finalize + apply (V transposed), 5 B/element",
+        },
+    }
+    del q, k, v, out
+    return res
+
+
+def bench_gemm(args, cfg) -> dict:
+    import torch
+
+    from repercep_runtime_amd import ops
+    from repercep_runtime_amd.workloads import gemm_inputs
+
+    dev = torch.device("cuda", 0)
+    a, w = gemm_inputs(cfg, device=dev)
+    sw, wt8 = ops.fp8_linear_weight(w)   # weights quantized once, like a loaded layer
+    out = torch.empty((cfg.M, cfg.N), dtype=torch.bfloat16, device=dev)
+    st = torch.cuda.current_stream(dev)
+
+    def step(ev=None):
+        if ev is not None:
+            ev[0].record(st)
+        sa, a8 = ops.scale_quantize(a, "tensor", "bhsd")
+        if ev is not None:
+            ev[1].record(st)
+        ops.fp8_gemm(a8.view(torch.uint8), wt8, sa, sw, b_transposed=True, out=out)
+        if ev is not None:
+            ev[2].record(st)
+
+    for _ in range(args.warmup):
+        step()
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    for e in evs:
+        step(e)
+    torch.cuda.synchronize()
+    step_ms = sum(e[0].elapsed_time(e[2]) for e in evs) / len(evs)
+    gemm_ms = sum(e[1].elapsed_time(e[2]) for e in evs) / len(evs)
+    quant_ms = sum(e[0].elapsed_time(e[1]) for e in evs) / len(evs)
+    tf = cfg.flops / (gemm_ms * 1e-3) / 1e12
+    return {
+        "metric": "FP8 scaled GEMM TFLOP/s (Wan FFN up-projection)",
+        "value": round(cfg.flops / (step_ms * 1e-3) / 1e12, 2), "unit": "TFLOP/s",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(step_ms, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "fp8_e4m3fn (fp32 accumulate, bf16 out)",
+        "data": "synthetic: seeded A ~ N(0,1), W ~ N(0,0.02) bf16",
+        "config": {"workload": cfg.name, "M": cfg.M, "K": cfg.K, "N": cfg.N},
+        "roofline": {"bound": "mfma", "achieved": round(tf, 2), "peak": FP8_PEAK_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(tf / FP8_PEAK_TFLOPS, 4),
+                     "traffic": None, "kernel": "gemm_kernel", "kernel_ms": round(gemm_ms, 4)},
+        "quantize": {"ms": round(quant_ms, 4),
+                     "achieved_GBps": round(5 * cfg.M * cfg.K / (quant_ms * 1e-3) / 1e9, 1)},
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--config", default="c3_wan_self",
+                    help="c1_cpu_runnable | c2_cosmos_self | c3_wan_self | c3_wan_cross | "
+                         "c5_shared_prefix | c4_wan_ffn_up")
+    ap.add_argument("--cpu-budget", type=float, default=12.0,
+                    help="seconds of CPU work for the cpu_baseline sample (0 disables)")
+    args = ap.parse_args()
+
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}, "
+              f"WORLD_SIZE={world}); the FP8 attention path shards over heads with no "
+              f"collective -- see DESIGN.md", file=sys.stderr)
+        return 2
+
+    import torch
+
+    if not torch.cuda.is_available():
+        print("bench.py: no GPU visible", file=sys.stderr)
+        return 1
+
+    from repercep_runtime_amd.workloads import ATTN_CONFIGS, C4
+
+    if args.config == C4.name:
+        res = bench_gemm(args, C4)
+    else:
+        cfg = ATTN_CONFIGS[args.config]
+        res = bench_attention(args, cfg)
+        if args.cpu_budget > 0:
+            log("[bench] timing the CPU baseline")
+            res["cpu_baseline"] = cpu_baseline(cfg, args.cpu_budget)
+    print(json.dumps(res), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

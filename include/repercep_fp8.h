@@ -1,0 +1,153 @@
+/*
+ * repercep_fp8.h -- C ABI of the MI355X (gfx950) FP8 attention hot path.
+ *
+ * One shared library, librepercep_fp8.so, built from the .hip sources in
+ * repercep_runtime_amd/csrc.  Plain pointers and sizes only: device
+ * pointers come from any HIP allocator, streams are hipStream_t passed as
+ * void* (NULL = the legacy default stream).  Every call is stream-ordered and
+ * asynchronous, allocates nothing, and returns an int status (RP_OK = 0);
+ * rp_last_error() gives a message for the calling thread's last failure.
+ *
+ * Number formats: FP8 codes are OCP e4m3fn bytes (bias 7, max 448,
+ * 0x7f/0xff = NaN, no infinities) -- the format gfx950 MFMAs consume.  Scales
+ * are *dequant* scales (fp32 multiplier that maps a code back to the input
+ * magnitude), one per group, exactly as the reference's _per_bh_scale
+ * returns them.
+ *
+ * Reference: miteshs/repercep-runtime.  Each entry point names the interface
+ * it replaces (file:line under the reference tree).
+ */
+#ifndef REPERCEP_FP8_H
+#define REPERCEP_FP8_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ------------------------------------------------------------- status */
+#define RP_OK 0
+#define RP_ERR_INVALID_ARGUMENT 1 /* null pointer, bad size/stride/enum        */
+#define RP_ERR_UNSUPPORTED 2      /* shape outside the compiled kernel set      */
+#define RP_ERR_WORKSPACE 3        /* workspace missing or too small             */
+#define RP_ERR_LAUNCH 4           /* the HIP runtime rejected a kernel launch   */
+
+/* Scale granularity (a group shares one amax/dequant scale). */
+#define RP_SCALE_PER_BH 0     /* one group per (batch, head): the reference's  */
+#define RP_SCALE_PER_TENSOR 1 /* one group for the whole tensor                */
+
+/* Layout of quantized codes written by rp_fp8_quantize*. */
+#define RP_LAYOUT_BHSD 0 /* (B, H, S, D) contiguous                              */
+#define RP_LAYOUT_BHDS 1 /* per (b, h): D rows of `ld` codes (S transposed), the */
+                         /* tail [S, ld) zero-filled; V operand of attention     */
+
+/* Output element type of rp_fp8_attn_fwd. */
+#define RP_OUT_BF16 0
+#define RP_OUT_F32 1
+
+/* Mask kinds of rp_fp8_attn_fwd. */
+#define RP_MASK_NONE 0
+#define RP_MASK_CAUSAL 1        /* key kv visible to query q iff kv <= q          */
+#define RP_MASK_SHARED_PREFIX 2 /* keys [0, prefix) visible to all queries; query */
+                                /* q sees suffix key j = kv - prefix iff          */
+                                /* j / suffix == q / suffix and j <= q            */
+
+int rp_abi_version(void);
+const char* rp_status_string(int status);
+const char* rp_last_error(void);
+
+/* ---------------------------------------------------------- quantize
+ * Input x: bf16 viewed as (B, H, S, D) with element strides sb, sh, ss for
+ * the first three axes and unit stride along D.  D must be a multiple of 8.
+ *
+ * rp_fp8_quant_workspace_bytes: device scratch the two-pass quantizer needs
+ * (per-block partial maxima plus per-group multipliers).
+ */
+size_t rp_fp8_quant_workspace_bytes(int64_t B, int64_t H, int64_t S, int64_t D, int granularity);
+
+/* Per-group dequant scales, dequant = bf16(max(amax|x|, bf16(1e-6)) / 425.6).
+ * Replaces _per_bh_scale, kernels/triton_kernels/fp8_flash_attn_hopper.py:374-385
+ * (OCP sibling of kernels/triton_kernels/fp8_flash_attn.py:425-436).
+ * dequant_out: float[B*H] (RP_SCALE_PER_BH) or float[1] (RP_SCALE_PER_TENSOR). */
+int rp_fp8_scale(const void* x, int64_t B, int64_t H, int64_t S, int64_t D,
+                 int64_t sb, int64_t sh, int64_t ss, int granularity,
+                 float* dequant_out, void* workspace, size_t workspace_bytes, void* stream);
+
+/* Codes = e4m3fn(clamp(x * (1 / dequant), -448, 448)), round to nearest even,
+ * given the per-group dequant scales.
+ * Replaces _quantize, kernels/triton_kernels/fp8_flash_attn_hopper.py:388-398
+ * (OCP sibling of kernels/triton_kernels/fp8_flash_attn.py:439-448) and the
+ * .contiguous() that follows it (fp8_flash_attn.py:526-528).
+ * layout RP_LAYOUT_BHSD: codes (B, H, S, D) contiguous, ld ignored.
+ * layout RP_LAYOUT_BHDS: codes (B, H, D, ld), ld >= S and ld % 128 == 0,
+ *                        D % 64 == 0; columns [S, ld) are written as 0. */
+int rp_fp8_quantize(const void* x, int64_t B, int64_t H, int64_t S, int64_t D,
+                    int64_t sb, int64_t sh, int64_t ss, int granularity,
+                    const float* dequant, uint8_t* codes, int layout, int64_t ld,
+                    void* stream);
+
+/* rp_fp8_scale followed by rp_fp8_quantize in one stream-ordered call
+ * (the pair _per_bh_scale + _quantize at fp8_flash_attn.py:522-528). */
+int rp_fp8_scale_quantize(const void* x, int64_t B, int64_t H, int64_t S, int64_t D,
+                          int64_t sb, int64_t sh, int64_t ss, int granularity,
+                          float* dequant_out, uint8_t* codes, int layout, int64_t ld,
+                          void* workspace, size_t workspace_bytes, void* stream);
+
+/* --------------------------------------------------------- attention
+ * FP8 flash-attention forward, FA-2 online softmax in fp32, both dot
+ * products on gfx950 e4m3 MFMAs, P re-quantized as e4m3fn(p * 448).
+ * Replaces the launch of _fp8_flash_attn_fwd_impl,
+ * kernels/triton_kernels/fp8_flash_attn.py:251-391 (launch :604-644) plus the
+ * fp32->input-dtype cast at :645 (written directly as bf16 here).
+ *   q8  : (B, H, Sq, D)  codes, contiguous
+ *   k8  : (B, H, Skv, D) codes, contiguous
+ *   vt8 : (B, H, D, ldv) codes, V transposed per head (RP_LAYOUT_BHDS),
+ *         ldv % 128 == 0, ldv >= Skv, columns [Skv, ldv) zero
+ *   q/k/v_scale : dequant scales, element bh*scale_stride for head bh = b*H+h
+ *         (scale_stride 1: per (b, h); 0: per tensor)
+ *   sm_scale : softmax temperature (the reference default is 1/sqrt(D))
+ *   out : (B, H, Sq, D) logical, element (b,h,s,d) at
+ *         out + b*osb + h*osh + s*oss + d (elements of out_dtype)
+ *   D in {64, 128}; mask per RP_MASK_*; Sq, Skv >= 1. */
+int rp_fp8_attn_fwd(const uint8_t* q8, const uint8_t* k8, const uint8_t* vt8, int64_t ldv,
+                    const float* q_scale, const float* k_scale, const float* v_scale,
+                    int scale_stride, float sm_scale, void* out, int out_dtype,
+                    int64_t osb, int64_t osh, int64_t oss,
+                    int B, int H, int Sq, int Skv, int D,
+                    int mask, int prefix_len, int suffix_len, void* stream);
+
+/* --------------------------------------------------------------- GEMM
+ * C (M, N) bf16 = bf16( fp32(A8 . B8) * (a_scale * b_scale) ).
+ * Replaces fp8_gemm_launch, kernels/hip/fp8_attn/fp8_gemm.hip:162-179
+ * (kernel :79-156), with B supplied K-contiguous: bt8 is B transposed,
+ * (N, K) with row stride ldb.  A8 (M, K) row stride lda; C row stride ldc.
+ * a_scale_dev / b_scale_dev: optional device pointers to the fp32 scales
+ * (e.g. produced by rp_fp8_scale with RP_SCALE_PER_TENSOR); when non-NULL
+ * they are used instead of the host values, avoiding a device->host read.
+ * K % 128 == 0; lda, ldb % 16 == 0. */
+int rp_fp8_gemm(const uint8_t* a8, const uint8_t* bt8, void* c,
+                int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldb, int64_t ldc,
+                float a_scale, float b_scale, const float* a_scale_dev,
+                const float* b_scale_dev, void* stream);
+
+/* FP8 byte transpose: dst (C, R) <- src (R, C); row strides lds, ldd.
+ * Turns the reference GEMM's row-major B (K, N) into the (N, K) operand. */
+int rp_fp8_transpose(const uint8_t* src, uint8_t* dst, int64_t R, int64_t C,
+                     int64_t lds, int64_t ldd, void* stream);
+
+/* ---------------------------------------------------------- self-test
+ * Device routines exposed so the tests can pin them exhaustively against
+ * the CPU oracle.  They run the same device functions the kernels above use.
+ * rp_selftest_e4m3: out[i] = e4m3fn code of clamp(x[i], -448, 448).
+ * rp_selftest_scale: dequant[i] / qmul[i] from bf16 amax bit patterns. */
+int rp_selftest_e4m3(const float* x, uint8_t* out, int64_t n, void* stream);
+int rp_selftest_scale(const uint16_t* amax_bits, float* dequant, float* qmul, int64_t n,
+                      void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* REPERCEP_FP8_H */

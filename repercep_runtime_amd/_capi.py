@@ -1,0 +1,122 @@
+"""ctypes binding of librepercep_fp8.so (declarations in include/repercep_fp8.h).
+
+The library is the product: there is no Python or CPU fallback.  When the
+shared object is missing or cannot be loaded every entry point raises
+``HipLibraryError`` with the reason, so a GPU host without the built library
+fails loudly instead of silently computing something else.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().parent / "lib" / "librepercep_fp8.so"
+
+RP_OK = 0
+RP_SCALE_PER_BH = 0
+RP_SCALE_PER_TENSOR = 1
+RP_LAYOUT_BHSD = 0
+RP_LAYOUT_BHDS = 1
+RP_OUT_BF16 = 0
+RP_OUT_F32 = 1
+RP_MASK_NONE = 0
+RP_MASK_CAUSAL = 1
+RP_MASK_SHARED_PREFIX = 2
+
+#: Every function include/repercep_fp8.h declares.
+EXPORTS = (
+    "rp_abi_version", "rp_status_string", "rp_last_error",
+    "rp_fp8_quant_workspace_bytes", "rp_fp8_scale", "rp_fp8_quantize",
+    "rp_fp8_scale_quantize", "rp_fp8_attn_fwd", "rp_fp8_gemm", "rp_fp8_transpose",
+    "rp_selftest_e4m3", "rp_selftest_scale",
+)
+
+
+class HipLibraryError(RuntimeError):
+    """The gfx950 library is missing, failed to load, or a call failed."""
+
+
+_lib: ctypes.CDLL | None = None
+_load_error: str | None = None
+
+_vp = ctypes.c_void_p
+_i64 = ctypes.c_int64
+_int = ctypes.c_int
+_f32 = ctypes.c_float
+_sz = ctypes.c_size_t
+
+
+def _declare(L: ctypes.CDLL) -> None:
+    L.rp_abi_version.restype = _int
+    L.rp_abi_version.argtypes = []
+    L.rp_status_string.restype = ctypes.c_char_p
+    L.rp_status_string.argtypes = [_int]
+    L.rp_last_error.restype = ctypes.c_char_p
+    L.rp_last_error.argtypes = []
+    L.rp_fp8_quant_workspace_bytes.restype = _sz
+    L.rp_fp8_quant_workspace_bytes.argtypes = [_i64, _i64, _i64, _i64, _int]
+    L.rp_fp8_scale.restype = _int
+    L.rp_fp8_scale.argtypes = [_vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _int, _vp, _vp,
+                               _sz, _vp]
+    L.rp_fp8_quantize.restype = _int
+    L.rp_fp8_quantize.argtypes = [_vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _int, _vp, _vp,
+                                  _int, _i64, _vp]
+    L.rp_fp8_scale_quantize.restype = _int
+    L.rp_fp8_scale_quantize.argtypes = [_vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _int, _vp,
+                                        _vp, _int, _i64, _vp, _sz, _vp]
+    L.rp_fp8_attn_fwd.restype = _int
+    L.rp_fp8_attn_fwd.argtypes = [_vp, _vp, _vp, _i64, _vp, _vp, _vp, _int, _f32, _vp, _int,
+                                  _i64, _i64, _i64, _int, _int, _int, _int, _int, _int, _int,
+                                  _int, _vp]
+    L.rp_fp8_gemm.restype = _int
+    L.rp_fp8_gemm.argtypes = [_vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _f32, _f32,
+                              _vp, _vp, _vp]
+    L.rp_fp8_transpose.restype = _int
+    L.rp_fp8_transpose.argtypes = [_vp, _vp, _i64, _i64, _i64, _i64, _vp]
+    L.rp_selftest_e4m3.restype = _int
+    L.rp_selftest_e4m3.argtypes = [_vp, _vp, _i64, _vp]
+    L.rp_selftest_scale.restype = _int
+    L.rp_selftest_scale.argtypes = [_vp, _vp, _vp, _i64, _vp]
+
+
+def lib() -> ctypes.CDLL:
+    """The loaded library; raises HipLibraryError if it is not available."""
+    global _lib, _load_error
+    if _lib is not None:
+        return _lib
+    path = Path(os.environ.get("REPERCEP_FP8_LIB", str(LIB_PATH)))
+    if not path.exists():
+        _load_error = (f"{path} is missing: build it with "
+                       f"`python -c 'import __graft_entry__ as g; g.build()'`")
+        raise HipLibraryError(_load_error)
+    try:
+        L = ctypes.CDLL(str(path))
+    except OSError as exc:
+        _load_error = f"cannot load {path}: {exc}"
+        raise HipLibraryError(_load_error) from exc
+    _declare(L)
+    _lib = L
+    return L
+
+
+def available() -> bool:
+    try:
+        lib()
+    except HipLibraryError:
+        return False
+    return True
+
+
+def load_error() -> str | None:
+    return _load_error
+
+
+def check(status: int, what: str) -> None:
+    """Raise HipLibraryError for a non-zero status, with the library's message."""
+    if status != RP_OK:
+        L = lib()
+        msg = (L.rp_last_error() or b"").decode(errors="replace")
+        kind = (L.rp_status_string(status) or b"").decode(errors="replace")
+        raise HipLibraryError(f"{what}: {kind} ({status}): {msg}")

@@ -1,0 +1,76 @@
+"""Build librepercep_fp8.so (gfx950) in-tree from repercep_runtime_amd/csrc.
+
+Each .hip translation unit is compiled by hipcc in parallel into
+repercep_runtime_amd/_build/, then linked into repercep_runtime_amd/lib/.
+Flags:
+  --offload-arch=gfx950                     CDNA4 only, no host/device dual paths
+  -O3 -std=c++17 -fPIC
+  -Xclang -target-feature -Xclang -packed-fp32-ops
+                                            no packed-FP32 VALU forms
+  -mllvm -disable-promote-alloca-to-lds     keep per-thread staging in VGPRs
+No fast-math anywhere: the quantizer's fp32 division and reciprocal must be
+correctly rounded (IEEE), which is hipcc's default.
+"""
+
+from __future__ import annotations
+
+import os
+import subprocess
+import sys
+from concurrent.futures import ThreadPoolExecutor
+from pathlib import Path
+
+PKG = Path(__file__).resolve().parent
+CSRC = PKG / "csrc"
+BUILD = PKG / "_build"
+LIB_DIR = PKG / "lib"
+LIB = LIB_DIR / "librepercep_fp8.so"
+ROOT = PKG.parent
+
+HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+ARCH = "gfx950"
+COMMON = [
+    f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-mllvm", "-disable-promote-alloca-to-lds",
+    f"-I{ROOT / 'include'}",
+    "-Wall", "-Wno-unused-function",
+]
+SOURCES = ["rp_api.hip", "rp_quant.hip", "rp_attn.hip", "rp_gemm.hip"]
+
+
+def _compile(src: Path, obj: Path, verbose: bool) -> None:
+    cmd = [HIPCC, *COMMON, "-c", str(src), "-o", str(obj)]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    # hipcc's host pass reports the device-only feature flag as unknown; drop that noise.
+    noise = "is not a recognized feature for this target"
+    err = "\n".join(line for line in res.stderr.splitlines() if noise not in line)
+    if res.returncode != 0:
+        raise RuntimeError(f"hipcc failed for {src.name}:\n{err}")
+    if err.strip() and verbose:
+        print(err)
+
+
+def build(verbose: bool = False) -> Path:
+    """Compile every HIP source for gfx950 and link the shared library."""
+    BUILD.mkdir(exist_ok=True)
+    LIB_DIR.mkdir(exist_ok=True)
+    objs = [BUILD / (Path(s).stem + ".o") for s in SOURCES]
+    jobs = min(len(SOURCES), max(1, int(os.environ.get("MAX_JOBS", os.cpu_count() or 4))))
+    with ThreadPoolExecutor(max_workers=jobs) as ex:
+        futs = [ex.submit(_compile, CSRC / s, o, verbose) for s, o in zip(SOURCES, objs)]
+        for f in futs:
+            f.result()
+    tmp = LIB.with_suffix(".so.tmp")
+    cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    subprocess.run(cmd, check=True, capture_output=not verbose)
+    tmp.replace(LIB)
+    return LIB
+
+
+if __name__ == "__main__":
+    print(build(verbose="-v" in sys.argv))

@@ -1,0 +1,81 @@
+// Shared device helpers for the gfx950 FP8 attention path.
+//
+// Everything here is written for CDNA4 (gfx950): wave64, OCP e4m3fn FP8
+// (bias 7, max 448, S.1111.111 = NaN), the f8f6f4 MFMA family, 160 KiB LDS.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/repercep_fp8.h"
+
+namespace rp {
+
+typedef int i32x8 __attribute__((ext_vector_type(8)));
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+constexpr int kWave = 64;
+constexpr float kE4m3Max = 448.0f;
+// 0.95 * 448 evaluated in double is 425.59999999999997; torch applies the
+// scalar divisor as the nearest fp32 value, 425.6f.
+constexpr float kScaleDivisor = 425.6f;
+
+// ------------------------------------------------------------------ bf16
+__device__ __forceinline__ float bf16_to_f32(uint32_t b) { return __uint_as_float(b << 16); }
+
+// fp32 -> bf16 bits, round to nearest even; NaN stays NaN (quieted).
+__device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x40u;
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return u >> 16;
+}
+
+__device__ __forceinline__ float bf16_round(float f) { return bf16_to_f32(f32_to_bf16_bits(f)); }
+
+// -------------------------------------------------------------- e4m3fn
+// Two fp32 -> two e4m3fn codes in bits [16*hi, 16*hi+16) of `old`, using the
+// gfx950 hardware conversion (round to nearest even).
+template <bool kHi>
+__device__ __forceinline__ int cvt_pk_e4m3(float a, float b, int old) {
+  return __builtin_amdgcn_cvt_pk_fp8_f32(a, b, old, kHi);
+}
+
+// Four fp32 -> one dword of codes, element 0 in the low byte.
+__device__ __forceinline__ uint32_t pack4_e4m3(float a, float b, float c, float d) {
+  int r = cvt_pk_e4m3<false>(a, b, 0);
+  r = cvt_pk_e4m3<true>(c, d, r);
+  return (uint32_t)r;
+}
+
+// Reference clamp: Tensor.clamp(-448, 448) propagates NaN.
+__device__ __forceinline__ float clamp_e4m3(float v) {
+  float c = fminf(fmaxf(v, -kE4m3Max), kE4m3Max);
+  return (v != v) ? v : c;
+}
+
+// ---------------------------------------------------------- reductions
+template <typename T>
+__device__ __forceinline__ T shfl_xor(T v, int mask) {
+  return __shfl_xor(v, mask, kWave);
+}
+
+__device__ __forceinline__ uint32_t umax32(uint32_t a, uint32_t b) { return a > b ? a : b; }
+
+// Dequant scale from the bf16 bit pattern of a group's |x| maximum, as the
+// reference computes it: clamp in bf16 against bf16(1e-6), divide by 425.6
+// in fp32, round the quotient to bf16.  Division is IEEE (this file is never
+// built with fast-math).
+__device__ __forceinline__ float dequant_from_amax_bits(uint32_t amax_bits) {
+  const float lo = __uint_as_float(0x3586u << 16);  // bf16(1e-6) = 9.98377799987793e-07
+  float a = bf16_to_f32(amax_bits);
+  if (!(a != a) && a < lo) a = lo;
+  return bf16_round(a / kScaleDivisor);
+}
+
+}  // namespace rp
+
+// Thread-local last-error message shared by all entry points.
+extern "C" void rp_set_error(const char* fmt, ...);

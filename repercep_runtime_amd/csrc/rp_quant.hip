@@ -1,0 +1,453 @@
+// Per-group amax scaling and BF16 -> OCP e4m3fn quantization for gfx950.
+//
+// Behaviour follows the reference quantizer
+// (kernels/triton_kernels/fp8_flash_attn_hopper.py:374-398; gfx942 sibling
+// kernels/triton_kernels/fp8_flash_attn.py:425-448):
+//   dequant = bf16(max(amax|x|, bf16(1e-6)) / 425.6)       per group
+//   code    = e4m3fn(clamp(float(x) * (1/dequant), +-448))  round to nearest even
+// The reference runs this as six torch ops over fp32 temporaries (about
+// 33 B of HBM traffic per element).  Here it is two streaming passes plus a
+// tiny per-group finalize: 2 B/element to find the maximum, 2 B read + 1 B
+// written to quantize -- 5 B/element, the algorithmic minimum.
+//
+// Pass 1 (amax_partial): each 256-thread block reduces a contiguous slab of
+//   one group with packed 16-bit integer max over |x| bit patterns (exact
+//   and order-free; NaN patterns sort above +inf, so NaN propagates like
+//   torch.amax) and writes one partial per block -- no atomics, no memset.
+// Pass 2 (scale_finalize): one block per group folds its partials and forms
+//   the dequant scale.
+// Pass 3 (apply / apply_t): re-reads x, multiplies by the correctly rounded
+//   fp32 reciprocal and converts with the gfx950 v_cvt_pk_fp8_f32.
+//   apply_t writes V transposed per head (D rows of ld codes), which is the
+//   layout the attention kernel's P.V MFMA reads K-contiguous.
+//
+// This translation unit must not be compiled with fast-math: the scale
+// division and the reciprocal have to be IEEE correctly rounded.
+
+#include "rp_common.h"
+
+#include <stdarg.h>
+#include <stdio.h>
+
+namespace rp {
+namespace {
+
+constexpr int kQThreads = 256;
+constexpr int64_t kElemsPerBlock = 16384;  // 32 KiB of bf16 per block per pass
+
+struct QParams {
+  const uint16_t* x;
+  int64_t B, H, S, D;
+  int64_t sb, sh, ss;
+  int64_t rows_per_group;  // rows (one row = D elements) in one group
+  int64_t ngroups;
+  int64_t rpb;             // rows per block
+  int64_t nbg;             // blocks per group
+  int vpr_log2;            // log2(D / 8): vectors of 8 elements per row
+};
+
+// Walks global rows r = bh*S + s of the (B, H, S, D) view.
+struct RowCursor {
+  int64_t s, bh, base;
+  __device__ void init(int64_t r, const QParams& p) {
+    bh = r / p.S;
+    s = r - bh * p.S;
+    base = (bh / p.H) * p.sb + (bh % p.H) * p.sh;
+  }
+  __device__ void advance(int64_t step, const QParams& p) {
+    s += step;
+    while (s >= p.S) {
+      s -= p.S;
+      ++bh;
+      base = (bh / p.H) * p.sb + (bh % p.H) * p.sh;
+    }
+  }
+};
+
+__device__ __forceinline__ uint32_t pk_umax16(uint32_t a, uint32_t b) {
+  // two independent 16-bit unsigned maxima in one dword
+  uint32_t lo = umax32(a & 0xffffu, b & 0xffffu);
+  uint32_t hi = umax32(a >> 16, b >> 16);
+  return lo | (hi << 16);
+}
+
+__global__ __launch_bounds__(kQThreads) void amax_partial_kernel(QParams p, uint32_t* partial) {
+  const int64_t blk = blockIdx.x;
+  const int64_t g = blk / p.nbg;
+  const int64_t j = blk - g * p.nbg;
+  const int64_t first = j * p.rpb;
+  const int64_t nrows = min(p.rpb, p.rows_per_group - first);
+  const int vpr_mask = (1 << p.vpr_log2) - 1;
+  const int col = threadIdx.x & vpr_mask;
+  const int64_t roff = threadIdx.x >> p.vpr_log2;
+  const int64_t step = kQThreads >> p.vpr_log2;
+
+  uint32_t m = 0;
+  if (roff < nrows) {
+    RowCursor cur;
+    cur.init(g * p.rows_per_group + first + roff, p);
+    for (int64_t r = roff; r < nrows; r += step) {
+      const uint4 v = *reinterpret_cast<const uint4*>(p.x + cur.base + cur.s * p.ss + col * 8);
+      m = pk_umax16(m, v.x & 0x7fff7fffu);
+      m = pk_umax16(m, v.y & 0x7fff7fffu);
+      m = pk_umax16(m, v.z & 0x7fff7fffu);
+      m = pk_umax16(m, v.w & 0x7fff7fffu);
+      cur.advance(step, p);
+    }
+  }
+  uint32_t m16 = umax32(m & 0xffffu, m >> 16);
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) m16 = umax32(m16, (uint32_t)shfl_xor((int)m16, o));
+  __shared__ uint32_t wmax[kQThreads / kWave];
+  if ((threadIdx.x & (kWave - 1)) == 0) wmax[threadIdx.x / kWave] = m16;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    uint32_t r = wmax[0];
+#pragma unroll
+    for (int w = 1; w < kQThreads / kWave; ++w) r = umax32(r, wmax[w]);
+    partial[blk] = r;
+  }
+}
+
+__global__ __launch_bounds__(kQThreads) void scale_finalize_kernel(const uint32_t* partial,
+                                                                   int64_t nbg, float* dequant) {
+  const int64_t g = blockIdx.x;
+  uint32_t m = 0;
+  for (int64_t i = threadIdx.x; i < nbg; i += kQThreads) m = umax32(m, partial[g * nbg + i]);
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) m = umax32(m, (uint32_t)shfl_xor((int)m, o));
+  __shared__ uint32_t wmax[kQThreads / kWave];
+  if ((threadIdx.x & (kWave - 1)) == 0) wmax[threadIdx.x / kWave] = m;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    uint32_t r = wmax[0];
+#pragma unroll
+    for (int w = 1; w < kQThreads / kWave; ++w) r = umax32(r, wmax[w]);
+    dequant[g] = dequant_from_amax_bits(r);
+  }
+}
+
+__device__ __forceinline__ uint32_t quant4(uint32_t lo_pair, uint32_t hi_pair, float qm) {
+  const float a = clamp_e4m3(bf16_to_f32(lo_pair & 0xffffu) * qm);
+  const float b = clamp_e4m3(bf16_to_f32(lo_pair >> 16) * qm);
+  const float c = clamp_e4m3(bf16_to_f32(hi_pair & 0xffffu) * qm);
+  const float d = clamp_e4m3(bf16_to_f32(hi_pair >> 16) * qm);
+  return pack4_e4m3(a, b, c, d);
+}
+
+// BHSD output: codes[r*D + d] for global row r = bh*S + s.
+__global__ __launch_bounds__(kQThreads) void quant_apply_kernel(QParams p, const float* dequant,
+                                                                int per_bh, uint8_t* codes) {
+  const int64_t blk = blockIdx.x;
+  const int64_t g = blk / p.nbg;
+  const int64_t j = blk - g * p.nbg;
+  const int64_t first = j * p.rpb;
+  const int64_t nrows = min(p.rpb, p.rows_per_group - first);
+  const int vpr_mask = (1 << p.vpr_log2) - 1;
+  const int col = threadIdx.x & vpr_mask;
+  const int64_t roff = threadIdx.x >> p.vpr_log2;
+  const int64_t step = kQThreads >> p.vpr_log2;
+  if (roff >= nrows) return;
+
+  RowCursor cur;
+  const int64_t r0 = g * p.rows_per_group + first + roff;
+  cur.init(r0, p);
+  // group of the first row; a block never straddles groups
+  const float qm = 1.0f / dequant[per_bh ? cur.bh : 0];
+  int64_t r = r0;
+  for (int64_t k = roff; k < nrows; k += step) {
+    const uint4 v = *reinterpret_cast<const uint4*>(p.x + cur.base + cur.s * p.ss + col * 8);
+    uint2 o;
+    o.x = quant4(v.x, v.y, qm);
+    o.y = quant4(v.z, v.w, qm);
+    *reinterpret_cast<uint2*>(codes + r * p.D + col * 8) = o;
+    cur.advance(step, p);
+    r += step;
+  }
+}
+
+// BHDS output: per head, codes[(bh*D + d)*ld + s]; columns [S, ld) zeroed.
+// Tile: 128 rows (s) x 64 columns (d).  Thread t loads rows 4*(t&31)+i,
+// column chunk t>>5 (8 elements), transposes its 4x8 codes in registers and
+// writes 8 dwords [d][s..s+3] into LDS; the tile then leaves as 64 rows of
+// 128 contiguous codes.
+__global__ __launch_bounds__(kQThreads) void quant_apply_t_kernel(QParams p, const float* dequant,
+                                                                  int per_bh, uint8_t* codes,
+                                                                  int64_t ld) {
+  __shared__ __attribute__((aligned(16))) uint8_t tile[64 * 128];
+  const int64_t s0 = (int64_t)blockIdx.x * 128;
+  const int64_t d0 = (int64_t)blockIdx.y * 64;
+  const int64_t bh = blockIdx.z;
+  const float qm = 1.0f / dequant[per_bh ? bh : 0];
+  const int64_t base = (bh / p.H) * p.sb + (bh % p.H) * p.sh + d0;
+  const int r4 = threadIdx.x & 31;
+  const int c = threadIdx.x >> 5;
+
+  uint32_t w[4][2];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int64_t s = s0 + 4 * r4 + i;
+    if (s < p.S) {
+      const uint4 v = *reinterpret_cast<const uint4*>(p.x + base + s * p.ss + c * 8);
+      w[i][0] = quant4(v.x, v.y, qm);
+      w[i][1] = quant4(v.z, v.w, qm);
+    } else {
+      w[i][0] = 0u;
+      w[i][1] = 0u;
+    }
+  }
+  // 4x4 byte transposes: rows i (s) x columns e (d) -> dword per column.
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const uint32_t t0 = __builtin_amdgcn_perm(w[1][h], w[0][h], 0x05010400u);
+    const uint32_t t1 = __builtin_amdgcn_perm(w[1][h], w[0][h], 0x07030602u);
+    const uint32_t t2 = __builtin_amdgcn_perm(w[3][h], w[2][h], 0x05010400u);
+    const uint32_t t3 = __builtin_amdgcn_perm(w[3][h], w[2][h], 0x07030602u);
+    const uint32_t col0 = __builtin_amdgcn_perm(t2, t0, 0x05040100u);
+    const uint32_t col1 = __builtin_amdgcn_perm(t2, t0, 0x07060302u);
+    const uint32_t col2 = __builtin_amdgcn_perm(t3, t1, 0x05040100u);
+    const uint32_t col3 = __builtin_amdgcn_perm(t3, t1, 0x07060302u);
+    const int d = c * 8 + h * 4;
+    *reinterpret_cast<uint32_t*>(&tile[(d + 0) * 128 + 4 * r4]) = col0;
+    *reinterpret_cast<uint32_t*>(&tile[(d + 1) * 128 + 4 * r4]) = col1;
+    *reinterpret_cast<uint32_t*>(&tile[(d + 2) * 128 + 4 * r4]) = col2;
+    *reinterpret_cast<uint32_t*>(&tile[(d + 3) * 128 + 4 * r4]) = col3;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    const int dr = (threadIdx.x >> 3) + 32 * k;
+    const int ch = threadIdx.x & 7;
+    const uint4 v = *reinterpret_cast<const uint4*>(&tile[dr * 128 + ch * 16]);
+    *reinterpret_cast<uint4*>(codes + (bh * p.D + d0 + dr) * ld + s0 + ch * 16) = v;
+  }
+}
+
+__global__ void selftest_e4m3_kernel(const float* x, uint8_t* out, int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const float v = clamp_e4m3(x[i]);
+  out[i] = (uint8_t)(cvt_pk_e4m3<false>(v, 0.0f, 0) & 0xff);
+}
+
+__global__ void selftest_scale_kernel(const uint16_t* amax_bits, float* dequant, float* qmul,
+                                      int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const float dq = dequant_from_amax_bits(amax_bits[i]);
+  dequant[i] = dq;
+  qmul[i] = 1.0f / dq;
+}
+
+// ------------------------------------------------------------------ host
+struct Plan {
+  QParams p;
+  int per_bh;
+  size_t ws_bytes;
+};
+
+bool is_pow2(int64_t v) { return v > 0 && (v & (v - 1)) == 0; }
+int ilog2(int64_t v) {
+  int r = 0;
+  while ((int64_t(1) << r) < v) ++r;
+  return r;
+}
+
+int make_plan(const void* x, int64_t B, int64_t H, int64_t S, int64_t D, int64_t sb, int64_t sh,
+              int64_t ss, int granularity, Plan* out) {
+  if (B <= 0 || H <= 0 || S <= 0 || D <= 0) {
+    rp_set_error("quantize: non-positive shape (%lld, %lld, %lld, %lld)", (long long)B,
+                 (long long)H, (long long)S, (long long)D);
+    return RP_ERR_INVALID_ARGUMENT;
+  }
+  if (granularity != RP_SCALE_PER_BH && granularity != RP_SCALE_PER_TENSOR) {
+    rp_set_error("quantize: unknown granularity %d", granularity);
+    return RP_ERR_INVALID_ARGUMENT;
+  }
+  if (D % 8 != 0) {
+    rp_set_error("quantize: D=%lld must be a multiple of 8", (long long)D);
+    return RP_ERR_UNSUPPORTED;
+  }
+  if ((reinterpret_cast<uintptr_t>(x) & 15u) != 0 || (ss % 8) != 0 || (sh % 8) != 0 ||
+      (sb % 8) != 0) {
+    rp_set_error("quantize: input pointer and strides must be 16-byte aligned");
+    return RP_ERR_UNSUPPORTED;
+  }
+  QParams p{};
+  p.x = static_cast<const uint16_t*>(x);
+  const bool contiguous = (ss == D) && (sh == S * D) && (sb == H * S * D);
+  if (contiguous) {
+    // A contiguous tensor is re-viewed as rows of 8 elements: every group is
+    // then a contiguous run of rows and the per-thread walk is one vector.
+    const int64_t rows_per_bh = S * D / 8;
+    p.B = B; p.H = H; p.S = rows_per_bh; p.D = 8;
+    p.sb = H * S * D; p.sh = S * D; p.ss = 8;
+  } else {
+    if (!is_pow2(D) || D > 2048) {
+      rp_set_error("quantize: strided input needs a power-of-two D <= 2048 (got %lld)",
+                   (long long)D);
+      return RP_ERR_UNSUPPORTED;
+    }
+    p.B = B; p.H = H; p.S = S; p.D = D; p.sb = sb; p.sh = sh; p.ss = ss;
+  }
+  const int64_t total_rows = p.B * p.H * p.S;
+  p.ngroups = granularity == RP_SCALE_PER_BH ? B * H : 1;
+  p.rows_per_group = total_rows / p.ngroups;
+  p.rpb = kElemsPerBlock / p.D;
+  p.nbg = (p.rows_per_group + p.rpb - 1) / p.rpb;
+  p.vpr_log2 = ilog2(p.D / 8);
+  out->p = p;
+  out->per_bh = granularity == RP_SCALE_PER_BH;
+  out->ws_bytes = (size_t)(p.ngroups * p.nbg) * sizeof(uint32_t);
+  return RP_OK;
+}
+
+int check_launch(const char* what) {
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) {
+    rp_set_error("%s: launch failed: %s", what, hipGetErrorString(e));
+    return RP_ERR_LAUNCH;
+  }
+  return RP_OK;
+}
+
+int launch_scale(const Plan& pl, float* dequant_out, void* ws, size_t ws_bytes, hipStream_t st) {
+  if (ws == nullptr || ws_bytes < pl.ws_bytes) {
+    rp_set_error("scale: workspace of %zu bytes needed, got %zu", pl.ws_bytes, ws_bytes);
+    return RP_ERR_WORKSPACE;
+  }
+  uint32_t* partial = static_cast<uint32_t*>(ws);
+  const int64_t nblocks = pl.p.ngroups * pl.p.nbg;
+  hipLaunchKernelGGL(amax_partial_kernel, dim3((unsigned)nblocks), dim3(kQThreads), 0, st, pl.p,
+                     partial);
+  int rc = check_launch("amax_partial");
+  if (rc) return rc;
+  hipLaunchKernelGGL(scale_finalize_kernel, dim3((unsigned)pl.p.ngroups), dim3(kQThreads), 0, st,
+                     partial, pl.p.nbg, dequant_out);
+  return check_launch("scale_finalize");
+}
+
+int launch_apply(const Plan& pl, const void* x, int64_t B, int64_t H, int64_t S, int64_t D,
+                 int64_t sb, int64_t sh, int64_t ss, const float* dequant, uint8_t* codes,
+                 int layout, int64_t ld, hipStream_t st) {
+  if (layout == RP_LAYOUT_BHSD) {
+    const int64_t nblocks = pl.p.ngroups * pl.p.nbg;
+    hipLaunchKernelGGL(quant_apply_kernel, dim3((unsigned)nblocks), dim3(kQThreads), 0, st, pl.p,
+                       dequant, pl.per_bh, codes);
+    return check_launch("quant_apply");
+  }
+  if (layout != RP_LAYOUT_BHDS) {
+    rp_set_error("quantize: unknown layout %d", layout);
+    return RP_ERR_INVALID_ARGUMENT;
+  }
+  if (D % 64 != 0 || ld < S || ld % 128 != 0) {
+    rp_set_error("quantize(BHDS): needs D %% 64 == 0 and ld >= S with ld %% 128 == 0 "
+                 "(D=%lld S=%lld ld=%lld)", (long long)D, (long long)S, (long long)ld);
+    return RP_ERR_UNSUPPORTED;
+  }
+  QParams q{};
+  q.x = static_cast<const uint16_t*>(x);
+  q.B = B; q.H = H; q.S = S; q.D = D; q.sb = sb; q.sh = sh; q.ss = ss;
+  if (B * H > 65535) {
+    rp_set_error("quantize(BHDS): B*H=%lld exceeds the grid limit", (long long)(B * H));
+    return RP_ERR_UNSUPPORTED;
+  }
+  dim3 grid((unsigned)(ld / 128), (unsigned)(D / 64), (unsigned)(B * H));
+  hipLaunchKernelGGL(quant_apply_t_kernel, grid, dim3(kQThreads), 0, st, q, dequant, pl.per_bh,
+                     codes, ld);
+  return check_launch("quant_apply_t");
+}
+
+}  // namespace
+}  // namespace rp
+
+using namespace rp;
+
+extern "C" size_t rp_fp8_quant_workspace_bytes(int64_t B, int64_t H, int64_t S, int64_t D,
+                                               int granularity) {
+  // Assumes a contiguous input; the strided plan never needs more rows per
+  // group, and its rows hold at least as many elements.
+  Plan pl;
+  const void* dummy = reinterpret_cast<const void*>(uintptr_t(256));
+  if (make_plan(dummy, B, H, S, D, H * S * D, S * D, D, granularity, &pl) != RP_OK) return 0;
+  Plan pl2;
+  size_t strided = 0;
+  if (make_plan(dummy, B, H, S, D, H * S * D + 8, S * D + 8, D, granularity, &pl2) == RP_OK)
+    strided = pl2.ws_bytes;
+  return pl.ws_bytes > strided ? pl.ws_bytes : strided;
+}
+
+extern "C" int rp_fp8_scale(const void* x, int64_t B, int64_t H, int64_t S, int64_t D, int64_t sb,
+                            int64_t sh, int64_t ss, int granularity, float* dequant_out,
+                            void* workspace, size_t workspace_bytes, void* stream) {
+  if (x == nullptr || dequant_out == nullptr) {
+    rp_set_error("scale: null pointer");
+    return RP_ERR_INVALID_ARGUMENT;
+  }
+  Plan pl;
+  int rc = make_plan(x, B, H, S, D, sb, sh, ss, granularity, &pl);
+  if (rc) return rc;
+  return launch_scale(pl, dequant_out, workspace, workspace_bytes,
+                      static_cast<hipStream_t>(stream));
+}
+
+extern "C" int rp_fp8_quantize(const void* x, int64_t B, int64_t H, int64_t S, int64_t D,
+                               int64_t sb, int64_t sh, int64_t ss, int granularity,
+                               const float* dequant, uint8_t* codes, int layout, int64_t ld,
+                               void* stream) {
+  if (x == nullptr || dequant == nullptr || codes == nullptr) {
+    rp_set_error("quantize: null pointer");
+    return RP_ERR_INVALID_ARGUMENT;
+  }
+  Plan pl;
+  int rc = make_plan(x, B, H, S, D, sb, sh, ss, granularity, &pl);
+  if (rc) return rc;
+  return launch_apply(pl, x, B, H, S, D, sb, sh, ss, dequant, codes, layout, ld,
+                      static_cast<hipStream_t>(stream));
+}
+
+extern "C" int rp_fp8_scale_quantize(const void* x, int64_t B, int64_t H, int64_t S, int64_t D,
+                                     int64_t sb, int64_t sh, int64_t ss, int granularity,
+                                     float* dequant_out, uint8_t* codes, int layout, int64_t ld,
+                                     void* workspace, size_t workspace_bytes, void* stream) {
+  if (x == nullptr || dequant_out == nullptr || codes == nullptr) {
+    rp_set_error("scale_quantize: null pointer");
+    return RP_ERR_INVALID_ARGUMENT;
+  }
+  Plan pl;
+  int rc = make_plan(x, B, H, S, D, sb, sh, ss, granularity, &pl);
+  if (rc) return rc;
+  if (layout == RP_LAYOUT_BHDS && (D % 64 != 0 || ld < S || ld % 128 != 0)) {
+    rp_set_error("scale_quantize(BHDS): needs D %% 64 == 0 and ld >= S with ld %% 128 == 0");
+    return RP_ERR_UNSUPPORTED;
+  }
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  rc = launch_scale(pl, dequant_out, workspace, workspace_bytes, st);
+  if (rc) return rc;
+  return launch_apply(pl, x, B, H, S, D, sb, sh, ss, dequant_out, codes, layout, ld, st);
+}
+
+extern "C" int rp_selftest_e4m3(const float* x, uint8_t* out, int64_t n, void* stream) {
+  if (x == nullptr || out == nullptr || n < 0) {
+    rp_set_error("selftest_e4m3: bad arguments");
+    return RP_ERR_INVALID_ARGUMENT;
+  }
+  if (n == 0) return RP_OK;
+  const int64_t blocks = (n + 255) / 256;
+  hipLaunchKernelGGL(selftest_e4m3_kernel, dim3((unsigned)blocks), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), x, out, n);
+  return check_launch("selftest_e4m3");
+}
+
+extern "C" int rp_selftest_scale(const uint16_t* amax_bits, float* dequant, float* qmul, int64_t n,
+                                 void* stream) {
+  if (amax_bits == nullptr || dequant == nullptr || qmul == nullptr || n < 0) {
+    rp_set_error("selftest_scale: bad arguments");
+    return RP_ERR_INVALID_ARGUMENT;
+  }
+  if (n == 0) return RP_OK;
+  const int64_t blocks = (n + 255) / 256;
+  hipLaunchKernelGGL(selftest_scale_kernel, dim3((unsigned)blocks), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), amax_bits, dequant, qmul, n);
+  return check_launch("selftest_scale");
+}

@@ -1,0 +1,186 @@
+"""GPU parity of the FP8 flash-attention forward against the tile-exact CPU oracle.
+
+Reference behaviour: kernels/triton_kernels/fp8_flash_attn.py:294-391 (kernel
+body) and :480-645 (wrapper), OCP P cast per fp8_flash_attn_hopper.py:322.
+The oracle runs with the kernel's key-tile width (BLOCK_N = 128) because the
+running max after each tile sets P's quantization grid.
+
+Tolerances: BASELINE.json's max-abs 2e-2 / mean-abs 2e-3 against the
+torch-emulated FP8 result (scaled by the output's peak magnitude when that
+exceeds 1, see tests/_helpers.baseline_tolerance), plus a relative mean error
+bound of 1e-2: the kernel and the oracle run the same algorithm, so they differ
+only by fp32 rounding (exp2 vs exp, summation order) and the rare P code
+that rounding flips.
+"""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import native
+from repercep_runtime_amd import ops
+from repercep_runtime_amd.workloads import C1, C3_CROSS, C3_SELF, C5, AttnConfig, attn_inputs
+from tests._helpers import baseline_tolerance, bf16_bits, codes_np, err_stats, vt_to_bhsd
+
+pytestmark = pytest.mark.gpu
+
+REL_TOL = 1e-2
+
+
+def _oracle_rows(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, heads: list[int],
+                 rows: np.ndarray, *, sm_scale: float, mask: int = 0, prefix: int = 0,
+                 suffix: int = 1, granularity: str = "bh") -> tuple[np.ndarray, dict]:
+    """Oracle output (len(heads), len(rows), D) for (B=1) CPU tensors."""
+    B, H, Sq, D = q.shape
+    n = B * H if granularity == "bh" else 1
+    qs, q8 = native.quantize_groups(bf16_bits(q), n)
+    ks, k8 = native.quantize_groups(bf16_bits(k), n)
+    vs, v8 = native.quantize_groups(bf16_bits(v), n)
+    outs = []
+    for h in heads:
+        si = h if granularity == "bh" else 0
+        outs.append(native.attn_rows(q8[0, h], k8[0, h], v8[0, h], qs[si], ks[si], vs[si],
+                                     sm_scale, rows, block_n=ops.BLOCK_N, mask=mask,
+                                     prefix=prefix, suffix=suffix))
+    return np.stack(outs), {"q8": q8, "k8": k8, "v8": v8, "qs": qs, "ks": ks, "vs": vs}
+
+
+def _check(got: np.ndarray, ref: np.ndarray, what: str, rel_tol: float = REL_TOL) -> dict:
+    st = err_stats(got, ref)
+    max_tol, mean_tol = baseline_tolerance(ref)
+    print(f"{what}: {st} (tol max {max_tol:.3g}, mean {mean_tol:.3g})", flush=True)
+    assert np.isfinite(got).all(), f"{what}: non-finite output"
+    assert st["max_abs"] <= max_tol, f"{what}: {st}"
+    assert st["mean_abs"] <= mean_tol, f"{what}: {st}"
+    assert st["rel_mean"] <= rel_tol, f"{what}: {st}"
+    return st
+
+
+@pytest.mark.parametrize("out_dtype", [torch.float32, torch.bfloat16])
+def test_c1_all_rows(gpu: torch.device, out_dtype: torch.dtype) -> None:
+    """BASELINE config 1, (1, 8, 1024, 64): every output element vs the oracle."""
+    q, k, v = attn_inputs(C1)
+    sm = 1.0 / math.sqrt(C1.D)
+    out = ops.fp8_flash_attention(q.to(gpu), k.to(gpu), v.to(gpu), out_dtype=out_dtype)
+    ref, _ = _oracle_rows(q, k, v, list(range(C1.H)), np.arange(C1.Sq), sm_scale=sm)
+    got = out.float().cpu().numpy()[0]
+    if out_dtype == torch.bfloat16:
+        ref = torch.from_numpy(ref).to(torch.bfloat16).float().numpy()
+    _check(got, ref, f"c1 {out_dtype}")
+
+
+CASES = [
+    # name, B, H, Sq, Skv, D, causal
+    ("self_ragged_d128", 1, 2, 1000, 1000, 128, False),
+    ("self_ragged_d64", 2, 1, 777, 777, 64, False),
+    ("cross_d128", 1, 2, 300, 512, 128, False),
+    ("cross_short_kv", 1, 1, 1000, 131, 128, False),
+    ("single_key", 1, 1, 64, 1, 128, False),
+    ("single_query", 1, 3, 1, 300, 64, False),
+    ("causal_d128", 1, 2, 700, 700, 128, True),
+    ("causal_d64", 1, 2, 513, 513, 64, True),
+    ("tiny", 1, 1, 5, 7, 64, False),
+]
+
+
+@pytest.mark.parametrize("case", CASES, ids=[c[0] for c in CASES])
+def test_shapes_vs_oracle(gpu: torch.device, case: tuple) -> None:
+    name, B, H, Sq, Skv, D, causal = case
+    g = torch.Generator().manual_seed(sum(map(ord, name)))
+    q = torch.randn(B, H, Sq, D, generator=g).to(torch.bfloat16)
+    k = torch.randn(B, H, Skv, D, generator=g).to(torch.bfloat16)
+    v = torch.randn(B, H, Skv, D, generator=g).to(torch.bfloat16)
+    sm = 1.0 / math.sqrt(D)
+    out = ops.fp8_flash_attention(q.to(gpu), k.to(gpu), v.to(gpu), causal=causal,
+                                  out_dtype=torch.float32).cpu().numpy()
+    rows = np.arange(Sq)
+    for b in range(B):
+        ref, _ = _oracle_rows(q[b:b + 1], k[b:b + 1], v[b:b + 1], list(range(H)), rows,
+                              sm_scale=sm, mask=1 if causal else 0)
+        _check(out[b], ref, f"{name} b={b}")
+
+
+def test_per_tensor_granularity(gpu: torch.device) -> None:
+    g = torch.Generator().manual_seed(5)
+    q, k, v = (torch.randn(1, 4, 600, 128, generator=g).mul(1 + i).to(torch.bfloat16)
+               for i in range(3))
+    out = ops.fp8_flash_attention(q.to(gpu), k.to(gpu), v.to(gpu), granularity="tensor",
+                                  out_dtype=torch.float32).cpu().numpy()[0]
+    ref, _ = _oracle_rows(q, k, v, [0, 1, 2, 3], np.arange(600), sm_scale=128 ** -0.5,
+                          granularity="tensor")
+    _check(out, ref, "per-tensor")
+
+
+def test_custom_softmax_scale(gpu: torch.device) -> None:
+    g = torch.Generator().manual_seed(9)
+    q, k, v = (torch.randn(1, 2, 256, 64, generator=g).to(torch.bfloat16) for _ in range(3))
+    out = ops.fp8_flash_attention(q.to(gpu), k.to(gpu), v.to(gpu), scale=0.3,
+                                  out_dtype=torch.float32).cpu().numpy()[0]
+    ref, _ = _oracle_rows(q, k, v, [0, 1], np.arange(256), sm_scale=0.3)
+    _check(out, ref, "scale=0.3")
+
+
+def test_shared_prefix_candidates_c5(gpu: torch.device) -> None:
+    """512-token shared prefix + 16 candidates x 8 suffix tokens."""
+    q, k, v = attn_inputs(C5)
+    out = ops.fp8_flash_attention(q.to(gpu), k.to(gpu), v.to(gpu), prefix_len=C5.prefix,
+                                  suffix_len=C5.suffix, out_dtype=torch.float32)
+    ref, _ = _oracle_rows(q, k, v, list(range(C5.H)), np.arange(C5.Sq),
+                          sm_scale=C5.D ** -0.5, mask=2, prefix=C5.prefix, suffix=C5.suffix)
+    _check(out.cpu().numpy()[0], ref, "c5 shared prefix")
+
+
+def test_output_into_strided_bshd_buffer(gpu: torch.device) -> None:
+    """Kernel writes through output strides: a permuted (B, S, H, D) buffer."""
+    g = torch.Generator().manual_seed(21)
+    q, k, v = (torch.randn(2, 300, 3, 128, generator=g).to(torch.bfloat16) for _ in range(3))
+    qg, kg, vg = q.to(gpu), k.to(gpu), v.to(gpu)
+    out = torch.full((2, 300, 3, 128), float("nan"), dtype=torch.bfloat16, device=gpu)
+    ops.fp8_flash_attention(qg.permute(0, 2, 1, 3), kg.permute(0, 2, 1, 3),
+                            vg.permute(0, 2, 1, 3), out=out.permute(0, 2, 1, 3))
+    ref_bhsd = ops.fp8_flash_attention(qg.permute(0, 2, 1, 3).contiguous(),
+                                       kg.permute(0, 2, 1, 3).contiguous(),
+                                       vg.permute(0, 2, 1, 3).contiguous())
+    assert torch.equal(out.permute(0, 2, 1, 3), ref_bhsd)
+
+
+def test_codes_seen_by_kernel_match_oracle_codes(gpu: torch.device) -> None:
+    """The attention wrapper's quantized operands are the oracle's codes, bit for bit."""
+    q, k, v = attn_inputs(C1)
+    _, q8_ref = native.quantize_groups(bf16_bits(q), C1.B * C1.H)
+    _, v8_ref = native.quantize_groups(bf16_bits(v), C1.B * C1.H)
+    qs, q8 = ops.scale_quantize(q.to(gpu), "bh", "bhsd")
+    vs, vt8 = ops.scale_quantize(v.to(gpu), "bh", "bhds")
+    assert np.array_equal(codes_np(q8), q8_ref)
+    assert np.array_equal(vt_to_bhsd(codes_np(vt8), C1.Skv), v8_ref)
+
+
+def _wan_sample(gpu: torch.device, cfg: AttnConfig, heads: list[int], nrows: int) -> None:
+    q, k, v = attn_inputs(cfg, device=gpu)
+    out = ops.fp8_flash_attention(q, k, v, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    rng = np.random.default_rng(0)
+    rows = np.sort(rng.choice(cfg.Sq, size=nrows, replace=False))
+    qc, kc, vc = q[:, heads].cpu(), k[:, heads].cpu(), v[:, heads].cpu()
+    # per-(b,h) scales depend only on the head's own data, so slicing heads is exact
+    ref, _ = _oracle_rows(qc, kc, vc, list(range(len(heads))), rows,
+                          sm_scale=cfg.D ** -0.5)
+    got = out[0, heads][:, torch.from_numpy(rows).to(gpu)].cpu().numpy()
+    _check(got, ref, f"{cfg.name} heads {heads} rows {nrows}")
+    assert torch.isfinite(out).all()
+    del q, k, v, out
+    torch.cuda.empty_cache()
+
+
+def test_wan_self_attention_full_shape_sampled_rows(gpu: torch.device) -> None:
+    """C3 self (1, 40, 75600, 128): full kernel run, 128 rows x 3 heads vs oracle."""
+    _wan_sample(gpu, C3_SELF, [0, 17, 39], 128)
+
+
+def test_wan_cross_attention_full_shape_sampled_rows(gpu: torch.device) -> None:
+    """C3 cross (Skv = 512): 512 rows x 4 heads vs oracle."""
+    _wan_sample(gpu, C3_CROSS, [0, 5, 20, 39], 512)

@@ -1,0 +1,200 @@
+"""GPU parity of the FP8 quantizer against the CPU oracle: bit-exact codes and scales.
+
+Reference behaviour: _per_bh_scale / _quantize,
+kernels/triton_kernels/fp8_flash_attn_hopper.py:374-398.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import native
+from repercep_runtime_amd import ops
+from repercep_runtime_amd.workloads import C1, C3_SELF, attn_inputs
+from tests._helpers import bf16_bits, codes_np, vt_to_bhsd
+
+pytestmark = pytest.mark.gpu
+
+
+def _nan_code(c: np.ndarray) -> np.ndarray:
+    return (c & 0x7F) == 0x7F
+
+
+def _assert_codes_equal(got: np.ndarray, ref: np.ndarray) -> None:
+    """Bit-exact, except that the sign of a NaN code is not specified."""
+    both_nan = _nan_code(got) & _nan_code(ref)
+    bad = (got != ref) & ~both_nan
+    n_bad = int(bad.sum())
+    if n_bad:
+        idx = np.flatnonzero(bad.ravel())[:8]
+        pytest.fail(f"{n_bad} code mismatches; first at {idx}: got {got.ravel()[idx]}, "
+                    f"want {ref.ravel()[idx]}")
+
+
+def _assert_scales_equal(got: np.ndarray, ref: np.ndarray) -> None:
+    g = got.astype(np.float32)
+    r = ref.astype(np.float32)
+    same = (g.view(np.uint32) == r.view(np.uint32)) | (np.isnan(g) & np.isnan(r))
+    assert same.all(), f"scales differ: got {g[~same][:8]}, want {r[~same][:8]}"
+
+
+def _oracle(x_cpu: torch.Tensor, granularity: str) -> tuple[np.ndarray, np.ndarray]:
+    bits = bf16_bits(x_cpu.contiguous())
+    n = x_cpu.shape[0] * x_cpu.shape[1] if granularity == "bh" else 1
+    return native.quantize_groups(bits, n)
+
+
+def test_hw_e4m3_cvt_matches_torch_cast_on_every_fp32_pattern(gpu: torch.device) -> None:
+    """v_cvt_pk_fp8_f32 (after the reference's +-448 clamp) vs torch's cast, all 2^32 inputs."""
+    chunk = 1 << 28
+    total_bad = 0
+    for start in range(0, 1 << 32, chunk):
+        u = torch.arange(start, start + chunk, dtype=torch.int64, device=gpu).to(torch.int32)
+        x = u.view(torch.float32)
+        hw = ops.selftest_e4m3(x)
+        ref = x.clamp(-448.0, 448.0).to(torch.float8_e4m3fn).view(torch.uint8)
+        nan_both = ((hw & 0x7F) == 0x7F) & ((ref & 0x7F) == 0x7F)
+        bad = (hw != ref) & ~nan_both
+        nb = int(bad.sum().item())
+        if nb:
+            i = int(torch.nonzero(bad)[0].item())
+            print(f"chunk {start:#x}: {nb} mismatches, first x bits {start + i:#010x} "
+                  f"hw {int(hw[i])} ref {int(ref[i])}", flush=True)
+        total_bad += nb
+        del u, x, hw, ref, bad, nan_both
+    assert total_bad == 0
+
+
+def test_scale_formula_on_every_bf16_amax(gpu: torch.device) -> None:
+    bits = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    dq, qm = ops.selftest_scale(torch.from_numpy(bits.view(np.int16)).to(gpu))
+    ref = np.array([native.dequant_from_amax(int(b)) for b in bits], dtype=np.float32)
+    _assert_scales_equal(dq.cpu().numpy(), ref)
+    with np.errstate(divide="ignore", invalid="ignore"):
+        ref_qm = np.float32(1.0) / ref
+    _assert_scales_equal(qm.cpu().numpy(), ref_qm)
+
+
+SHAPES = [
+    (1, 8, 1024, 64),
+    (2, 3, 257, 128),
+    (1, 1, 5, 64),
+    (1, 2, 1, 128),
+    (3, 1, 130, 64),
+]
+
+
+@pytest.mark.parametrize("shape", SHAPES)
+@pytest.mark.parametrize("granularity", ["bh", "tensor"])
+def test_quantize_bhsd_bit_exact(gpu: torch.device, shape: tuple[int, ...],
+                                 granularity: str) -> None:
+    g = torch.Generator().manual_seed(sum(shape))
+    x = torch.randn(shape, generator=g).mul(3.0).to(torch.bfloat16)
+    ref_s, ref_c = _oracle(x, granularity)
+    dq, codes = ops.scale_quantize(x.to(gpu), granularity, "bhsd")
+    _assert_scales_equal(dq.cpu().numpy(), ref_s)
+    _assert_codes_equal(codes_np(codes), ref_c)
+    # separate scale / apply entry points agree with the fused one
+    dq2 = ops.per_bh_scale(x.to(gpu), granularity)
+    _assert_scales_equal(dq2.cpu().numpy(), ref_s)
+    c2 = ops.quantize(x.to(gpu), dq2, granularity, "bhsd")
+    _assert_codes_equal(codes_np(c2), ref_c)
+
+
+@pytest.mark.parametrize("shape", [(1, 8, 1024, 64), (2, 3, 257, 128), (1, 2, 1, 128),
+                                   (1, 1, 300, 256)])
+def test_quantize_bhds_transposed_bit_exact(gpu: torch.device, shape: tuple[int, ...]) -> None:
+    g = torch.Generator().manual_seed(7 + sum(shape))
+    x = torch.randn(shape, generator=g).to(torch.bfloat16)
+    ref_s, ref_c = _oracle(x, "bh")
+    dq, vt = ops.scale_quantize(x.to(gpu), "bh", "bhds")
+    B, H, S, D = shape
+    vt_np = codes_np(vt)
+    assert vt_np.shape == (B, H, D, (S + 127) // 128 * 128)
+    _assert_scales_equal(dq.cpu().numpy(), ref_s)
+    _assert_codes_equal(vt_to_bhsd(vt_np, S), ref_c)
+    assert not vt_np[..., S:].any(), "padding columns must be zero"
+
+
+def test_quantize_strided_bshd_view(gpu: torch.device) -> None:
+    """A permuted (B, S, H, D) buffer is read in place (diffusers layout)."""
+    g = torch.Generator().manual_seed(3)
+    bshd = torch.randn(2, 300, 4, 128, generator=g).to(torch.bfloat16)
+    x_view = bshd.to(gpu).permute(0, 2, 1, 3)          # (B, H, S, D) strided view
+    ref_s, ref_c = _oracle(bshd.permute(0, 2, 1, 3).contiguous(), "bh")
+    for gran in ("bh", "tensor"):
+        ref_s, ref_c = _oracle(bshd.permute(0, 2, 1, 3).contiguous(), gran)
+        dq, codes = ops.scale_quantize(x_view, gran, "bhsd")
+        _assert_scales_equal(dq.cpu().numpy(), ref_s)
+        _assert_codes_equal(codes_np(codes), ref_c)
+        dqt, vt = ops.scale_quantize(x_view, gran, "bhds")
+        _assert_codes_equal(vt_to_bhsd(codes_np(vt), 300), ref_c)
+
+
+def _special_inputs() -> list[tuple[str, torch.Tensor]]:
+    g = torch.Generator().manual_seed(11)
+    base = torch.randn(2, 2, 64, 64, generator=g)
+    cases = []
+    z = base.clone()
+    z[0, 1] = 0.0                                   # all-zero group -> amax clamps to 1e-6
+    cases.append(("zero_group", z))
+    n = base.clone()
+    n[1, 0, 3, 5] = float("nan")                     # NaN propagates through amax
+    cases.append(("nan", n))
+    i = base.clone()
+    i[0, 0, 7, 7] = float("inf")                     # inf amax -> q_mul 0 -> zeros and NaN
+    i[1, 1, 2, 2] = float("-inf")
+    cases.append(("inf", i))
+    m0 = base.clone()
+    m0[0, 0] = -0.0                                  # -0.0 group -> code 0x80
+    m0[0, 0, 0, 0] = 0.0
+    cases.append(("neg_zero", m0))
+    tiny = base.clone() * 1e-7                       # amax below 1e-6
+    cases.append(("tiny", tiny))
+    big = base.clone() * 1e37                        # near the bf16 top
+    cases.append(("huge", big))
+    sub = base.clone()
+    sub[1, 1] = sub[1, 1] * 1e-38                    # bf16 subnormal inputs
+    cases.append(("subnormal", sub))
+    return [(name, t.to(torch.bfloat16)) for name, t in cases]
+
+
+@pytest.mark.parametrize("name,x", _special_inputs(), ids=[c[0] for c in _special_inputs()])
+@pytest.mark.parametrize("granularity", ["bh", "tensor"])
+def test_quantize_special_values(gpu: torch.device, name: str, x: torch.Tensor,
+                                 granularity: str) -> None:
+    ref_s, ref_c = _oracle(x, granularity)
+    dq, codes = ops.scale_quantize(x.to(gpu), granularity, "bhsd")
+    _assert_scales_equal(dq.cpu().numpy(), ref_s)
+    _assert_codes_equal(codes_np(codes), ref_c)
+
+
+def test_quantize_c1_matches_torch_restatement(gpu: torch.device) -> None:
+    """C1 inputs: GPU codes equal the reference's own torch ops run on the CPU."""
+    from oracle import quant
+
+    q, k, v = attn_inputs(C1)
+    for x in (q, k, v):
+        dq_ref, codes_ref = quant.quantize_codes(x, "bh")
+        dq, codes = ops.scale_quantize(x.to(gpu), "bh", "bhsd")
+        _assert_scales_equal(dq.cpu().numpy(), dq_ref)
+        _assert_codes_equal(codes_np(codes), codes_ref)
+
+
+def test_quantize_wan_full_size_every_element(gpu: torch.device) -> None:
+    """C3 (1, 40, 75600, 128): every code and scale of Q, K and (transposed) V."""
+    q, k, v = attn_inputs(C3_SELF, device=gpu)
+    for name, x, layout in (("q", q, "bhsd"), ("k", k, "bhsd"), ("v", v, "bhds")):
+        dq, codes = ops.scale_quantize(x, "bh", layout)
+        ref_s, ref_c = _oracle(x.cpu(), "bh")
+        _assert_scales_equal(dq.cpu().numpy(), ref_s)
+        got = codes_np(codes)
+        if layout == "bhds":
+            got = vt_to_bhsd(got, x.shape[2])
+        _assert_codes_equal(got, ref_c)
+        print(f"{name}: {ref_c.size} codes equal", flush=True)
+        del dq, codes, got, ref_c
+    del q, k, v
+    torch.cuda.empty_cache()
