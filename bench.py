@@ -243,6 +243,10 @@ def main() -> int:
     ap.add_argument("--config", default="c3_wan_self",
                     help="c1_cpu_runnable | c2_cosmos_self | c3_wan_self | c3_wan_cross | "
                          "c5_shared_prefix | c4_wan_ffn_up")
+    ap.add_argument("--copy-calibration-mib", type=int, default=0,
+                    help="run one device-to-device copy of this many MiB first, so a "
+                         "rocprofv3 --pmc FETCH_SIZE/WRITE_SIZE run can scale the counters "
+                         "against a plain copy of known size")
     ap.add_argument("--cpu-budget", type=float, default=12.0,
                     help="seconds of CPU work for the cpu_baseline sample (0 disables)")
     args = ap.parse_args()
@@ -262,6 +266,14 @@ def main() -> int:
 
     from repercep_runtime_amd.workloads import ATTN_CONFIGS, C4
 
+    if args.copy_calibration_mib > 0:
+        n = args.copy_calibration_mib << 20
+        src = torch.ones(n, dtype=torch.uint8, device="cuda")
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"[bench] calibration copy of {args.copy_calibration_mib} MiB done")
+        del src, dst
     if args.config == C4.name:
         res = bench_gemm(args, C4)
     else:

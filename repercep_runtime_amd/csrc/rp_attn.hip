@@ -43,12 +43,13 @@
 
 #include "rp_common.h"
 
+#include <stdlib.h>
+#include <string.h>
+
 namespace rp {
 namespace {
 
 constexpr int kBlockN = 128;  // keys per tile = K depth of the P.V MFMA
-constexpr int kWaves = 4;
-constexpr int kThreads = kWaves * kWave;
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLog2PMax = 8.807354922057604f;  // log2(448)
 
@@ -84,77 +85,112 @@ __device__ __forceinline__ float max3f(float a, float b, float c) {
   return __builtin_fmaxf(a, __builtin_fmaxf(b, c));
 }
 
-template <int D>
+template <int D, int NW>
 struct Geo {
+  static constexpr int THREADS = NW * kWave;
   static constexpr int KCH = D / 16;                 // 16-byte chunks per K row
   static constexpr int ETILES = D / 16;              // 16-row tiles of O^T
   static constexpr int K_BYTES = kBlockN * D;
   static constexpr int V_BYTES = D * kBlockN;
   static constexpr int STAGE = K_BYTES + V_BYTES;
-  static constexpr int K_LOADS = K_BYTES / 16 / kThreads;
-  static constexpr int V_LOADS = V_BYTES / 16 / kThreads;
+  static constexpr int K_LOADS = K_BYTES / 16 / THREADS;
+  static constexpr int V_LOADS = V_BYTES / 16 / THREADS;
   static_assert(D == 64 || D == 128, "head dim");
-  static_assert(K_LOADS * 16 * kThreads == K_BYTES, "K tile split");
+  static_assert(K_LOADS * 16 * THREADS == K_BYTES, "K tile split");
+  static_assert(V_LOADS * 16 * THREADS == V_BYTES, "V tile split");
 };
 
 // Chunk swizzles (16-byte granules) for the two LDS tiles.
 template <int D>
 __device__ __forceinline__ int k_swz(int r) {
-  return ((r & 3) | ((r >> 3) & 4)) & (Geo<D>::KCH - 1);
+  return ((r & 3) | ((r >> 3) & 4)) & (D / 16 - 1);
 }
 __device__ __forceinline__ int v_swz(int d) { return d & 7; }
 
-// One (K, V^T) tile: global -> registers.  Rows past Skv re-read the last
-// key (their scores are masked); V^T rows are zero-padded to ldv.
-template <int D>
-__device__ __forceinline__ void load_tile(const AttnArgs& a, const uint8_t* kh, const uint8_t* vh,
-                                          int kb, int tid, i32x4 (&sk)[Geo<D>::K_LOADS],
-                                          i32x4 (&sv)[Geo<D>::V_LOADS]) {
-  using G = Geo<D>;
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+typedef __attribute__((address_space(1))) void* gbl_ptr_t;
+
+// 16 bytes global -> LDS without passing through VGPRs.  `lds_block` must be
+// wave-uniform: lane i lands at lds_block + 16*i.
+__device__ __forceinline__ void gload_lds16(const void* src, void* lds_block) {
+  __builtin_amdgcn_global_load_lds((gbl_ptr_t)src, (lds_ptr_t)lds_block, 16, 0, 0);
+}
+
+// Per-thread byte offsets of the direct-to-LDS loads of one (K, V^T) tile,
+// relative to the tile's first key.  Each wave instruction fills one
+// contiguous KiB of LDS, so the XOR swizzle is applied on the global side:
+// the lane that lands on physical chunk `phys` of row r fetches logical chunk
+// phys ^ swz(r).
+template <int D, int NW>
+struct TileOffsets {
+  uint32_t k[Geo<D, NW>::K_LOADS];  // relative to kh + kv0*D
+  uint32_t v[Geo<D, NW>::V_LOADS];  // relative to vh + kv0
+  int k_row[Geo<D, NW>::K_LOADS];   // key row of each K load inside the tile
+};
+
+template <int D, int NW>
+__device__ __forceinline__ TileOffsets<D, NW> tile_offsets(int64_t ldv, int wave, int lane) {
+  using G = Geo<D, NW>;
+  TileOffsets<D, NW> o;
+#pragma unroll
+  for (int n = 0; n < G::K_LOADS; ++n) {
+    const int p = (n * NW + wave) * kWave + lane;
+    const int r = p / G::KCH, phys = p % G::KCH;
+    o.k_row[n] = r;
+    o.k[n] = (uint32_t)(r * D + ((phys ^ k_swz<D>(r)) << 4));
+  }
+#pragma unroll
+  for (int n = 0; n < G::V_LOADS; ++n) {
+    const int p = (n * NW + wave) * kWave + lane;
+    const int d = p >> 3, phys = p & 7;
+    o.v[n] = (uint32_t)(d * ldv + ((phys ^ v_swz(d)) << 4));
+  }
+  return o;
+}
+
+// Issue tile `kb` into one LDS stage.  K rows past Skv (last tile only)
+// re-read the last key -- their scores are masked; V^T is zero-padded to ldv.
+template <int D, int NW>
+__device__ __forceinline__ void issue_tile(const AttnArgs& a, const uint8_t* kh, const uint8_t* vh,
+                                           const TileOffsets<D, NW>& o, int kb, uint8_t* stage,
+                                           int wave) {
+  using G = Geo<D, NW>;
   const int kv0 = kb * kBlockN;
+  const uint8_t* kt = kh + (int64_t)kv0 * D;
+  const bool tail = kv0 + kBlockN > a.Skv;
 #pragma unroll
   for (int n = 0; n < G::K_LOADS; ++n) {
-    const int ci = tid + kThreads * n;
-    const int r = ci / G::KCH, c = ci % G::KCH;
-    const int kv = min(kv0 + r, a.Skv - 1);
-    sk[n] = *reinterpret_cast<const i32x4*>(kh + (int64_t)kv * D + c * 16);
+    uint32_t off = o.k[n];
+    if (tail && kv0 + o.k_row[n] >= a.Skv)
+      off = off - (uint32_t)((kv0 + o.k_row[n] - (a.Skv - 1)) * D);
+    gload_lds16(kt + off, stage + (n * NW + wave) * 1024);
   }
+  const uint8_t* vt = vh + kv0;
+  uint8_t* vst = stage + G::K_BYTES;
 #pragma unroll
-  for (int n = 0; n < G::V_LOADS; ++n) {
-    const int ci = tid + kThreads * n;
-    const int d = ci >> 3, c = ci & 7;
-    sv[n] = *reinterpret_cast<const i32x4*>(vh + (int64_t)d * a.ldv + kv0 + c * 16);
-  }
+  for (int n = 0; n < G::V_LOADS; ++n) gload_lds16(vt + o.v[n], vst + (n * NW + wave) * 1024);
 }
 
-// registers -> swizzled LDS stage
-template <int D>
-__device__ __forceinline__ void store_tile(uint8_t* kl, int tid,
-                                           const i32x4 (&sk)[Geo<D>::K_LOADS],
-                                           const i32x4 (&sv)[Geo<D>::V_LOADS]) {
-  using G = Geo<D>;
-  uint8_t* vl = kl + G::K_BYTES;
-#pragma unroll
-  for (int n = 0; n < G::K_LOADS; ++n) {
-    const int ci = tid + kThreads * n;
-    const int r = ci / G::KCH, c = ci % G::KCH;
-    *reinterpret_cast<i32x4*>(kl + r * D + ((c ^ k_swz<D>(r)) << 4)) = sk[n];
-  }
-#pragma unroll
-  for (int n = 0; n < G::V_LOADS; ++n) {
-    const int ci = tid + kThreads * n;
-    const int d = ci >> 3, c = ci & 7;
-    *reinterpret_cast<i32x4*>(vl + d * kBlockN + ((c ^ v_swz(d)) << 4)) = sv[n];
-  }
+__device__ __forceinline__ void wait_vmem_all() {
+  // s_waitcnt vmcnt(0): direct-to-LDS loads have landed
+  __builtin_amdgcn_s_waitcnt(0x0F70);
 }
 
-template <int D, int QT, bool OUT_F32>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1)))
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  const __bf16 a = (__bf16)lo, b = (__bf16)hi;  // v_cvt_pk_bf16_f32, round to nearest even
+  return (uint32_t)__builtin_bit_cast(uint16_t, a) | ((uint32_t)__builtin_bit_cast(uint16_t, b) << 16);
+}
+
+// NW waves per workgroup, each owning QT 16-row query tiles; launch bounds
+// ask for two waves per SIMD (256 VGPRs each) so one wave's MFMAs overlap
+// the other's softmax.
+template <int D, int QT, int NW, bool OUT_F32>
+__global__ __launch_bounds__(NW * kWave, 8 / NW)
 void attn_fwd_kernel(AttnArgs a) {
-  using G = Geo<D>;
+  using G = Geo<D, NW>;
   constexpr int QROWS = 16 * QT;
-  constexpr int BLOCK_M = QROWS * kWaves;
-  __shared__ __attribute__((aligned(16))) uint8_t smem[2 * G::STAGE];
+  constexpr int BLOCK_M = QROWS * NW;
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * G::STAGE];
 
   // ---- work item (XCD-aware remap of the linear workgroup id)
   const int w = blockIdx.x;
@@ -184,6 +220,16 @@ void attn_fwd_kernel(AttnArgs a) {
   // exp2 domain: s2 = dot * c2 with c2 = sm_scale*q_scale*k_scale*log2(e)
   const float c2 = ((a.sm_scale * q_scale) * k_scale) * kLog2e;
 
+  // ---- key range: causal blocks past the block's last query are skipped
+  int n_kb = (a.Skv + kBlockN - 1) / kBlockN;
+  if (a.mask == RP_MASK_CAUSAL) {
+    const int q_last = min(q_block0 + BLOCK_M, a.Sq) - 1;
+    n_kb = min(n_kb, q_last / kBlockN + 1);
+  }
+
+  const TileOffsets<D, NW> toff = tile_offsets<D, NW>(a.ldv, wave, lane);
+  issue_tile<D, NW>(a, kh, vh, toff, 0, smem, wave);
+
   // ---- Q^T operand (B operand of S^T), resident for the whole kernel
   i32x8 qop[QT];
 #pragma unroll
@@ -196,16 +242,6 @@ void attn_fwd_kernel(AttnArgs a) {
       qop[u] = i32x8{0, 0, 0, 0, 0, 0, 0, 0};
     }
   }
-
-  // ---- key range: causal blocks past the block's last query are skipped
-  int n_kb = (a.Skv + kBlockN - 1) / kBlockN;
-  if (a.mask == RP_MASK_CAUSAL) {
-    const int q_last = min(q_block0 + BLOCK_M, a.Sq) - 1;
-    n_kb = min(n_kb, q_last / kBlockN + 1);
-  }
-
-  i32x4 stage_k[G::K_LOADS];
-  i32x4 stage_v[G::V_LOADS];
 
   // ---- online softmax state (per lane: query q_wave0 + 16u + li)
   f32x4 acc[QT][G::ETILES];
@@ -221,54 +257,59 @@ void attn_fwd_kernel(AttnArgs a) {
   // K operand row of tile t for this lane: 32*(li>>2) + 4t + (li&3).  Its
   // swizzle reads bits 0-1 and 5 of the row, which 4t (t < 8) never changes.
   const int k_row0 = 32 * (li >> 2) + (li & 3);
+  const int k_sw = k_swz<D>(k_row0);
   const bool k_has = 32 * lg < D;
+  const int k_off0 = k_row0 * D + (((2 * lg) ^ k_sw) << 4);
+  const int k_off1 = k_row0 * D + (((2 * lg + 1) ^ k_sw) << 4);
 
-  load_tile<D>(a, kh, vh, 0, tid, stage_k, stage_v);
-  store_tile<D>(smem, tid, stage_k, stage_v);
+  wait_vmem_all();
   __syncthreads();
 
   for (int kb = 0; kb < n_kb; ++kb) {
     const int st = kb & 1;
-    const bool more = kb + 1 < n_kb;
-    if (more) load_tile<D>(a, kh, vh, kb + 1, tid, stage_k, stage_v);
+    if (kb + 1 < n_kb) issue_tile<D, NW>(a, kh, vh, toff, kb + 1, smem + (st ^ 1) * G::STAGE, wave);
 
     const uint8_t* kl = smem + st * G::STAGE;
     const uint8_t* vl = kl + G::K_BYTES;
     const int kv0 = kb * kBlockN;
 
-    // ---- S^T = K . Q^T   (s[u][t][r]: key kv0 + 32*lg + 4t + r, query u)
-    f32x4 s[QT][8];
-#pragma unroll
-    for (int t = 0; t < 8; ++t) {
-      i32x8 kop;
-      if (k_has) {
-        const int r = k_row0 + 4 * t;
-        const int sw = k_swz<D>(r);
-        const uint8_t* row = kl + r * D;
-        kop = cat8(*reinterpret_cast<const i32x4*>(row + (((2 * lg) ^ sw) << 4)),
-                   *reinterpret_cast<const i32x4*>(row + (((2 * lg + 1) ^ sw) << 4)));
-      } else {
-        kop = i32x8{0, 0, 0, 0, 0, 0, 0, 0};
-      }
-#pragma unroll
-      for (int u = 0; u < QT; ++u) s[u][t] = mfma_16x16x128(kop, qop[u], f32x4{0.f, 0.f, 0.f, 0.f});
-    }
-
-    // ---- masking (only tiles that can contain an invisible key)
     const bool tail = kv0 + kBlockN > a.Skv;
     bool need_mask = tail;
     if (a.mask == RP_MASK_CAUSAL) need_mask |= kv0 + kBlockN - 1 > q_wave0;
     if (a.mask == RP_MASK_SHARED_PREFIX) need_mask |= kv0 + kBlockN > a.prefix;
-    if (need_mask) {
-      // Every supported mask is "kv < pre_end, or lo <= kv <= hi" with a
-      // per-query window [lo, hi]: none/tail: [0, Skv-1]; causal:
-      // [0, min(q, Skv-1)]; shared prefix: keys before the prefix end plus
-      // the query's own candidate suffix up to itself.  Branch-free selects.
-      const float ninf = -__builtin_inff();
-      const int kvl = kv0 + 32 * lg;  // key of (t, r) is kvl + 4t + r
-      const int pre_end = a.mask == RP_MASK_SHARED_PREFIX ? min(a.prefix, a.Skv) : 0;
+    const int kvl = kv0 + 32 * lg;  // key of (t, r) is kvl + 4t + r
+    const int pre_end = a.mask == RP_MASK_SHARED_PREFIX ? min(a.prefix, a.Skv) : 0;
+
+    i32x8 pop[QT];
 #pragma unroll
-      for (int u = 0; u < QT; ++u) {
+    for (int u = 0; u < QT; ++u) {
+      // ---- S^T tile column block u: s[t][r] = score(query u, key kvl + 4t + r)
+      f32x4 s[8];
+      // Re-read K per query tile u rather than keeping 8 K operands (64 VGPRs)
+      // live across u: the empty asm hides that the address is unchanged.
+      // (a 32-bit LDS offset, so the loads stay ds_read_b128)
+      int kbu = st * G::STAGE;
+      asm volatile("" : "+v"(kbu));
+#pragma unroll
+      for (int t = 0; t < 8; ++t) {
+        i32x8 kop = i32x8{0, 0, 0, 0, 0, 0, 0, 0};
+        if (k_has)
+          kop = cat8(*reinterpret_cast<const i32x4*>(smem + kbu + k_off0 + 4 * t * D),
+                     *reinterpret_cast<const i32x4*>(smem + kbu + k_off1 + 4 * t * D));
+        s[t] = mfma_16x16x128(kop, qop[u], f32x4{0.f, 0.f, 0.f, 0.f});
+      }
+      // Pipeline the scheduler to "2 LDS reads, 1 MFMA" so only a couple of
+      // K operands are in flight (each holds 8 VGPRs).
+#pragma unroll
+      for (int t = 0; t < 8; ++t) {
+        __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // DS read
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+      }
+
+      // ---- masking: every supported mask is "kv < pre_end, or lo <= kv <= hi"
+      // with a per-query window; bitwise predicates, one select per score.
+      if (need_mask) {
+        const float ninf = -__builtin_inff();
         const int q = q_wave0 + 16 * u + li;
         int lo = 0, hi = a.Skv - 1;
         if (a.mask == RP_MASK_CAUSAL) hi = min(q, hi);
@@ -276,62 +317,59 @@ void attn_fwd_kernel(AttnArgs a) {
           lo = a.prefix + q - q % a.suffix;
           hi = min(a.prefix + q, hi);
         }
-        // shift to tile-relative offsets so the inner test is on 4t + r only
         const int lo_t = lo - kvl, hi_t = hi - kvl, pe_t = pre_end - kvl;
 #pragma unroll
         for (int t = 0; t < 8; ++t)
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
-            // bitwise (not short-circuit) logic: compares + one select, no branches
             const int o = 4 * t + r;
             const int vis = ((o >= lo_t) & (o <= hi_t)) | (o < pe_t);
-            s[u][t][r] = vis ? s[u][t][r] : ninf;
+            s[t][r] = vis ? s[t][r] : ninf;
           }
       }
-    }
 
-    // ---- online softmax, P -> e4m3 B operand
-    i32x8 pop[QT];
-    bool rescale = false;
-    float alpha[QT];
+      // ---- online softmax for this lane's query
+      float mx = max3f(s[0][0], s[0][1], s[0][2]);
+      mx = max3f(mx, s[0][3], s[1][0]);
+      mx = max3f(mx, s[1][1], s[1][2]);
+      mx = max3f(mx, s[1][3], s[2][0]);
 #pragma unroll
-    for (int u = 0; u < QT; ++u) {
-      float mx = s[u][0][0];
-#pragma unroll
-      for (int t = 0; t < 8; ++t) {
-        mx = max3f(mx, s[u][t][0], s[u][t][1]);
-        mx = max3f(mx, s[u][t][2], s[u][t][3]);
+      for (int t = 2; t < 8; ++t) {
+        if (t > 2) mx = max3f(mx, s[t][0], s[t][1]);
+        else mx = __builtin_fmaxf(mx, s[t][1]);
+        mx = max3f(mx, s[t][2], s[t][3]);
       }
       mx = __builtin_fmaxf(mx, shfl_xor(mx, 16));
       mx = __builtin_fmaxf(mx, shfl_xor(mx, 32));
       const float m_new = __builtin_fmaxf(m_run[u], mx * c2);
       const float m_use = (m_new == -__builtin_inff()) ? 0.0f : m_new;
-      alpha[u] = __builtin_amdgcn_exp2f(m_run[u] - m_use);
-      rescale |= (alpha[u] != 1.0f);
+      const float alpha = __builtin_amdgcn_exp2f(m_run[u] - m_use);
       m_run[u] = m_new;
       const float moff = m_use - kLog2PMax;
-      float psum = 0.0f;
+      float ps0 = 0.0f, ps1 = 0.0f;
       int pw[8];
 #pragma unroll
       for (int t = 0; t < 8; ++t) {
-        const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[u][t][0], c2, -moff));
-        const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[u][t][1], c2, -moff));
-        const float p2 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[u][t][2], c2, -moff));
-        const float p3 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[u][t][3], c2, -moff));
-        psum += (p0 + p1) + (p2 + p3);
+        const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[t][0], c2, -moff));
+        const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[t][1], c2, -moff));
+        const float p2 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[t][2], c2, -moff));
+        const float p3 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[t][3], c2, -moff));
+        ps0 += p0 + p1;
+        ps1 += p2 + p3;
         pw[t] = (int)pack4_e4m3(p0, p1, p2, p3);
       }
-      l_run[u] = l_run[u] * alpha[u] + psum;
+      l_run[u] = l_run[u] * alpha + (ps0 + ps1);
       pop[u] = i32x8{pw[0], pw[1], pw[2], pw[3], pw[4], pw[5], pw[6], pw[7]};
-    }
-    if (__any(rescale)) {
+      // Materialise P for this query tile here: without this the optimiser
+      // sinks every tile's exp/pack into the P.V phase and keeps all S live.
+      asm volatile("" : "+v"(pop[u]));
+      if (__any(alpha != 1.0f)) {
 #pragma unroll
-      for (int u = 0; u < QT; ++u)
-#pragma unroll
-        for (int e = 0; e < G::ETILES; ++e) acc[u][e] *= alpha[u];
+        for (int e = 0; e < G::ETILES; ++e) acc[u][e] *= alpha;
+      }
     }
 
-    // ---- O^T += V^T . P^T
+    // ---- O^T += V^T . P^T  (each V^T operand read once, used for every u)
 #pragma unroll
     for (int e = 0; e < G::ETILES; ++e) {
       const int d = 16 * e + li;
@@ -342,8 +380,13 @@ void attn_fwd_kernel(AttnArgs a) {
 #pragma unroll
       for (int u = 0; u < QT; ++u) acc[u][e] = mfma_16x16x128(vop, pop[u], acc[u][e]);
     }
+#pragma unroll
+    for (int e = 0; e < G::ETILES; ++e) {
+      __builtin_amdgcn_sched_group_barrier(0x100, 2, 1);   // DS read
+      __builtin_amdgcn_sched_group_barrier(0x008, QT, 1);  // MFMA
+    }
 
-    if (more) store_tile<D>(smem + (st ^ 1) * G::STAGE, tid, stage_k, stage_v);
+    wait_vmem_all();
     __syncthreads();
   }
 
@@ -367,8 +410,8 @@ void attn_fwd_kernel(AttnArgs a) {
               make_float4(o0, o1, o2, o3);
         } else {
           uint2 pk;
-          pk.x = f32_to_bf16_bits(o0) | (f32_to_bf16_bits(o1) << 16);
-          pk.y = f32_to_bf16_bits(o2) | (f32_to_bf16_bits(o3) << 16);
+          pk.x = pack_bf16x2(o0, o1);
+          pk.y = pack_bf16x2(o2, o3);
           *reinterpret_cast<uint2*>(static_cast<uint16_t*>(a.out) + obase + d) = pk;
         }
       }
@@ -376,10 +419,10 @@ void attn_fwd_kernel(AttnArgs a) {
   }
 }
 
-template <int D, int QT>
+template <int D, int QT, int NW>
 int launch_attn(const AttnArgs& base, bool out_f32, hipStream_t st) {
   AttnArgs a = base;
-  constexpr int BLOCK_M = 16 * QT * kWaves;
+  constexpr int BLOCK_M = 16 * QT * NW;
   a.n_qblocks = (a.Sq + BLOCK_M - 1) / BLOCK_M;
   const int64_t work = (int64_t)a.n_qblocks * a.B * a.H;
   if (work > 0x7fffffff) {
@@ -388,9 +431,11 @@ int launch_attn(const AttnArgs& base, bool out_f32, hipStream_t st) {
   }
   a.n_work = (int)work;
   if (out_f32)
-    hipLaunchKernelGGL((attn_fwd_kernel<D, QT, true>), dim3(a.n_work), dim3(kThreads), 0, st, a);
+    hipLaunchKernelGGL((attn_fwd_kernel<D, QT, NW, true>), dim3(a.n_work), dim3(NW * kWave), 0, st,
+                       a);
   else
-    hipLaunchKernelGGL((attn_fwd_kernel<D, QT, false>), dim3(a.n_work), dim3(kThreads), 0, st, a);
+    hipLaunchKernelGGL((attn_fwd_kernel<D, QT, NW, false>), dim3(a.n_work), dim3(NW * kWave), 0,
+                       st, a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) {
     rp_set_error("attn: launch failed: %s", hipGetErrorString(e));
@@ -463,6 +508,11 @@ extern "C" int rp_fp8_attn_fwd(const uint8_t* q8, const uint8_t* k8, const uint8
   a.mask = mask; a.prefix = prefix_len; a.suffix = suffix_len > 0 ? suffix_len : 1;
   hipStream_t st = static_cast<hipStream_t>(stream);
   const bool f32 = out_dtype == RP_OUT_F32;
-  if (D == 128) return launch_attn<128, 2>(a, f32, st);
-  return launch_attn<64, 4>(a, f32, st);
+  const char* cfg = getenv("RP_ATTN_CFG");  // tuning hook: "qt,nw"
+  if (cfg && D == 128) {
+    if (!strcmp(cfg, "2,4")) return launch_attn<128, 2, 4>(a, f32, st);
+    if (!strcmp(cfg, "2,8")) return launch_attn<128, 2, 8>(a, f32, st);
+  }
+  if (D == 128) return launch_attn<128, 2, 8>(a, f32, st);
+  return launch_attn<64, 2, 8>(a, f32, st);
 }
