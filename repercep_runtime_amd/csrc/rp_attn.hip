@@ -9,42 +9,46 @@
 //
 // Mapping onto CDNA4
 // ------------------
-// * Matrix core: v_mfma_f32_16x16x128_f8f6f4 (e4m3 x e4m3, fp32 acc).  For
-//   one 16x16 tile, lane l holds row/column l%16 of an operand and k-slots
-//   [32*(l/16), +32) (32 bytes); the accumulator holds rows 4*(l/16)+r,
-//   column l%16, r = 0..3.
-// * S^T = K . Q^T instead of S = Q . K^T: the accumulator of S^T puts one
-//   query per lane (column l%16) and keys down the rows, which is exactly
-//   the B-operand layout the P.V product needs, so P never leaves
-//   registers and never round-trips through LDS.  The K operand rows are
-//   gathered in a permuted order (row 4g+r of tile t is key 32g+4t+r) so
-//   that lane group g ends up owning keys [32g, 32g+32) of the 128-key
-//   block in ascending byte order.
+// * Matrix core: v_mfma_f32_32x32x64_f8f6f4 (e4m3 x e4m3, fp32 acc).  For
+//   one tile, lane l holds row/column l%32 of an operand and k-slots
+//   [32*(l/32), +32) (32 bytes); the accumulator gives lane l column l%32 and
+//   rows 8*(r/4) + 4*(l/32) + r%4 for its 16 registers r.
+// * S^T = K . Q^T instead of S = Q . K^T: the accumulator then holds one
+//   query per lane (column l%32) and keys down the rows -- exactly the
+//   B-operand layout of the P.V product, so P never leaves registers.  The
+//   K operand rows are gathered in a permuted order,
+//       row rho of key tile h  <-  key 64(h/2) + 32((rho/4)%2) + 16(h%2)
+//                                      + 4(rho/8) + rho%4,
+//   so that, for key tiles 2m and 2m+1, lane group g holds keys
+//   64m + 32g + [0, 32) in register order: the 32 bytes it feeds the
+//   O^T += V^T . P^T MFMA over those 64 keys.
 // * O^T = V^T . P^T: V^T is the A operand, read as 32 contiguous bytes per
 //   lane from the per-head transposed V (layout RP_LAYOUT_BHDS written by
 //   the quantizer).  The O^T accumulator again holds one query per lane, so
-//   the online-softmax rescale (acc *= alpha) is lane-local.
-// * Row statistics: each lane keeps the running max m and a partial row
-//   sum for its query over its 32 keys; the max is combined across the 4
-//   lanes sharing a query (xor 16, xor 32) each tile, the sums once at the
-//   end.
+//   the online-softmax rescale (acc *= alpha) is lane-local.  One 32x32
+//   operand feeds 32 queries, so each wave reads every K and V^T byte of a
+//   tile from LDS once for its 32 query rows.
+// * Row statistics: each lane keeps the running max and a partial row sum
+//   for its query over its 64 keys of the tile; the two lanes sharing a
+//   query (l, l^32) combine the max every tile and the sums once at the end.
 // * Softmax in base 2: exp(x) = exp2(x*log2e); log2e and all dequant
-//   factors are folded into one multiplier, and log2(448) into the row
+//   factors are folded into one multiplier and log2(448) into the row
 //   offset, so each score costs one FMA + one v_exp_f32 to become the
 //   e4m3-ready value p*448.  The rescale of O is skipped for a tile when no
 //   row of the wave raised its maximum (alpha == 1 exactly).
-// * 4 waves per workgroup, each wave owns QT*16 query rows; K/V tiles of
-//   128 keys are double-buffered in LDS (XOR-swizzled 16-byte chunks so the
-//   operand reads are bank-conflict free) and prefetched from HBM one tile
-//   ahead through registers.
+// * Workgroup of 8 waves x 32 query rows, two waves per SIMD (<= 256 VGPRs
+//   each), in two groups of four that alternate between an MFMA phase and a
+//   softmax phase at every workgroup barrier, so that on each SIMD one
+//   wave's MFMAs overlap the other wave's softmax.  K tiles of 128 keys are
+//   double-buffered and V^T tiles triple-buffered in LDS, loaded with
+//   global_load_lds_dwordx4 (no VGPR staging); each LDS row carries one
+//   16-byte pad granule so every 16-lane ds_read_b128 group hits 16
+//   distinct bank groups.
 // * Grid: one workgroup per (head, query block), remapped so that the
 //   workgroups resident on one XCD (dispatch is round-robin over the 8
 //   XCDs) work on the same head and share its K/V through that XCD's L2.
 
 #include "rp_common.h"
-
-#include <stdlib.h>
-#include <string.h>
 
 namespace rp {
 namespace {
@@ -71,41 +75,56 @@ struct AttnArgs {
   int n_work;
 };
 
-__device__ __forceinline__ f32x4 mfma_16x16x128(const i32x8& a, const i32x8& b, const f32x4& c) {
+__device__ __forceinline__ f32x16 mfma_32x32x64(const i32x8& a, const i32x8& b, const f32x16& c) {
   // cbsz = blgp = 0: both operands OCP e4m3; scale operands 0 select the
   // unscaled instruction.
-  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, 0, 0, 0);
+  return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, 0, 0, 0, 0, 0, 0);
 }
 
 __device__ __forceinline__ i32x8 cat8(const i32x4& lo, const i32x4& hi) {
   return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
 }
 
+// v_max3_f32 straight from asm: the builtin form makes the compiler quiet
+// every MFMA result (v_max_f32 x, x, x) first, which doubles the VALU cost of
+// the row max.  Scores are never signalling NaNs.
 __device__ __forceinline__ float max3f(float a, float b, float c) {
-  return __builtin_fmaxf(a, __builtin_fmaxf(b, c));
+  float r;
+  asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+  return r;
 }
 
 template <int D, int NW>
 struct Geo {
   static constexpr int THREADS = NW * kWave;
   static constexpr int KCH = D / 16;                 // 16-byte chunks per K row
-  static constexpr int ETILES = D / 16;              // 16-row tiles of O^T
-  static constexpr int K_BYTES = kBlockN * D;
-  static constexpr int V_BYTES = D * kBlockN;
-  static constexpr int STAGE = K_BYTES + V_BYTES;
-  static constexpr int K_LOADS = K_BYTES / 16 / THREADS;
-  static constexpr int V_LOADS = V_BYTES / 16 / THREADS;
+  static constexpr int KSTEPS = D / 64;              // 64-deep MFMA steps over D
+  static constexpr int ETILES = D / 32;              // 32-row tiles of O^T
+  // LDS pitches carry one 16-byte pad granule per row: the granule count per
+  // row (9 or 5) is odd, so 16 consecutive rows start in 16 distinct 16-byte
+  // bank groups and every operand read is conflict-free without swizzling.
+  static constexpr int K_PITCH = D + 16;
+  static constexpr int V_PITCH = kBlockN + 16;
+  static constexpr int K_GRAN = K_PITCH / 16;   // granules per K row
+  static constexpr int V_GRAN = V_PITCH / 16;
+  static constexpr int K_BYTES = kBlockN * K_PITCH;
+  static constexpr int V_BYTES = D * V_PITCH;
+  static constexpr int K_BLKS = kBlockN * K_GRAN / 64;  // wave instructions per K tile
+  static constexpr int V_BLKS = D * V_GRAN / 64;
+  static constexpr int K_LOADS_MAX = (K_BLKS + NW - 1) / NW;
+  static constexpr int V_LOADS_MAX = (V_BLKS + NW - 1) / NW;
+  static constexpr int K_STAGES = 2;               // ping-pong layout:
+  static constexpr int V_STAGES = 3;               // V^T lives one step longer
+  static constexpr int LDS_BYTES = K_STAGES * K_BYTES + V_STAGES * V_BYTES;
   static_assert(D == 64 || D == 128, "head dim");
-  static_assert(K_LOADS * 16 * THREADS == K_BYTES, "K tile split");
-  static_assert(V_LOADS * 16 * THREADS == V_BYTES, "V tile split");
+  static_assert(K_BLKS * 64 == kBlockN * K_GRAN && V_BLKS * 64 == D * V_GRAN, "whole KiB blocks");
 };
 
-// Chunk swizzles (16-byte granules) for the two LDS tiles.
-template <int D>
-__device__ __forceinline__ int k_swz(int r) {
-  return ((r & 3) | ((r >> 3) & 4)) & (D / 16 - 1);
+// Key (row inside the 128-key tile) that row rho of the S^T A operand of key
+// tile h carries.
+__device__ __forceinline__ int key_of(int h, int rho) {
+  return 64 * (h >> 1) + 32 * ((rho >> 2) & 1) + 16 * (h & 1) + ((rho >> 3) << 2) + (rho & 3);
 }
-__device__ __forceinline__ int v_swz(int d) { return d & 7; }
 
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 typedef __attribute__((address_space(1))) void* gbl_ptr_t;
@@ -121,11 +140,27 @@ __device__ __forceinline__ void gload_lds16(const void* src, void* lds_block) {
 // contiguous KiB of LDS, so the XOR swizzle is applied on the global side:
 // the lane that lands on physical chunk `phys` of row r fetches logical chunk
 // phys ^ swz(r).
+// Combine a lane's value with lane l^32's (the other half of the wave)
+// through v_permlane32_swap -- a VALU op, no LDS round trip.
+__device__ __forceinline__ float xhalf_max(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return max3f(__uint_as_float(r[0]), __uint_as_float(r[1]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float xhalf_sum(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// Direct-to-LDS loads of one (K, V^T) tile.  Each wave instruction fills one
+// contiguous KiB (64 granules) of LDS; granule p of a tile is row p / GRAN,
+// slot p % GRAN.  K rows are stored in S^T A-operand order (LDS row 32h + rho
+// holds key_of(h, rho)); V^T rows are d.  Pad slots re-load the row's first
+// granule (valid memory, never read).
 template <int D, int NW>
 struct TileOffsets {
-  uint32_t k[Geo<D, NW>::K_LOADS];  // relative to kh + kv0*D
-  uint32_t v[Geo<D, NW>::V_LOADS];  // relative to vh + kv0
-  int k_row[Geo<D, NW>::K_LOADS];   // key row of each K load inside the tile
+  uint32_t k[Geo<D, NW>::K_LOADS_MAX];  // relative to kh + kv0*D
+  int k_key[Geo<D, NW>::K_LOADS_MAX];   // key inside the tile
+  uint32_t v[Geo<D, NW>::V_LOADS_MAX];  // relative to vh + kv0
 };
 
 template <int D, int NW>
@@ -133,42 +168,48 @@ __device__ __forceinline__ TileOffsets<D, NW> tile_offsets(int64_t ldv, int wave
   using G = Geo<D, NW>;
   TileOffsets<D, NW> o;
 #pragma unroll
-  for (int n = 0; n < G::K_LOADS; ++n) {
+  for (int n = 0; n < G::K_LOADS_MAX; ++n) {
     const int p = (n * NW + wave) * kWave + lane;
-    const int r = p / G::KCH, phys = p % G::KCH;
-    o.k_row[n] = r;
-    o.k[n] = (uint32_t)(r * D + ((phys ^ k_swz<D>(r)) << 4));
+    const int row = p / G::K_GRAN, slot = p % G::K_GRAN;
+    const int key = key_of(row >> 5, row & 31);
+    o.k_key[n] = key;
+    o.k[n] = (uint32_t)(key * D + (slot < D / 16 ? slot : 0) * 16);
   }
 #pragma unroll
-  for (int n = 0; n < G::V_LOADS; ++n) {
+  for (int n = 0; n < G::V_LOADS_MAX; ++n) {
     const int p = (n * NW + wave) * kWave + lane;
-    const int d = p >> 3, phys = p & 7;
-    o.v[n] = (uint32_t)(d * ldv + ((phys ^ v_swz(d)) << 4));
+    const int d = p / G::V_GRAN, slot = p % G::V_GRAN;
+    o.v[n] = (uint32_t)(d * ldv + (slot < kBlockN / 16 ? slot : 0) * 16);
   }
   return o;
 }
 
-// Issue tile `kb` into one LDS stage.  K rows past Skv (last tile only)
-// re-read the last key -- their scores are masked; V^T is zero-padded to ldv.
+// Issue tile `kb`.  K rows past Skv (last tile only) re-read the last key --
+// their scores are masked; V^T is zero-padded to ldv.
 template <int D, int NW>
 __device__ __forceinline__ void issue_tile(const AttnArgs& a, const uint8_t* kh, const uint8_t* vh,
-                                           const TileOffsets<D, NW>& o, int kb, uint8_t* stage,
-                                           int wave) {
+                                           const TileOffsets<D, NW>& o, int kb, uint8_t* kst,
+                                           uint8_t* vst, int wave) {
   using G = Geo<D, NW>;
   const int kv0 = kb * kBlockN;
   const uint8_t* kt = kh + (int64_t)kv0 * D;
   const bool tail = kv0 + kBlockN > a.Skv;
 #pragma unroll
-  for (int n = 0; n < G::K_LOADS; ++n) {
-    uint32_t off = o.k[n];
-    if (tail && kv0 + o.k_row[n] >= a.Skv)
-      off = off - (uint32_t)((kv0 + o.k_row[n] - (a.Skv - 1)) * D);
-    gload_lds16(kt + off, stage + (n * NW + wave) * 1024);
+  for (int n = 0; n < G::K_LOADS_MAX; ++n) {
+    const int blk = n * NW + wave;
+    if (blk < G::K_BLKS) {
+      uint32_t off = o.k[n];
+      if (tail && kv0 + o.k_key[n] >= a.Skv)
+        off = off - (uint32_t)((kv0 + o.k_key[n] - (a.Skv - 1)) * D);
+      gload_lds16(kt + off, kst + blk * 1024);
+    }
   }
   const uint8_t* vt = vh + kv0;
-  uint8_t* vst = stage + G::K_BYTES;
 #pragma unroll
-  for (int n = 0; n < G::V_LOADS; ++n) gload_lds16(vt + o.v[n], vst + (n * NW + wave) * 1024);
+  for (int n = 0; n < G::V_LOADS_MAX; ++n) {
+    const int blk = n * NW + wave;
+    if (blk < G::V_BLKS) gload_lds16(vt + o.v[n], vst + blk * 1024);
+  }
 }
 
 __device__ __forceinline__ void wait_vmem_all() {
@@ -181,16 +222,34 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
   return (uint32_t)__builtin_bit_cast(uint16_t, a) | ((uint32_t)__builtin_bit_cast(uint16_t, b) << 16);
 }
 
-// NW waves per workgroup, each owning QT 16-row query tiles; launch bounds
-// ask for two waves per SIMD (256 VGPRs each) so one wave's MFMAs overlap
-// the other's softmax.
-template <int D, int QT, int NW, bool OUT_F32>
-__global__ __launch_bounds__(NW * kWave, 8 / NW)
+// Eight waves per workgroup in two groups of four; waves w and w+4 share a
+// SIMD.  The groups run half a step out of phase ("ping-pong"), separated by
+// workgroup barriers, so that on every SIMD one wave issues MFMAs while the
+// other runs the softmax:
+//
+//   slot 2i   : group 0  MFMA(i)        group 1  SOFTMAX(i-1)
+//   slot 2i+1 : group 0  SOFTMAX(i)     group 1  MFMA(i)
+//
+//   MFMA(i)    = S^T(i) = K(i) . Q^T   and   O^T += V^T(i-1) . P^T(i-1)
+//   SOFTMAX(i) = mask, running max, P(i) = e4m3(p * 448), row sums,
+//                O^T *= alpha(i)  (after the P(i-1) contribution, before P(i)'s)
+//
+// Numbering the workgroup barriers from the prologue's (0), group 0 runs
+// MFMA(j) between barriers 2j and 2j+1 and group 1 between 2j+1 and 2j+2.
+// Tile j (K(j), V^T(j)) overwrites K(j-2) and V^T(j-3), whose last reads end
+// at barrier 2j-2, and is first read right after barrier 2j; so every wave
+// issues its share of tile j after barrier 2j-2 and waits for it
+// (s_waitcnt vmcnt(0)) before barrier 2j.
+template <int D, bool OUT_F32>
+__global__ __launch_bounds__(512, 1)
 void attn_fwd_kernel(AttnArgs a) {
+  constexpr int NW = 8;
   using G = Geo<D, NW>;
-  constexpr int QROWS = 16 * QT;
+  constexpr int QROWS = 32;
   constexpr int BLOCK_M = QROWS * NW;
-  __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * G::STAGE];
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[G::LDS_BYTES];
+  uint8_t* const kbuf = smem;                              // K_STAGES x K_BYTES
+  uint8_t* const vbuf = smem + G::K_STAGES * G::K_BYTES;   // V_STAGES x V_BYTES
 
   // ---- work item (XCD-aware remap of the linear workgroup id)
   const int w = blockIdx.x;
@@ -204,11 +263,13 @@ void attn_fwd_kernel(AttnArgs a) {
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
   const int wave = tid >> 6;
-  const int li = lane & 15;  // row/column inside a 16x16 tile
-  const int lg = lane >> 4;  // k-slot group (32 bytes)
+  const int group = wave >> 2;
+  const int lq = lane & 31;  // query column / operand row inside a 32x32 tile
+  const int lg = lane >> 5;  // k-slot group (32 bytes)
 
   const int q_block0 = qb * BLOCK_M;
   const int q_wave0 = q_block0 + wave * QROWS;
+  const int q = q_wave0 + lq;  // this lane's query
 
   const uint8_t* qh = a.q + (int64_t)bh * a.Sq * D;
   const uint8_t* kh = a.k + (int64_t)bh * a.Skv * D;
@@ -228,183 +289,164 @@ void attn_fwd_kernel(AttnArgs a) {
   }
 
   const TileOffsets<D, NW> toff = tile_offsets<D, NW>(a.ldv, wave, lane);
-  issue_tile<D, NW>(a, kh, vh, toff, 0, smem, wave);
+  issue_tile<D, NW>(a, kh, vh, toff, 0, kbuf, vbuf, wave);
 
   // ---- Q^T operand (B operand of S^T), resident for the whole kernel
-  i32x8 qop[QT];
+  i32x8 qop[G::KSTEPS];
+  {
+    const i32x4* src = reinterpret_cast<const i32x4*>(qh + (int64_t)min(q, a.Sq - 1) * D + 32 * lg);
 #pragma unroll
-  for (int u = 0; u < QT; ++u) {
-    const int qrow = min(q_wave0 + 16 * u + li, a.Sq - 1);
-    if (32 * lg < D) {
-      const i32x4* src = reinterpret_cast<const i32x4*>(qh + (int64_t)qrow * D + 32 * lg);
-      qop[u] = cat8(src[0], src[1]);
-    } else {
-      qop[u] = i32x8{0, 0, 0, 0, 0, 0, 0, 0};
-    }
+    for (int ks = 0; ks < G::KSTEPS; ++ks) qop[ks] = cat8(src[4 * ks], src[4 * ks + 1]);
   }
 
-  // ---- online softmax state (per lane: query q_wave0 + 16u + li)
-  f32x4 acc[QT][G::ETILES];
-  float m_run[QT], l_run[QT];
-#pragma unroll
-  for (int u = 0; u < QT; ++u) {
-    m_run[u] = -__builtin_inff();
-    l_run[u] = 0.0f;
-#pragma unroll
-    for (int e = 0; e < G::ETILES; ++e) acc[u][e] = f32x4{0.f, 0.f, 0.f, 0.f};
-  }
+  // per-lane LDS byte offsets of the operand reads (inside one stage): row
+  // lq of each 32-row operand block, k-slot group lg; the rest is immediate
+  const int k_base = lq * G::K_PITCH + 32 * lg;
+  const int v_base = lq * G::V_PITCH + 32 * lg;
 
-  // K operand row of tile t for this lane: 32*(li>>2) + 4t + (li&3).  Its
-  // swizzle reads bits 0-1 and 5 of the row, which 4t (t < 8) never changes.
-  const int k_row0 = 32 * (li >> 2) + (li & 3);
-  const int k_sw = k_swz<D>(k_row0);
-  const bool k_has = 32 * lg < D;
-  const int k_off0 = k_row0 * D + (((2 * lg) ^ k_sw) << 4);
-  const int k_off1 = k_row0 * D + (((2 * lg + 1) ^ k_sw) << 4);
+  f32x16 acc[G::ETILES];
+#pragma unroll
+  for (int e = 0; e < G::ETILES; ++e) acc[e] = f32x16{};
+  float m_run = -__builtin_inff(), l_run = 0.0f;
+  f32x16 s[4];
+  i32x8 pop[2] = {i32x8{}, i32x8{}};
 
   wait_vmem_all();
   __syncthreads();
+  if (group == 1) {  // group 1 starts half a step behind
+    if (n_kb > 1)
+      issue_tile<D, NW>(a, kh, vh, toff, 1, kbuf + G::K_BYTES, vbuf + G::V_BYTES, wave);
+    __syncthreads();
+  }
 
-  for (int kb = 0; kb < n_kb; ++kb) {
-    const int st = kb & 1;
-    if (kb + 1 < n_kb) issue_tile<D, NW>(a, kh, vh, toff, kb + 1, smem + (st ^ 1) * G::STAGE, wave);
-
-    const uint8_t* kl = smem + st * G::STAGE;
-    const uint8_t* vl = kl + G::K_BYTES;
-    const int kv0 = kb * kBlockN;
-
-    const bool tail = kv0 + kBlockN > a.Skv;
-    bool need_mask = tail;
-    if (a.mask == RP_MASK_CAUSAL) need_mask |= kv0 + kBlockN - 1 > q_wave0;
-    if (a.mask == RP_MASK_SHARED_PREFIX) need_mask |= kv0 + kBlockN > a.prefix;
-    const int kvl = kv0 + 32 * lg;  // key of (t, r) is kvl + 4t + r
-    const int pre_end = a.mask == RP_MASK_SHARED_PREFIX ? min(a.prefix, a.Skv) : 0;
-
-    i32x8 pop[QT];
+  for (int i = 0; i <= n_kb; ++i) {
+    // ================= MFMA(i) =================
+    // Tile j is issued by every wave right after workgroup barrier 2j-2 and
+    // waited for before barrier 2j (the prologue's barrier is number 0):
+    // group 0 issues at the start of MFMA(j-1) and waits at the end of
+    // SOFTMAX(j-1); group 1 issues at the start of SOFTMAX(j-2) and waits at
+    // the end of MFMA(j-1).
+    if (group == 0 && i + 1 < n_kb)
+      issue_tile<D, NW>(a, kh, vh, toff, i + 1, kbuf + ((i + 1) & 1) * G::K_BYTES,
+                        vbuf + ((i + 1) % 3) * G::V_BYTES, wave);
+    if (i < n_kb) {
+      const uint8_t* kl = kbuf + (i & 1) * G::K_BYTES + k_base;
 #pragma unroll
-    for (int u = 0; u < QT; ++u) {
-      // ---- S^T tile column block u: s[t][r] = score(query u, key kvl + 4t + r)
-      f32x4 s[8];
-      // Re-read K per query tile u rather than keeping 8 K operands (64 VGPRs)
-      // live across u: the empty asm hides that the address is unchanged.
-      // (a 32-bit LDS offset, so the loads stay ds_read_b128)
-      int kbu = st * G::STAGE;
-      asm volatile("" : "+v"(kbu));
+      for (int hh = 0; hh < 4; ++hh) {
 #pragma unroll
-      for (int t = 0; t < 8; ++t) {
-        i32x8 kop = i32x8{0, 0, 0, 0, 0, 0, 0, 0};
-        if (k_has)
-          kop = cat8(*reinterpret_cast<const i32x4*>(smem + kbu + k_off0 + 4 * t * D),
-                     *reinterpret_cast<const i32x4*>(smem + kbu + k_off1 + 4 * t * D));
-        s[t] = mfma_16x16x128(kop, qop[u], f32x4{0.f, 0.f, 0.f, 0.f});
+        for (int ks = 0; ks < G::KSTEPS; ++ks) {
+          const uint8_t* p = kl + 32 * hh * G::K_PITCH + 64 * ks;
+          const i32x8 kop = cat8(*reinterpret_cast<const i32x4*>(p),
+                                 *reinterpret_cast<const i32x4*>(p + 16));
+          // first k-step starts from the inline constant 0 (no zeroed registers)
+          s[hh] = mfma_32x32x64(kop, qop[ks], ks == 0 ? f32x16{} : s[hh]);
+        }
       }
-      // Pipeline the scheduler to "2 LDS reads, 1 MFMA" so only a couple of
-      // K operands are in flight (each holds 8 VGPRs).
+    }
+    if (i > 0) {
+      const uint8_t* vl = vbuf + ((i - 1) % 3) * G::V_BYTES + v_base;
 #pragma unroll
-      for (int t = 0; t < 8; ++t) {
-        __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // DS read
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+      for (int e = 0; e < G::ETILES; ++e) {
+#pragma unroll
+        for (int m = 0; m < 2; ++m) {
+          const uint8_t* p = vl + 32 * e * G::V_PITCH + 64 * m;
+          const i32x8 vop = cat8(*reinterpret_cast<const i32x4*>(p),
+                                 *reinterpret_cast<const i32x4*>(p + 16));
+          acc[e] = mfma_32x32x64(vop, pop[m], acc[e]);
+        }
       }
+    }
+    if (group == 1) wait_vmem_all();
+    __syncthreads();
 
-      // ---- masking: every supported mask is "kv < pre_end, or lo <= kv <= hi"
-      // with a per-query window; bitwise predicates, one select per score.
+    // ================= SOFTMAX(i) =================
+    if (group == 1 && i + 2 < n_kb)
+      issue_tile<D, NW>(a, kh, vh, toff, i + 2, kbuf + ((i + 2) & 1) * G::K_BYTES,
+                        vbuf + ((i + 2) % 3) * G::V_BYTES, wave);
+    if (i < n_kb) {
+      const int kv0 = i * kBlockN;
+      bool need_mask = kv0 + kBlockN > a.Skv;
+      if (a.mask == RP_MASK_CAUSAL) need_mask |= kv0 + kBlockN - 1 > q_wave0;
+      if (a.mask == RP_MASK_SHARED_PREFIX) need_mask |= kv0 + kBlockN > a.prefix;
       if (need_mask) {
+        // every supported mask is "kv < pre_end, or lo <= kv <= hi" with a
+        // per-query window; bitwise predicates, one select per score
         const float ninf = -__builtin_inff();
-        const int q = q_wave0 + 16 * u + li;
         int lo = 0, hi = a.Skv - 1;
         if (a.mask == RP_MASK_CAUSAL) hi = min(q, hi);
         if (a.mask == RP_MASK_SHARED_PREFIX) {
           lo = a.prefix + q - q % a.suffix;
           hi = min(a.prefix + q, hi);
         }
+        const int pre_end = a.mask == RP_MASK_SHARED_PREFIX ? min(a.prefix, a.Skv) : 0;
+        const int kvl = kv0 + 32 * lg;
         const int lo_t = lo - kvl, hi_t = hi - kvl, pe_t = pre_end - kvl;
 #pragma unroll
-        for (int t = 0; t < 8; ++t)
+        for (int hh = 0; hh < 4; ++hh)
 #pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int o = 4 * t + r;
+          for (int r = 0; r < 16; ++r) {
+            const int o = 64 * (hh >> 1) + 16 * (hh & 1) + r;  // key - kvl
             const int vis = ((o >= lo_t) & (o <= hi_t)) | (o < pe_t);
-            s[t][r] = vis ? s[t][r] : ninf;
+            s[hh][r] = vis ? s[hh][r] : ninf;
           }
       }
-
-      // ---- online softmax for this lane's query
-      float mx = max3f(s[0][0], s[0][1], s[0][2]);
-      mx = max3f(mx, s[0][3], s[1][0]);
-      mx = max3f(mx, s[1][1], s[1][2]);
-      mx = max3f(mx, s[1][3], s[2][0]);
+      // row max over the lane's 64 scores: four independent v_max3 chains
+      // (one per key tile), then combine
+      float mt[4];
 #pragma unroll
-      for (int t = 2; t < 8; ++t) {
-        if (t > 2) mx = max3f(mx, s[t][0], s[t][1]);
-        else mx = __builtin_fmaxf(mx, s[t][1]);
-        mx = max3f(mx, s[t][2], s[t][3]);
+      for (int hh = 0; hh < 4; ++hh) {
+        float x = max3f(s[hh][0], s[hh][1], s[hh][2]);
+#pragma unroll
+        for (int r = 3; r < 15; r += 2) x = max3f(x, s[hh][r], s[hh][r + 1]);
+        mt[hh] = max3f(x, s[hh][15], s[hh][15]);
       }
-      mx = __builtin_fmaxf(mx, shfl_xor(mx, 16));
-      mx = __builtin_fmaxf(mx, shfl_xor(mx, 32));
-      const float m_new = __builtin_fmaxf(m_run[u], mx * c2);
+      float mx = max3f(mt[0], mt[1], max3f(mt[2], mt[3], mt[3]));
+      mx = xhalf_max(mx);
+      const float m_new = __builtin_fmaxf(m_run, mx * c2);
       const float m_use = (m_new == -__builtin_inff()) ? 0.0f : m_new;
-      const float alpha = __builtin_amdgcn_exp2f(m_run[u] - m_use);
-      m_run[u] = m_new;
+      const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
+      m_run = m_new;
       const float moff = m_use - kLog2PMax;
-      float ps0 = 0.0f, ps1 = 0.0f;
-      int pw[8];
+      float ps[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-      for (int t = 0; t < 8; ++t) {
-        const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[t][0], c2, -moff));
-        const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[t][1], c2, -moff));
-        const float p2 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[t][2], c2, -moff));
-        const float p3 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[t][3], c2, -moff));
-        ps0 += p0 + p1;
-        ps1 += p2 + p3;
-        pw[t] = (int)pack4_e4m3(p0, p1, p2, p3);
+      for (int m = 0; m < 2; ++m) {
+        int pw[8];
+#pragma unroll
+        for (int wd = 0; wd < 8; ++wd) {
+          const int hh = 2 * m + (wd >> 2);
+          const int r = 4 * (wd & 3);
+          const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[hh][r + 0], c2, -moff));
+          const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[hh][r + 1], c2, -moff));
+          const float p2 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[hh][r + 2], c2, -moff));
+          const float p3 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[hh][r + 3], c2, -moff));
+          ps[wd & 3] += (p0 + p1) + (p2 + p3);
+          pw[wd] = (int)pack4_e4m3(p0, p1, p2, p3);
+        }
+        pop[m] = i32x8{pw[0], pw[1], pw[2], pw[3], pw[4], pw[5], pw[6], pw[7]};
       }
-      l_run[u] = l_run[u] * alpha + (ps0 + ps1);
-      pop[u] = i32x8{pw[0], pw[1], pw[2], pw[3], pw[4], pw[5], pw[6], pw[7]};
-      // Materialise P for this query tile here: without this the optimiser
-      // sinks every tile's exp/pack into the P.V phase and keeps all S live.
-      asm volatile("" : "+v"(pop[u]));
+      l_run = l_run * alpha + ((ps[0] + ps[1]) + (ps[2] + ps[3]));
       if (__any(alpha != 1.0f)) {
 #pragma unroll
-        for (int e = 0; e < G::ETILES; ++e) acc[u][e] *= alpha;
+        for (int e = 0; e < G::ETILES; ++e) acc[e] *= alpha;
       }
     }
-
-    // ---- O^T += V^T . P^T  (each V^T operand read once, used for every u)
-#pragma unroll
-    for (int e = 0; e < G::ETILES; ++e) {
-      const int d = 16 * e + li;
-      const int sw = v_swz(d);
-      const uint8_t* row = vl + d * kBlockN;
-      const i32x8 vop = cat8(*reinterpret_cast<const i32x4*>(row + (((2 * lg) ^ sw) << 4)),
-                             *reinterpret_cast<const i32x4*>(row + (((2 * lg + 1) ^ sw) << 4)));
-#pragma unroll
-      for (int u = 0; u < QT; ++u) acc[u][e] = mfma_16x16x128(vop, pop[u], acc[u][e]);
-    }
-#pragma unroll
-    for (int e = 0; e < G::ETILES; ++e) {
-      __builtin_amdgcn_sched_group_barrier(0x100, 2, 1);   // DS read
-      __builtin_amdgcn_sched_group_barrier(0x008, QT, 1);  // MFMA
-    }
-
-    wait_vmem_all();
+    if (group == 0) wait_vmem_all();
     __syncthreads();
   }
+  if (group == 0) __syncthreads();  // balance group 1's extra opening barrier
 
   // ---- epilogue: out = acc * v_scale / l  (acc carries P*448, l sums P*448)
+  const float l = xhalf_sum(l_run);
+  const float inv = v_scale / l;
+  if (q < a.Sq) {
+    const int64_t obase = (int64_t)b * a.osb + (int64_t)h * a.osh + (int64_t)q * a.oss;
 #pragma unroll
-  for (int u = 0; u < QT; ++u) {
-    float l = l_run[u];
-    l += shfl_xor(l, 16);
-    l += shfl_xor(l, 32);
-    const float inv = v_scale / l;
-    const int q = q_wave0 + 16 * u + li;
-    if (q < a.Sq) {
-      const int64_t obase = (int64_t)b * a.osb + (int64_t)h * a.osh + (int64_t)q * a.oss;
+    for (int e = 0; e < G::ETILES; ++e)
 #pragma unroll
-      for (int e = 0; e < G::ETILES; ++e) {
-        const int d = 16 * e + 4 * lg;
-        const float o0 = acc[u][e][0] * inv, o1 = acc[u][e][1] * inv;
-        const float o2 = acc[u][e][2] * inv, o3 = acc[u][e][3] * inv;
+      for (int i = 0; i < 4; ++i) {
+        const int d = 32 * e + 8 * i + 4 * lg;
+        const float o0 = acc[e][4 * i + 0] * inv, o1 = acc[e][4 * i + 1] * inv;
+        const float o2 = acc[e][4 * i + 2] * inv, o3 = acc[e][4 * i + 3] * inv;
         if constexpr (OUT_F32) {
           *reinterpret_cast<float4*>(static_cast<float*>(a.out) + obase + d) =
               make_float4(o0, o1, o2, o3);
@@ -415,14 +457,13 @@ void attn_fwd_kernel(AttnArgs a) {
           *reinterpret_cast<uint2*>(static_cast<uint16_t*>(a.out) + obase + d) = pk;
         }
       }
-    }
   }
 }
 
-template <int D, int QT, int NW>
+template <int D>
 int launch_attn(const AttnArgs& base, bool out_f32, hipStream_t st) {
   AttnArgs a = base;
-  constexpr int BLOCK_M = 16 * QT * NW;
+  constexpr int BLOCK_M = 32 * 8;
   a.n_qblocks = (a.Sq + BLOCK_M - 1) / BLOCK_M;
   const int64_t work = (int64_t)a.n_qblocks * a.B * a.H;
   if (work > 0x7fffffff) {
@@ -431,11 +472,9 @@ int launch_attn(const AttnArgs& base, bool out_f32, hipStream_t st) {
   }
   a.n_work = (int)work;
   if (out_f32)
-    hipLaunchKernelGGL((attn_fwd_kernel<D, QT, NW, true>), dim3(a.n_work), dim3(NW * kWave), 0, st,
-                       a);
+    hipLaunchKernelGGL((attn_fwd_kernel<D, true>), dim3(a.n_work), dim3(512), 0, st, a);
   else
-    hipLaunchKernelGGL((attn_fwd_kernel<D, QT, NW, false>), dim3(a.n_work), dim3(NW * kWave), 0,
-                       st, a);
+    hipLaunchKernelGGL((attn_fwd_kernel<D, false>), dim3(a.n_work), dim3(512), 0, st, a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) {
     rp_set_error("attn: launch failed: %s", hipGetErrorString(e));
@@ -508,11 +547,6 @@ extern "C" int rp_fp8_attn_fwd(const uint8_t* q8, const uint8_t* k8, const uint8
   a.mask = mask; a.prefix = prefix_len; a.suffix = suffix_len > 0 ? suffix_len : 1;
   hipStream_t st = static_cast<hipStream_t>(stream);
   const bool f32 = out_dtype == RP_OUT_F32;
-  const char* cfg = getenv("RP_ATTN_CFG");  // tuning hook: "qt,nw"
-  if (cfg && D == 128) {
-    if (!strcmp(cfg, "2,4")) return launch_attn<128, 2, 4>(a, f32, st);
-    if (!strcmp(cfg, "2,8")) return launch_attn<128, 2, 8>(a, f32, st);
-  }
-  if (D == 128) return launch_attn<128, 2, 8>(a, f32, st);
-  return launch_attn<64, 2, 8>(a, f32, st);
+  if (D == 128) return launch_attn<128>(a, f32, st);
+  return launch_attn<64>(a, f32, st);
 }
