@@ -11,8 +11,10 @@ flash-attention forward writing bf16 output -- the work of the reference's
 4*B*H*S^2*D per step / step time).  ``roofline`` is the attention kernel's
 own MFMA roofline, its average launch time measured with HIP events on the
 stream the kernel runs on.  ``quantize`` reports the quantizer's HBM rate
-(5 bytes per element).  ``cpu_baseline`` times the reference's CPU
-attention path (torch SDPA on CPU, bf16) on a bounded sample.
+(5 bytes per element).  ``cpu_baseline`` times the CPU oracle (the C
+restatement of the reference's FP8 attention) on a bounded sample, and
+``cpu_reference_sdpa`` the reference's own CPU attention path (one torch
+SDPA call in bf16).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config NAME]
 """
@@ -49,12 +51,63 @@ def _traffic_from_profiles(kernel: str, workload: str) -> float | None:
         return None
 
 
+def _grow(run, start: int, limit: int, budget_s: float) -> tuple[int, float]:
+    """Grow a row count by 4x until one timed run takes about budget_s / 4 or more."""
+    rows = min(start, limit)
+    run(rows)  # warm-up (thread pool, allocator, page faults)
+    t = run(rows)
+    while rows < limit and t < budget_s / 4:
+        rows = min(limit, rows * 4)
+        t = run(rows)
+    return rows, t
+
+
 def cpu_baseline(cfg, budget_s: float) -> dict:
-    """Reference CPU attention (torch SDPA, bf16, all host cores) on one head,
-    a row slice of the queries against all keys, extrapolated to the config."""
+    """The CPU oracle (C restatement of the reference's FP8 attention, OpenMP
+    over query rows) on one head of the workload: a row slice of the queries
+    against all keys, scaled to the workload's FLOPs."""
+    import numpy as np
     import torch
 
-    from oracle.cpu_sdpa import cpu_model, cpu_threads, sdpa_cpu
+    from oracle import native
+    from oracle.cpu_sdpa import cpu_model
+
+    gen = torch.Generator().manual_seed(cfg.seed)
+    k = torch.randn(cfg.Skv, cfg.D, generator=gen).to(torch.bfloat16)
+    v = torch.randn(cfg.Skv, cfg.D, generator=gen).to(torch.bfloat16)
+    q = torch.randn(min(cfg.Sq, 65536), cfg.D, generator=gen).to(torch.bfloat16)
+    bits = [t.view(torch.int16).numpy().view(np.uint16) for t in (q, k, v)]
+    (qs,), q8 = native.quantize_groups(bits[0], 1)
+    (ks,), k8 = native.quantize_groups(bits[1], 1)
+    (vs,), v8 = native.quantize_groups(bits[2], 1)
+    threads = native.num_threads()
+
+    def run(rows: int) -> float:
+        idx = np.arange(rows, dtype=np.int32)
+        t0 = time.perf_counter()
+        native.attn_rows(q8, k8, v8, qs, ks, vs, cfg.D ** -0.5, idx)
+        return time.perf_counter() - t0
+
+    rows, t = _grow(run, 16, q8.shape[0], budget_s)
+    tflops = 4.0 * rows * cfg.Skv * cfg.D / t / 1e12
+    return {
+        "value": round(tflops, 5),
+        "unit": "TFLOP/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": (f"C oracle (tile-exact FP8 emulation, {threads} OpenMP threads, "
+                   f"{cpu_model()}): 1 head, {rows} query rows x {cfg.Skv} keys x D={cfg.D} "
+                   f"in {t:.2f} s; full {cfg.name} extrapolates to "
+                   f"{cfg.flops / (tflops * 1e12):.0f} s"),
+    }
+
+
+def cpu_sdpa_baseline(cfg, budget_s: float) -> dict:
+    """The reference's CPU attention path (one torch SDPA call in bf16, all
+    host cores) on one head, a row slice of the queries against all keys."""
+    import torch
+
+    from oracle.cpu_sdpa import cpu_threads, sdpa_cpu
 
     threads = cpu_threads()
     gen = torch.Generator().manual_seed(cfg.seed)
@@ -67,25 +120,10 @@ def cpu_baseline(cfg, budget_s: float) -> dict:
         sdpa_cpu(q, k, v)
         return time.perf_counter() - t0
 
-    rows = min(256, cfg.Sq)
-    run(rows)  # warm-up (thread pool, allocator)
-    t = run(rows)
-    # grow the slice to fill about budget_s of CPU work
-    while rows < cfg.Sq and t < budget_s / 4:
-        rows = min(cfg.Sq, rows * 4)
-        t = run(rows)
-    flops_sample = 4.0 * rows * cfg.Skv * cfg.D
-    tflops = flops_sample / t / 1e12
-    return {
-        "value": round(tflops, 4),
-        "unit": "TFLOP/s",
-        "cores": threads,
-        "kind": "port",
-        "sample": (f"torch SDPA on CPU (bf16, {threads} threads, {cpu_model()}): 1 head, "
-                   f"{rows} query rows x {cfg.Skv} keys x D={cfg.D} in {t:.2f} s; "
-                   f"full {cfg.name} extrapolates to "
-                   f"{cfg.flops / (tflops * 1e12):.0f} s"),
-    }
+    rows, t = _grow(run, 256, cfg.Sq, budget_s)
+    tflops = 4.0 * rows * cfg.Skv * cfg.D / t / 1e12
+    return {"value": round(tflops, 4), "unit": "TFLOP/s", "cores": threads,
+            "sample": f"torch SDPA bf16 on CPU, 1 head, {rows} query rows in {t:.2f} s"}
 
 
 def bench_attention(args, cfg) -> dict:
@@ -282,6 +320,7 @@ def main() -> int:
         if args.cpu_budget > 0:
             log("[bench] timing the CPU baseline")
             res["cpu_baseline"] = cpu_baseline(cfg, args.cpu_budget)
+            res["cpu_reference_sdpa"] = cpu_sdpa_baseline(cfg, args.cpu_budget / 3)
     print(json.dumps(res), flush=True)
     return 0
 
