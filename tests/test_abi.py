@@ -1,0 +1,117 @@
+"""The C-ABI library loads on a CPU-only host and exports what its header declares.
+
+No compute call is made here (there is no GPU): only host-side entry points
+(version, status strings, workspace sizing) and argument checks that every
+entry point performs before it touches the device.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import re
+import subprocess
+from pathlib import Path
+
+import pytest
+
+from repercep_runtime_amd import _capi
+
+ROOT = Path(__file__).resolve().parent.parent
+HEADER = ROOT / "include" / "repercep_fp8.h"
+FAKE = 1 << 20           # 16-byte aligned non-null address; never dereferenced
+
+
+def _declared() -> set[str]:
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return set(re.findall(r"^[A-Za-z_][\w\s\*]*?\b(rp_\w+)\s*\(", text, flags=re.M))
+
+
+def test_header_declarations_match_binding() -> None:
+    declared = _declared()
+    assert declared, "no declarations parsed"
+    assert declared == set(_capi.EXPORTS)
+
+
+def test_library_exports_every_declared_symbol() -> None:
+    assert _capi.LIB_PATH.exists(), "build first: python -c 'import __graft_entry__ as g; g.build()'"
+    nm = subprocess.run(["nm", "-D", "--defined-only", str(_capi.LIB_PATH)], check=True,
+                        capture_output=True, text=True).stdout
+    exported = {line.split()[-1] for line in nm.splitlines() if " T " in line}
+    missing = _declared() - exported
+    assert not missing, f"not exported: {sorted(missing)}"
+    L = _capi.lib()
+    for name in _declared():
+        assert isinstance(getattr(L, name), ctypes._CFuncPtr)
+
+
+def test_no_oracle_or_torch_symbols_in_library() -> None:
+    """The product library is self-contained: it links neither the oracle nor torch."""
+    deps = subprocess.run(["readelf", "-d", str(_capi.LIB_PATH)], check=True,
+                          capture_output=True, text=True).stdout
+    assert "fp8_oracle" not in deps and "libtorch" not in deps and "libc10" not in deps
+    nm = subprocess.run(["nm", "-D", str(_capi.LIB_PATH)], check=True, capture_output=True,
+                        text=True).stdout
+    assert " or_" not in nm
+
+
+def test_version_and_status_strings() -> None:
+    L = _capi.lib()
+    assert L.rp_abi_version() == 1
+    assert L.rp_status_string(0) == b"ok"
+    assert L.rp_status_string(1) == b"invalid argument"
+    assert L.rp_status_string(2) == b"unsupported shape or layout"
+    assert L.rp_status_string(3) == b"workspace missing or too small"
+    assert L.rp_status_string(4) == b"kernel launch failed"
+    assert L.rp_status_string(99) == b"unknown status"
+
+
+def test_workspace_sizing_is_host_only() -> None:
+    L = _capi.lib()
+    small = L.rp_fp8_quant_workspace_bytes(1, 8, 1024, 64, _capi.RP_SCALE_PER_BH)
+    big = L.rp_fp8_quant_workspace_bytes(1, 40, 75600, 128, _capi.RP_SCALE_PER_BH)
+    assert 0 < small <= big < (64 << 20)
+    assert L.rp_fp8_quant_workspace_bytes(0, 8, 1024, 64, 0) == 0        # invalid -> 0
+
+
+def _attn(L, **kw) -> int:
+    a = dict(q8=FAKE, k8=FAKE, vt8=FAKE, ldv=128, qs=FAKE, ks=FAKE, vs=FAKE, stride=1,
+             sm=0.125, out=FAKE, odt=0, osb=8 * 128 * 128, osh=128 * 128, oss=128, B=1, H=8,
+             Sq=128, Skv=128, D=128, mask=0, prefix=0, suffix=1, stream=None)
+    a.update(kw)
+    return L.rp_fp8_attn_fwd(*a.values())
+
+
+@pytest.mark.parametrize("kw,status,msg", [
+    (dict(q8=None), 1, "null pointer"),
+    (dict(D=96), 2, "head dim"),
+    (dict(Sq=0), 1, "non-positive"),
+    (dict(ldv=100), 1, "ldv"),
+    (dict(mask=7), 1, "unknown mask"),
+    (dict(mask=2, suffix=0), 1, "shared-prefix"),
+    (dict(odt=5), 1, "out_dtype"),
+    (dict(stride=3), 1, "scale_stride"),
+    (dict(k8=FAKE + 8), 2, "aligned"),
+])
+def test_attention_argument_checks(kw: dict, status: int, msg: str) -> None:
+    L = _capi.lib()
+    assert _attn(L, **kw) == status
+    assert msg in L.rp_last_error().decode()
+
+
+@pytest.mark.parametrize("args,status,msg", [
+    ((None, FAKE, FAKE, 64, 64, 64, 64, 64, 64), 1, "null pointer"),
+    ((FAKE, FAKE, FAKE, 64, 64, 0, 64, 64, 64), 1, "bad sizes"),
+    ((FAKE, FAKE, FAKE, 64, 64, 40, 40, 40, 64), 2, "multiples of 16"),
+    ((FAKE, FAKE, FAKE + 4, 64, 64, 64, 64, 64, 64), 2, "aligned"),
+])
+def test_gemm_argument_checks(args: tuple, status: int, msg: str) -> None:
+    L = _capi.lib()
+    assert L.rp_fp8_gemm(*args, 1.0, 1.0, None, None, None) == status
+    assert msg in L.rp_last_error().decode()
+
+
+def test_quantizer_argument_checks() -> None:
+    L = _capi.lib()
+    assert L.rp_fp8_scale(None, 1, 1, 16, 64, 1024, 1024, 64, 0, FAKE, FAKE, 4096, None) == 1
+    assert L.rp_fp8_scale_quantize(FAKE, 1, 1, 16, 64, 1024, 1024, 64, 5, FAKE, FAKE, 0, 0,
+                                   FAKE, 4096, None) != 0

@@ -184,3 +184,63 @@ def test_wan_self_attention_full_shape_sampled_rows(gpu: torch.device) -> None:
 def test_wan_cross_attention_full_shape_sampled_rows(gpu: torch.device) -> None:
     """C3 cross (Skv = 512): 512 rows x 4 heads vs oracle."""
     _wan_sample(gpu, C3_CROSS, [0, 5, 20, 39], 512)
+
+
+# ----------------------------------------------------------------------------
+# The reference's own acceptance tests, re-expressed against this package's op
+# (tests/test_attention_fp8.py:102-154, tests/test_fp8_attention_ada.py:115-201).
+
+def _sdpa_case(gpu: torch.device, shape: tuple[int, int, int, int]):
+    torch.manual_seed(0)
+    q = torch.randn(*shape, device=gpu, dtype=torch.bfloat16) / 8.0
+    k = torch.randn(*shape, device=gpu, dtype=torch.bfloat16) / 8.0
+    v = torch.randn(*shape, device=gpu, dtype=torch.bfloat16)
+    return q, k, v
+
+
+def _rel_vs_sdpa(out: torch.Tensor, ref: torch.Tensor) -> float:
+    return ((out.float() - ref.float()).abs().mean() / ref.float().abs().mean()).item()
+
+
+@pytest.mark.parametrize("shape,causal,bound", [
+    ((1, 4, 256, 64), False, 0.15),      # test_attention_fp8.py:102-126
+    ((1, 4, 256, 64), True, 0.15),       # test_attention_fp8.py:129-154
+    ((1, 8, 4096, 128), False, 0.10),    # test_fp8_attention_ada.py:115-146
+    ((1, 8, 4096, 64), False, 0.10),     # test_fp8_attention_ada.py:149-172
+    ((1, 8, 4096, 128), True, 0.10),     # test_fp8_attention_ada.py:175-201
+])
+def test_op_matches_sdpa_like_the_reference(gpu: torch.device, shape: tuple, causal: bool,
+                                            bound: float) -> None:
+    from repercep_runtime_amd.attention import FP8HipAttention, NaiveAttention
+
+    op = FP8HipAttention()
+    assert op.available
+    q, k, v = _sdpa_case(gpu, shape)
+    ref = NaiveAttention()(q.float(), k.float(), v.float(), causal=causal)
+    out = op(q, k, v, causal=causal)
+    assert out.shape == ref.shape and out.dtype == torch.bfloat16
+    assert torch.isfinite(out).all()
+    rel = _rel_vs_sdpa(out, ref)
+    print(f"{shape} causal={causal}: mean rel vs SDPA {rel:.4f}", flush=True)
+    assert rel < bound
+
+
+def test_diffusers_bridge_runs_fp8_kernel_on_bshd(gpu: torch.device) -> None:
+    """(B, S, H, D) through the dispatcher bridge: FP8 branch taken, equal to
+    the op on permuted copies, close to SDPA."""
+    from repercep_runtime_amd.attention import diffusers_backend as db
+
+    g = torch.Generator(device=gpu).manual_seed(4)
+    q = torch.randn(1, 4096, 4, 128, device=gpu, generator=g).to(torch.bfloat16)
+    k = torch.randn(1, 4096, 4, 128, device=gpu, generator=g).to(torch.bfloat16)
+    v = torch.randn(1, 4096, 4, 128, device=gpu, generator=g).to(torch.bfloat16)
+    assert db._route_should_use_fp8(q, k, v)
+    out = db._repercep_fp8_attention(q, k, v)
+    via_op = ops.fp8_flash_attention(q.permute(0, 2, 1, 3).contiguous(),
+                                     k.permute(0, 2, 1, 3).contiguous(),
+                                     v.permute(0, 2, 1, 3).contiguous())
+    assert torch.equal(out, via_op.permute(0, 2, 1, 3))
+    ref = torch.nn.functional.scaled_dot_product_attention(
+        q.permute(0, 2, 1, 3).float(), k.permute(0, 2, 1, 3).float(),
+        v.permute(0, 2, 1, 3).float()).permute(0, 2, 1, 3)
+    assert _rel_vs_sdpa(out, ref) < 0.10
