@@ -126,7 +126,8 @@ int rp_fp8_attn_fwd(const uint8_t* q8, const uint8_t* k8, const uint8_t* vt8, in
  * a_scale_dev / b_scale_dev: optional device pointers to the fp32 scales
  * (e.g. produced by rp_fp8_scale with RP_SCALE_PER_TENSOR); when non-NULL
  * they are used instead of the host values, avoiding a device->host read.
- * K % 128 == 0; lda, ldb % 16 == 0. */
+ * K, lda, ldb multiples of 16; N, ldc multiples of 4; a8 and bt8 16-byte
+ * aligned, c 8-byte aligned. */
 int rp_fp8_gemm(const uint8_t* a8, const uint8_t* bt8, void* c,
                 int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldb, int64_t ldc,
                 float a_scale, float b_scale, const float* a_scale_dev,
