@@ -8,6 +8,7 @@ Flags:
   -Xclang -target-feature -Xclang -packed-fp32-ops
                                             no packed-FP32 VALU forms
   -mllvm -disable-promote-alloca-to-lds     keep per-thread staging in VGPRs
+  -Wno-inline-asm                           M0 in an inline-asm clobber list
 No fast-math anywhere: the quantizer's fp32 division and reciprocal must be
 correctly rounded (IEEE), which is hipcc's default.
 """
@@ -35,6 +36,8 @@ COMMON = [
     "-mllvm", "-disable-promote-alloca-to-lds",
     f"-I{ROOT / 'include'}",
     "-Wall", "-Wno-unused-function",
+    # the attention kernel's direct-to-LDS load is inline asm that sets M0
+    "-Wno-inline-asm",
 ]
 SOURCES = ["rp_api.hip", "rp_quant.hip", "rp_attn.hip", "rp_gemm.hip"]
 

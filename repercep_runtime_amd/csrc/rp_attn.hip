@@ -39,11 +39,15 @@
 // * Workgroup of 8 waves x 32 query rows, two waves per SIMD (<= 256 VGPRs
 //   each), in two groups of four that alternate between an MFMA phase and a
 //   softmax phase at every workgroup barrier, so that on each SIMD one
-//   wave's MFMAs overlap the other wave's softmax.  K tiles of 128 keys are
-//   double-buffered and V^T tiles triple-buffered in LDS, loaded with
-//   global_load_lds_dwordx4 (no VGPR staging); each LDS row carries one
-//   16-byte pad granule so every 16-lane ds_read_b128 group hits 16
-//   distinct bank groups.
+//   wave's MFMAs overlap the other wave's softmax.  A single wave issues
+//   VALU instructions at about one per 5 cycles (v_exp_f32 and
+//   v_cvt_pk_fp8_f32 one per 9), so the softmax phase, not the matrix core,
+//   sets the pace; the MFMA phase reads its LDS operands two MFMAs ahead so
+//   that it stays well inside the softmax phase's length.
+// * K tiles of 128 keys are double-buffered and V^T tiles triple-buffered
+//   in LDS, loaded by the four waves of group 0 with global_load_lds_dwordx4
+//   (no VGPR staging); each LDS row carries one 16-byte pad granule so every
+//   16-lane ds_read_b128 group hits 16 distinct bank groups.
 // * Grid: one workgroup per (head, query block), remapped so that the
 //   workgroups resident on one XCD (dispatch is round-robin over the 8
 //   XCDs) work on the same head and share its K/V through that XCD's L2.
@@ -129,11 +133,25 @@ __device__ __forceinline__ int key_of(int h, int rho) {
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 typedef __attribute__((address_space(1))) void* gbl_ptr_t;
 
-// 16 bytes global -> LDS without passing through VGPRs.  `lds_block` must be
-// wave-uniform: lane i lands at lds_block + 16*i.
-__device__ __forceinline__ void gload_lds16(const void* src, void* lds_block) {
-  __builtin_amdgcn_global_load_lds((gbl_ptr_t)src, (lds_ptr_t)lds_block, 16, 0, 0);
+// 16 bytes global -> LDS without passing through VGPRs.  `lds_block` (an LDS
+// byte address) must be wave-uniform: lane i lands at lds_block + 16*i.
+//
+// Written as inline asm on purpose.  The compiler books an LDS DMA as an
+// outstanding LDS event that can complete out of order, and then guards
+// every later ds_read with lgkmcnt(0) -- which serialises the operand reads
+// of the MFMA phase.  Hidden from it, the loads are waited for by the
+// explicit vmcnt(0) + workgroup barrier that precede every first read of a
+// tile.  M0 carries the LDS destination; nothing else in this kernel uses M0.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void gload_lds16(const void* src, uint32_t lds_block) {
+  const uint32_t base = __builtin_amdgcn_readfirstlane(lds_block);
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
+               :
+               : "v"(src), "s"(base)
+               : "memory", "m0");
 }
+#pragma clang diagnostic pop
 
 // Per-thread byte offsets of the direct-to-LDS loads of one (K, V^T) tile,
 // relative to the tile's first key.  Each wave instruction fills one
@@ -188,8 +206,8 @@ __device__ __forceinline__ TileOffsets<D, NW> tile_offsets(int64_t ldv, int wave
 // their scores are masked; V^T is zero-padded to ldv.
 template <int D, int NW>
 __device__ __forceinline__ void issue_tile(const AttnArgs& a, const uint8_t* kh, const uint8_t* vh,
-                                           const TileOffsets<D, NW>& o, int kb, uint8_t* kst,
-                                           uint8_t* vst, int wave) {
+                                           const TileOffsets<D, NW>& o, int kb, uint32_t kst,
+                                           uint32_t vst, int wave) {
   using G = Geo<D, NW>;
   const int kv0 = kb * kBlockN;
   const uint8_t* kt = kh + (int64_t)kv0 * D;
@@ -201,14 +219,14 @@ __device__ __forceinline__ void issue_tile(const AttnArgs& a, const uint8_t* kh,
       uint32_t off = o.k[n];
       if (tail && kv0 + o.k_key[n] >= a.Skv)
         off = off - (uint32_t)((kv0 + o.k_key[n] - (a.Skv - 1)) * D);
-      gload_lds16(kt + off, kst + blk * 1024);
+      gload_lds16(kt + off, kst + blk * 1024u);
     }
   }
   const uint8_t* vt = vh + kv0;
 #pragma unroll
   for (int n = 0; n < G::V_LOADS_MAX; ++n) {
     const int blk = n * NW + wave;
-    if (blk < G::V_BLKS) gload_lds16(vt + o.v[n], vst + blk * 1024);
+    if (blk < G::V_BLKS) gload_lds16(vt + o.v[n], vst + blk * 1024u);
   }
 }
 
@@ -220,6 +238,63 @@ __device__ __forceinline__ void wait_vmem_all() {
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
   const __bf16 a = (__bf16)lo, b = (__bf16)hi;  // v_cvt_pk_bf16_f32, round to nearest even
   return (uint32_t)__builtin_bit_cast(uint16_t, a) | ((uint32_t)__builtin_bit_cast(uint16_t, b) << 16);
+}
+
+// Two LDS reads (32 bytes per lane) of one MFMA operand.
+__device__ __forceinline__ i32x8 lds_op(const uint8_t* p) {
+  return cat8(*reinterpret_cast<const i32x4*>(p), *reinterpret_cast<const i32x4*>(p + 16));
+}
+
+// One MFMA phase: S^T = K(i) . Q^T (DO_S) and O^T += V^T(i-1) . P^T(i-1)
+// (DO_PV), as one stream of MFMAs whose operands are read from LDS through a
+// ring of kRing registers sets, kRing-1 MFMAs ahead of their use, so LDS
+// latency overlaps the matrix core instead of stalling it.  Consecutive
+// MFMAs write different accumulators (key tiles / head-dim tiles inner), so
+// none waits for its predecessor's result.
+constexpr int kRing = 3;
+
+template <int D, bool DO_S, bool DO_PV>
+__device__ __forceinline__ void mfma_phase(const uint8_t* kl, const uint8_t* vl,
+                                           const i32x8 (&qop)[D / 64], const i32x8 (&pop)[2],
+                                           f32x16 (&s)[4], f32x16 (&acc)[D / 32]) {
+  using G = Geo<D, 8>;
+  constexpr int NS = DO_S ? 4 * G::KSTEPS : 0;   // S^T steps: ks outer, key tile hh inner
+  constexpr int NP = DO_PV ? 2 * G::ETILES : 0;  // PV steps: k-half m outer, d tile e inner
+  constexpr int N = NS + NP;
+  auto addr = [&](int t) -> const uint8_t* {
+    if (t < NS) {
+      const int hh = t & 3, ks = t >> 2;
+      return kl + 32 * hh * G::K_PITCH + 64 * ks;
+    }
+    const int u = t - NS, e = u % G::ETILES, m = u / G::ETILES;
+    return vl + 32 * e * G::V_PITCH + 64 * m;
+  };
+  i32x8 ring[kRing];
+#pragma unroll
+  for (int t = 0; t < kRing - 1 && t < N; ++t) ring[t] = lds_op(addr(t));
+#pragma unroll
+  for (int t = 0; t < N; ++t) {
+    if (t + kRing - 1 < N) ring[(t + kRing - 1) % kRing] = lds_op(addr(t + kRing - 1));
+    const i32x8 op = ring[t % kRing];
+    if (t < NS) {
+      const int hh = t & 3, ks = t >> 2;
+      // the first k-step starts from the inline constant 0
+      s[hh] = mfma_32x32x64(op, qop[ks], ks == 0 ? f32x16{} : s[hh]);
+    } else {
+      const int u = t - NS, e = u % G::ETILES, m = u / G::ETILES;
+      acc[e] = mfma_32x32x64(op, pop[m], acc[e]);
+    }
+  }
+  // Pin that order for the machine scheduler, which would otherwise sink
+  // every read next to its MFMA to save registers: the first kRing-1
+  // operands' reads, then per step one MFMA followed by the reads of the
+  // operand kRing-1 steps ahead.
+  __builtin_amdgcn_sched_group_barrier(0x100, 2 * (kRing - 1), 0);
+#pragma unroll
+  for (int t = 0; t < N; ++t) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    if (t + kRing - 1 < N) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+  }
 }
 
 // Eight waves per workgroup in two groups of four; waves w and w+4 share a
@@ -237,9 +312,11 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
 // Numbering the workgroup barriers from the prologue's (0), group 0 runs
 // MFMA(j) between barriers 2j and 2j+1 and group 1 between 2j+1 and 2j+2.
 // Tile j (K(j), V^T(j)) overwrites K(j-2) and V^T(j-3), whose last reads end
-// at barrier 2j-2, and is first read right after barrier 2j; so every wave
-// issues its share of tile j after barrier 2j-2 and waits for it
-// (s_waitcnt vmcnt(0)) before barrier 2j.
+// at barrier 2j-2, and is first read right after barrier 2j; so group 0's
+// waves issue tile j after barrier 2j-2 and wait for it (s_waitcnt vmcnt(0))
+// before barrier 2j.  Only group 0 loads: the slot in which a group issues
+// loads costs its SIMD VALU time, and in this slot the MFMA group, not the
+// softmax group, has VALU time to spare.
 template <int D, bool OUT_F32>
 __global__ __launch_bounds__(512, 1)
 void attn_fwd_kernel(AttnArgs a) {
@@ -250,6 +327,9 @@ void attn_fwd_kernel(AttnArgs a) {
   __shared__ __attribute__((aligned(1024))) uint8_t smem[G::LDS_BYTES];
   uint8_t* const kbuf = smem;                              // K_STAGES x K_BYTES
   uint8_t* const vbuf = smem + G::K_STAGES * G::K_BYTES;   // V_STAGES x V_BYTES
+  // the same two regions as LDS byte addresses, for the direct-to-LDS loads
+  const uint32_t kbuf_lds = (uint32_t)(uintptr_t)(lds_ptr_t)smem;
+  const uint32_t vbuf_lds = kbuf_lds + G::K_STAGES * G::K_BYTES;
 
   // ---- work item (XCD-aware remap of the linear workgroup id)
   const int w = blockIdx.x;
@@ -288,8 +368,15 @@ void attn_fwd_kernel(AttnArgs a) {
     n_kb = min(n_kb, q_last / kBlockN + 1);
   }
 
-  const TileOffsets<D, NW> toff = tile_offsets<D, NW>(a.ldv, wave, lane);
-  issue_tile<D, NW>(a, kh, vh, toff, 0, kbuf, vbuf, wave);
+  // Group 0's four waves issue every tile (see the schedule below); their
+  // per-lane load offsets are fixed for the whole kernel.
+  constexpr int NL = 4;
+  const TileOffsets<D, NL> toff = tile_offsets<D, NL>(a.ldv, wave & 3, lane);
+  if (group == 0) issue_tile<D, NL>(a, kh, vh, toff, 0, kbuf_lds, vbuf_lds, wave);
+  // V^T stage 2 is read (times P = 0) by the first MFMA phase before tile 2
+  // lands there: clear it so that no stale NaN code can reach the accumulator.
+  for (int o = tid * 16; o < G::V_BYTES; o += G::THREADS * 16)
+    *reinterpret_cast<i32x4*>(vbuf + 2 * G::V_BYTES + o) = i32x4{0, 0, 0, 0};
 
   // ---- Q^T operand (B operand of S^T), resident for the whole kernel
   i32x8 qop[G::KSTEPS];
@@ -313,56 +400,24 @@ void attn_fwd_kernel(AttnArgs a) {
 
   wait_vmem_all();
   __syncthreads();
-  if (group == 1) {  // group 1 starts half a step behind
-    if (n_kb > 1)
-      issue_tile<D, NW>(a, kh, vh, toff, 1, kbuf + G::K_BYTES, vbuf + G::V_BYTES, wave);
-    __syncthreads();
-  }
+  if (group == 1) __syncthreads();  // group 1 starts half a step behind
 
   for (int i = 0; i <= n_kb; ++i) {
     // ================= MFMA(i) =================
-    // Tile j is issued by every wave right after workgroup barrier 2j-2 and
-    // waited for before barrier 2j (the prologue's barrier is number 0):
-    // group 0 issues at the start of MFMA(j-1) and waits at the end of
-    // SOFTMAX(j-1); group 1 issues at the start of SOFTMAX(j-2) and waits at
-    // the end of MFMA(j-1).
+    // Tile j is issued by group 0 at the start of MFMA(j-1), right after
+    // workgroup barrier 2j-2, and waited for at the end of SOFTMAX(j-1),
+    // before barrier 2j (the prologue's barrier is number 0).
     if (group == 0 && i + 1 < n_kb)
-      issue_tile<D, NW>(a, kh, vh, toff, i + 1, kbuf + ((i + 1) & 1) * G::K_BYTES,
-                        vbuf + ((i + 1) % 3) * G::V_BYTES, wave);
-    if (i < n_kb) {
-      const uint8_t* kl = kbuf + (i & 1) * G::K_BYTES + k_base;
-#pragma unroll
-      for (int hh = 0; hh < 4; ++hh) {
-#pragma unroll
-        for (int ks = 0; ks < G::KSTEPS; ++ks) {
-          const uint8_t* p = kl + 32 * hh * G::K_PITCH + 64 * ks;
-          const i32x8 kop = cat8(*reinterpret_cast<const i32x4*>(p),
-                                 *reinterpret_cast<const i32x4*>(p + 16));
-          // first k-step starts from the inline constant 0 (no zeroed registers)
-          s[hh] = mfma_32x32x64(kop, qop[ks], ks == 0 ? f32x16{} : s[hh]);
-        }
-      }
-    }
-    if (i > 0) {
-      const uint8_t* vl = vbuf + ((i - 1) % 3) * G::V_BYTES + v_base;
-#pragma unroll
-      for (int e = 0; e < G::ETILES; ++e) {
-#pragma unroll
-        for (int m = 0; m < 2; ++m) {
-          const uint8_t* p = vl + 32 * e * G::V_PITCH + 64 * m;
-          const i32x8 vop = cat8(*reinterpret_cast<const i32x4*>(p),
-                                 *reinterpret_cast<const i32x4*>(p + 16));
-          acc[e] = mfma_32x32x64(vop, pop[m], acc[e]);
-        }
-      }
-    }
-    if (group == 1) wait_vmem_all();
+      issue_tile<D, NL>(a, kh, vh, toff, i + 1, kbuf_lds + ((i + 1) & 1) * G::K_BYTES,
+                        vbuf_lds + ((i + 1) % 3) * G::V_BYTES, wave);
+    // Every MFMA phase runs both products: in the first one P is zero and
+    // V^T stage 2 holds zeros (cleared in the prologue), in the last one the
+    // S^T result is never used.
+    mfma_phase<D, true, true>(kbuf + (i & 1) * G::K_BYTES + k_base,
+                              vbuf + ((i + 2) % 3) * G::V_BYTES + v_base, qop, pop, s, acc);
     __syncthreads();
 
     // ================= SOFTMAX(i) =================
-    if (group == 1 && i + 2 < n_kb)
-      issue_tile<D, NW>(a, kh, vh, toff, i + 2, kbuf + ((i + 2) & 1) * G::K_BYTES,
-                        vbuf + ((i + 2) % 3) * G::V_BYTES, wave);
     if (i < n_kb) {
       const int kv0 = i * kBlockN;
       bool need_mask = kv0 + kBlockN > a.Skv;
