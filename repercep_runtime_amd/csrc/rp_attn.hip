@@ -153,11 +153,6 @@ __device__ __forceinline__ void gload_lds16(const void* src, uint32_t lds_block)
 }
 #pragma clang diagnostic pop
 
-// Per-thread byte offsets of the direct-to-LDS loads of one (K, V^T) tile,
-// relative to the tile's first key.  Each wave instruction fills one
-// contiguous KiB of LDS, so the XOR swizzle is applied on the global side:
-// the lane that lands on physical chunk `phys` of row r fetches logical chunk
-// phys ^ swz(r).
 // Combine a lane's value with lane l^32's (the other half of the wave)
 // through v_permlane32_swap -- a VALU op, no LDS round trip.
 __device__ __forceinline__ float xhalf_max(float x) {
@@ -305,9 +300,10 @@ __device__ __forceinline__ void mfma_phase(const uint8_t* kl, const uint8_t* vl,
 //   slot 2i   : group 0  MFMA(i)        group 1  SOFTMAX(i-1)
 //   slot 2i+1 : group 0  SOFTMAX(i)     group 1  MFMA(i)
 //
-//   MFMA(i)    = S^T(i) = K(i) . Q^T   and   O^T += V^T(i-1) . P^T(i-1)
-//   SOFTMAX(i) = mask, running max, P(i) = e4m3(p * 448), row sums,
-//                O^T *= alpha(i)  (after the P(i-1) contribution, before P(i)'s)
+//   MFMA(i)    = S^T(i) = K(i) . Q^T   and   O^T += V^T(i-1) . P^T(i-1),
+//                then, on the VALU while those drain: mask, running max and
+//                alpha(i) of tile i, O^T *= alpha(i)
+//   SOFTMAX(i) = P(i) = e4m3(p * 448) and the row sums
 //
 // Numbering the workgroup barriers from the prologue's (0), group 0 runs
 // MFMA(j) between barriers 2j and 2j+1 and group 1 between 2j+1 and 2j+2.
@@ -402,6 +398,7 @@ void attn_fwd_kernel(AttnArgs a) {
   __syncthreads();
   if (group == 1) __syncthreads();  // group 1 starts half a step behind
 
+  float alpha = 1.0f, moff = 0.0f;  // of the tile whose softmax comes next
   for (int i = 0; i <= n_kb; ++i) {
     // ================= MFMA(i) =================
     // Tile j is issued by group 0 at the start of MFMA(j-1), right after
@@ -415,9 +412,11 @@ void attn_fwd_kernel(AttnArgs a) {
     // S^T result is never used.
     mfma_phase<D, true, true>(kbuf + (i & 1) * G::K_BYTES + k_base,
                               vbuf + ((i + 2) % 3) * G::V_BYTES + v_base, qop, pop, s, acc);
-    __syncthreads();
-
-    // ================= SOFTMAX(i) =================
+    // The rest of the MFMA phase is softmax work that the VALU of this wave
+    // can do while its MFMAs drain (the softmax phase of the other wave on
+    // the SIMD is the critical path): mask, row max and alpha of tile i once
+    // S^T(i) has landed, then O^T *= alpha(i) once O^T += V^T(i-1) . P^T(i-1)
+    // has landed.
     if (i < n_kb) {
       const int kv0 = i * kBlockN;
       bool need_mask = kv0 + kBlockN > a.Skv;
@@ -457,11 +456,20 @@ void attn_fwd_kernel(AttnArgs a) {
       }
       float mx = max3f(mt[0], mt[1], max3f(mt[2], mt[3], mt[3]));
       mx = xhalf_max(mx);
-      const float m_new = __builtin_fmaxf(m_run, mx * c2);
+      const float m_new = max3f(m_run, mx * c2, mx * c2);
       const float m_use = (m_new == -__builtin_inff()) ? 0.0f : m_new;
-      const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
+      alpha = __builtin_amdgcn_exp2f(m_run - m_use);
       m_run = m_new;
-      const float moff = m_use - kLog2PMax;
+      moff = m_use - kLog2PMax;
+      if (__any(alpha != 1.0f)) {
+#pragma unroll
+        for (int e = 0; e < G::ETILES; ++e) acc[e] *= alpha;
+      }
+    }
+    __syncthreads();
+
+    // ================= SOFTMAX(i) =================
+    if (i < n_kb) {
       float ps[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
       for (int m = 0; m < 2; ++m) {
@@ -480,10 +488,6 @@ void attn_fwd_kernel(AttnArgs a) {
         pop[m] = i32x8{pw[0], pw[1], pw[2], pw[3], pw[4], pw[5], pw[6], pw[7]};
       }
       l_run = l_run * alpha + ((ps[0] + ps[1]) + (ps[2] + ps[3]));
-      if (__any(alpha != 1.0f)) {
-#pragma unroll
-        for (int e = 0; e < G::ETILES; ++e) acc[e] *= alpha;
-      }
     }
     if (group == 0) wait_vmem_all();
     __syncthreads();
