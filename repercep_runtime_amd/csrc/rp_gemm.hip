@@ -4,19 +4,22 @@
 // (fp32 accumulation, the product of the two scales applied once to the
 // accumulator, round-to-nearest-even bf16 output), on OCP e4m3fn operands.
 // The reference kernel is one wave per 16x16 tile with strided operand
-// gathers and no LDS; this one is an LDS-staged, double-buffered block GEMM
-// on v_mfma_f32_16x16x128_f8f6f4:
+// gathers and no LDS.  Here both operands are K-contiguous rows (A8 (M, K),
+// B8 transposed (N, K)), so every MFMA operand is 32 contiguous bytes per
+// lane, and the MFMA computes C^T tiles (A operand = rows of B^T, B operand
+// = rows of A): the accumulator gives each lane 4 consecutive output columns
+// of one row, stored as one 8-byte write.  Two kernels:
 //
-// * Both operands are K-contiguous rows (A8 (M, K), B8 transposed (N, K)),
-//   so every MFMA operand is 32 contiguous bytes per lane.
-// * The MFMA computes C^T tiles (A operand = rows of B^T, B operand = rows of
-//   A): the accumulator then gives each lane 4 consecutive output columns
-//   of one row, stored as one 8-byte write.
-// * Workgroup = 4 waves in a 2 x 2 grid over a BM x BN block tile; each
-//   K step of 128 stages BM + BN rows of 128 bytes in LDS (XOR-swizzled
-//   16-byte chunks) while the next step is fetched into registers.
-// * Workgroups are remapped so those resident on one XCD cover a compact
-//   patch of C and share operand rows in that XCD's L2.
+// * gemm256_kernel (K a multiple of 64, the production shapes): 256 x 256
+//   block tiles on v_mfma_f32_32x32x64_f8f6f4, four waves of 128 x 128 with
+//   their accumulators in AGPRs, operands streamed into a 4-stage LDS ring
+//   by direct-to-LDS loads three K slices ahead.
+// * gemm_kernel (any K multiple of 16): 256 x 128 block tiles on
+//   v_mfma_f32_16x16x128_f8f6f4, operands staged through VGPRs into a
+//   double-buffered, XOR-swizzled LDS tile, K tail zero-filled.
+//
+// Both remap workgroups so that those resident on one XCD cover a compact
+// patch of C and share operand rows in that XCD's L2.
 
 #include "rp_common.h"
 
@@ -187,6 +190,228 @@ void gemm_kernel(GemmArgs g) {
   }
 }
 
+
+// ------------------------------------------------------------- large tiles
+// The kernel for K a multiple of 64: 256 x 256 block tiles on
+// v_mfma_f32_32x32x64_f8f6f4, four waves (one per SIMD) of 128 x 128 each,
+// accumulators in AGPRs.  Operands reach LDS by global_load_lds_dwordx4 (no
+// VGPR staging) through a ring of kG2Stages K slices of 64 bytes, issued
+// three slices ahead; each LDS row carries a 16-byte pad granule so the
+// 16-lane ds_read_b128 groups are conflict-free.  The MFMA computes C^T
+// tiles (A operand = rows of B^T, B operand = rows of A), so each lane ends
+// with 4 consecutive output columns of one row per register group: one
+// 8-byte bf16 store.
+constexpr int kG2Threads = 256;
+constexpr int kG2Tile = 256;                        // BM = BN
+constexpr int kG2K = 64;                            // K bytes per slice = MFMA depth
+constexpr int kG2Pitch = kG2K + 16;                 // LDS row pitch
+constexpr int kG2Gran = kG2Pitch / 16;              // 16-byte granules per row (odd)
+constexpr int kG2Half = kG2Tile * kG2Pitch;         // A (or B^T) part of a stage
+constexpr int kG2Stage = 2 * kG2Half;
+constexpr int kG2Stages = 4;
+constexpr int kG2Ahead = kG2Stages - 1;             // slices in flight
+constexpr int kG2Loads = kG2Stage / 1024 / 4;       // 1 KiB loads per wave per slice
+constexpr int kG2ALoads = kG2Half / 1024 / 4;       // of which A
+static_assert(kG2Half % 4096 == 0, "A and B^T parts split evenly over the waves");
+static_assert(kG2Stages * kG2Stage <= 160 * 1024, "LDS");
+
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+// 16 bytes global -> LDS (lane i lands at lds_block + 16*i; lds_block
+// wave-uniform).  Inline asm keeps the load out of the compiler's waitcnt
+// bookkeeping, which would otherwise order every later ds_read behind it;
+// the kernel waits for its loads explicitly (vmcnt) before the barrier that
+// precedes their first read.  Nothing else in this kernel uses M0.
+__device__ __forceinline__ void g2_gload_lds16(const void* src, uint32_t lds_block) {
+  const uint32_t base = __builtin_amdgcn_readfirstlane(lds_block);
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
+               :
+               : "v"(src), "s"(base)
+               : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+// s_waitcnt vmcnt(N): all but this wave's N most recent loads have landed.
+template <int N>
+__device__ __forceinline__ void g2_wait_vmem() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
+__device__ __forceinline__ f32x16 mfma_32x32x64(const i32x8& a, const i32x8& b, const f32x16& c) {
+  return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, 0, 0, 0, 0, 0, 0);
+}
+
+__device__ __forceinline__ i32x8 g2_op(const uint8_t* p) {
+  return cat8(*reinterpret_cast<const i32x4*>(p), *reinterpret_cast<const i32x4*>(p + 16));
+}
+
+// two fp32 -> packed bf16 with v_cvt_pk_bf16_f32 (round to nearest even)
+__device__ __forceinline__ uint32_t g2_pack_bf16(float lo, float hi) {
+  const __bf16 a = (__bf16)lo, b = (__bf16)hi;
+  return (uint32_t)__builtin_bit_cast(uint16_t, a) | ((uint32_t)__builtin_bit_cast(uint16_t, b) << 16);
+}
+
+struct G2Ops {
+  i32x8 a[4], b[4];
+};
+
+__global__ __launch_bounds__(kG2Threads) __attribute__((amdgpu_waves_per_eu(1, 1)))
+void gemm256_kernel(GemmArgs g) {
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[kG2Stages * kG2Stage];
+  const uint32_t smem_lds = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)smem;
+
+  // XCD-aware remap, then a column-major walk over 8-tile-tall bands of C
+  // so that workgroups resident together share B^T rows (and A rows across
+  // neighbouring bands) in L2.
+  const int nwork = g.tiles_m * g.tiles_n;
+  const int w = blockIdx.x;
+  const int per = nwork >> 3, rem = nwork & 7;
+  const int xcd = w & 7;
+  const int L = xcd * per + min(xcd, rem) + (w >> 3);
+  constexpr int kBand = 8;
+  const int band_tiles = kBand * g.tiles_n;
+  const int band = L / band_tiles;
+  const int in_band = L - band * band_tiles;
+  const int band_h = min(kBand, g.tiles_m - band * kBand);
+  const int tm = band * kBand + in_band % band_h;
+  const int tn = in_band / band_h;
+  const int64_t m0 = (int64_t)tm * kG2Tile;
+  const int64_t n0 = (int64_t)tn * kG2Tile;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lq = lane & 31, lg = lane >> 5;
+  const int wm = wave >> 1, wn = wave & 1;
+
+  // this lane's direct-to-LDS loads: load n fills LDS KiB block n*4 + wave
+  // of a stage; blocks [0, kG2Half/1024) hold A rows, the rest B^T rows.
+  // Rows past M or N re-read the last row (their results are not stored).
+  const uint8_t* abase = g.a + m0 * g.lda;
+  const uint8_t* bbase = g.bt + n0 * g.ldb;
+  uint32_t gofs[kG2Loads];
+#pragma unroll
+  for (int n = 0; n < kG2Loads; ++n) {
+    const int blk = n * 4 + wave;
+    const bool is_a = n < kG2ALoads;
+    const int p = (is_a ? blk : blk - kG2Half / 1024) * kWave + lane;
+    const int row = p / kG2Gran, slot = p % kG2Gran;
+    const int s16 = (slot < kG2K / 16 ? slot : 0) * 16;
+    if (is_a) {
+      const int64_t r = min(m0 + row, g.M - 1) - m0;
+      gofs[n] = (uint32_t)(r * g.lda + s16);
+    } else {
+      const int64_t r = min(n0 + row, g.N - 1) - n0;
+      gofs[n] = (uint32_t)(r * g.ldb + s16);
+    }
+  }
+  const int nk = (int)(g.K / kG2K);
+  // load n of slice kk (slices past the end are not issued)
+  auto issue = [&](int n, int kk) __attribute__((always_inline)) {
+    const uint8_t* src = (n < kG2ALoads ? abase : bbase) + (int64_t)kk * kG2K + gofs[n];
+    g2_gload_lds16(src, smem_lds + (uint32_t)((kk % kG2Stages) * kG2Stage + (n * 4 + wave) * 1024));
+  };
+  // wait until slice kk has landed, with the slices after it (up to
+  // kG2Ahead - 1 of them, issued since) still in flight
+  auto wait_slice = [&](int kk) __attribute__((always_inline)) {
+    const int later = min(kG2Ahead - 1, nk - 1 - kk);
+    if (later >= 2) g2_wait_vmem<2 * kG2Loads>();
+    else if (later == 1) g2_wait_vmem<kG2Loads>();
+    else g2_wait_vmem<0>();
+  };
+
+  // per-lane operand offsets inside a stage
+  const int a_off = (wm * 128 + lq) * kG2Pitch + 32 * lg;
+  const int b_off = kG2Half + (wn * 128 + lq) * kG2Pitch + 32 * lg;
+  auto read_ops = [&](G2Ops& o, int kk) __attribute__((always_inline)) {
+    const uint8_t* st = smem + (kk % kG2Stages) * kG2Stage;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) o.a[i] = g2_op(st + a_off + 32 * i * kG2Pitch);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) o.b[j] = g2_op(st + b_off + 32 * j * kG2Pitch);
+  };
+
+  f32x16 acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = f32x16{};
+
+  for (int s = 0; s < kG2Ahead; ++s)
+    if (s < nk) {
+#pragma unroll
+      for (int n = 0; n < kG2Loads; ++n) issue(n, s);
+    }
+  wait_slice(0);
+  __syncthreads();
+
+  // One slice: 16 MFMAs on `cur`; the loads of slice kk+3 go out between
+  // them; after the 12th MFMA the wave waits for slice kk+1 and meets the
+  // others at the barrier, then reads slice kk+1's operands into `nxt` while
+  // its last four MFMAs run.  Slice kk+3 overwrites the stage of slice kk-1,
+  // whose reads all finished before the previous iteration's barrier.
+  auto step = [&](int kk, G2Ops& cur, G2Ops& nxt) __attribute__((always_inline)) {
+    const bool load = kk + kG2Ahead < nk;
+#pragma unroll
+    for (int t = 0; t < 16; ++t) {
+      const int i = t >> 2, j = t & 3;
+      acc[i][j] = mfma_32x32x64(cur.b[j], cur.a[i], acc[i][j]);
+      if (t < kG2Loads && load) issue(t, kk + kG2Ahead);
+      if (t == 11) {
+        if (kk + 1 < nk) wait_slice(kk + 1);
+        __syncthreads();
+        if (kk + 1 < nk) read_ops(nxt, kk + 1);
+      }
+    }
+  };
+  G2Ops o0, o1;
+  read_ops(o0, 0);
+  int kk = 0;
+  for (; kk + 1 < nk; kk += 2) {
+    step(kk, o0, o1);
+    step(kk + 1, o1, o0);
+  }
+  if (kk < nk) step(kk, o0, o1);
+
+  // epilogue: C[m][n] = bf16(acc * a_scale * b_scale)
+  const float scale = (g.a_dev ? *g.a_dev : g.a_scale) * (g.b_dev ? *g.b_dev : g.b_scale);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int64_t m = m0 + wm * 128 + 32 * i + lq;
+    if (m >= g.M) continue;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int64_t n = n0 + wn * 128 + 32 * j + 8 * q + 4 * lg;
+        if (n >= g.N) continue;
+        const f32x16& v = acc[i][j];
+        uint2 pk;
+        pk.x = g2_pack_bf16(v[4 * q + 0] * scale, v[4 * q + 1] * scale);
+        pk.y = g2_pack_bf16(v[4 * q + 2] * scale, v[4 * q + 3] * scale);
+        *reinterpret_cast<uint2*>(g.c + m * g.ldc + n) = pk;
+      }
+  }
+}
+
+int launch_gemm256(GemmArgs g, hipStream_t st) {
+  g.tiles_m = (int)((g.M + kG2Tile - 1) / kG2Tile);
+  g.tiles_n = (int)((g.N + kG2Tile - 1) / kG2Tile);
+  const int64_t nwork = (int64_t)g.tiles_m * g.tiles_n;
+  if (nwork > 0x7fffffff) {
+    rp_set_error("gemm: grid too large");
+    return RP_ERR_UNSUPPORTED;
+  }
+  hipLaunchKernelGGL(gemm256_kernel, dim3((unsigned)nwork), dim3(kG2Threads), 0, st, g);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) {
+    rp_set_error("gemm: launch failed: %s", hipGetErrorString(e));
+    return RP_ERR_LAUNCH;
+  }
+  return RP_OK;
+}
+
 // 64 x 64 byte-tile transpose through LDS.
 __global__ __launch_bounds__(256) void transpose_u8_kernel(const uint8_t* src, uint8_t* dst,
                                                            int64_t R, int64_t C, int64_t lds,
@@ -254,6 +479,11 @@ extern "C" int rp_fp8_gemm(const uint8_t* a8, const uint8_t* bt8, void* c, int64
   g.a = a8; g.bt = bt8; g.c = static_cast<uint16_t*>(c);
   g.M = M; g.N = N; g.K = K; g.lda = lda; g.ldb = ldb; g.ldc = ldc;
   g.a_scale = a_scale; g.b_scale = b_scale; g.a_dev = a_scale_dev; g.b_dev = b_scale_dev;
+  // the large-tile kernel reads whole 64-byte K slices and keeps tile
+  // offsets in 32 bits
+  if (K % kG2K == 0 && lda * (int64_t)kG2Tile < (int64_t)1 << 32 &&
+      ldb * (int64_t)kG2Tile < (int64_t)1 << 32)
+    return launch_gemm256(g, static_cast<hipStream_t>(stream));
   return launch_gemm<256, 128>(g, static_cast<hipStream_t>(stream));
 }
 

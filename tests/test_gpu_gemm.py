@@ -1,5 +1,8 @@
 """GPU parity of the FP8 scaled GEMM.
 
+Shapes with K a multiple of 64 run the large-tile kernel (one to nine 64-deep
+K slices, ragged M and N); K = 48 and K = 16 run the general kernel.
+
 Reference: kernels/hip/fp8_attn/fp8_gemm.hip:79-179 and its known-answer
 tests tests/test_mfma_fragment_layout.py:262-315 (restated here for the
 OCP e4m3fn format): all-ones -> every C == K, and small integers in [-2, 2]
@@ -21,17 +24,32 @@ from tests._helpers import bf16_bits, bf16_to_f32, bf16_ulp, codes_np, err_stats
 pytestmark = pytest.mark.gpu
 
 
+def _bf16_rne(x: np.ndarray) -> np.ndarray:
+    """float64 -> nearest bf16 value (via fp32, round to nearest even), as float64."""
+    f = np.asarray(x, dtype=np.float32)
+    return bf16_to_f32(np.asarray(torch.from_numpy(f).to(torch.bfloat16).view(torch.int16)
+                                  .numpy().view(np.uint16))).astype(np.float64)
+
+
 def _assert_one_rounding_apart(got: np.ndarray, ref: np.ndarray, a8: np.ndarray,
                                bt8: np.ndarray, scale: float) -> None:
-    """The kernel and the oracle agree up to the fp32 accumulation order: within one
-    bf16 ulp of the output plus a bound on the order-dependent fp32 rounding
-    (2^-16 of sum |a||b|, K <= 2^14).  Also reports BASELINE's error metrics."""
+    """Every kernel output is the bf16 rounding of some value within eps of the exact
+    scaled dot product, eps = 2^-14 * sum |a||b| * scale.  The f8f6f4 MFMA's dot
+    product is not an exactly rounded fp32 sum (measured: up to 2^-15.5 of
+    sum |a||b| away from it, identically for the 16x16x128 and 32x32x64 forms),
+    so a result may round to the bf16 neighbour of the oracle's.  Also reports
+    BASELINE's error metrics against the oracle (exact sum rounded once)."""
     st = err_stats(got, ref)
-    absab = np.abs(DECODE[a8].astype(np.float64)) @ np.abs(DECODE[bt8].astype(np.float64)).T
-    tol = bf16_ulp(np.maximum(np.abs(got), np.abs(ref))) + 2.0 ** -16 * absab * abs(scale)
-    bad = np.abs(got.astype(np.float64) - ref) > tol
-    print(st, "elements beyond one rounding:", int(bad.sum()), flush=True)
-    assert not bad.any(), f"{int(bad.sum())} elements differ by more than one rounding"
+    A = DECODE[a8].astype(np.float64)
+    Bt = DECODE[bt8].astype(np.float64)
+    exact = (A @ Bt.T) * float(np.float32(scale))
+    eps = 2.0 ** -14 * (np.abs(A) @ np.abs(Bt).T) * abs(scale)
+    lo = _bf16_rne(exact - eps)
+    hi = _bf16_rne(exact + eps)
+    g = got.astype(np.float64)
+    bad = (g < np.minimum(lo, hi)) | (g > np.maximum(lo, hi))
+    print(st, "outputs outside the rounding interval:", int(bad.sum()), flush=True)
+    assert not bad.any(), f"{int(bad.sum())} outputs are not a rounding of a value near the exact sum"
     assert st["rel_mean"] <= 1e-3
 
 
@@ -54,7 +72,8 @@ def test_small_integers_exact(gpu: torch.device, mnk: tuple[int, int, int]) -> N
     assert torch.equal(got, ref), f"max abs diff {(got - ref).abs().max().item()}"
 
 
-@pytest.mark.parametrize("mnk", [(257, 130 * 4, 384), (1000, 64, 512), (64, 1024, 1024)])
+@pytest.mark.parametrize("mnk", [(257, 130 * 4, 384), (1000, 64, 512), (64, 1024, 1024),
+                                 (600, 520, 192), (300, 300, 64), (2, 8, 576), (513, 260, 48)])
 def test_random_vs_oracle(gpu: torch.device, mnk: tuple[int, int, int]) -> None:
     M, N, K = mnk
     g = torch.Generator().manual_seed(M + N + K)
