@@ -10,13 +10,15 @@
 // tiny per-group finalize: 2 B/element to find the maximum, 2 B read + 1 B
 // written to quantize -- 5 B/element, the algorithmic minimum.
 //
-// Pass 1 (amax_partial): each 256-thread block reduces a contiguous slab of
-//   one group with packed 16-bit integer max over |x| bit patterns (exact
-//   and order-free; NaN patterns sort above +inf, so NaN propagates like
-//   torch.amax) and writes one partial per block -- no atomics, no memset.
+// Pass 1 (amax_flat / amax_partial): each 256-thread block reduces a
+//   32 KiB slab of one group with packed 16-bit integer max over |x| bit
+//   patterns (exact and order-free; NaN patterns sort above +inf, so NaN
+//   propagates like torch.amax) and writes one partial per block -- no
+//   atomics, no memset.  The _flat kernels serve contiguous tensors and issue
+//   all eight of a thread's 16-byte loads before using any.
 // Pass 2 (scale_finalize): one block per group folds its partials and forms
 //   the dequant scale.
-// Pass 3 (apply / apply_t): re-reads x, multiplies by the correctly rounded
+// Pass 3 (quant_flat / quant_apply / apply_t): re-reads x, multiplies by the correctly rounded
 //   fp32 reciprocal and converts with the gfx950 v_cvt_pk_fp8_f32.
 //   apply_t writes V transposed per head (D rows of ld codes), which is the
 //   layout the attention kernel's P.V MFMA reads K-contiguous.
@@ -135,6 +137,79 @@ __device__ __forceinline__ uint32_t quant4(uint32_t lo_pair, uint32_t hi_pair, f
   return pack4_e4m3(a, b, c, d);
 }
 
+
+// Contiguous (B, H, S, D) input: group g is the flat element range
+// [g*gsize, (g+1)*gsize).  Each block takes kElemsPerBlock elements of one
+// group; each thread issues all of its kFlatLoads 16-byte loads before using
+// any of them, so every wave keeps 8 loads in flight.
+constexpr int kFlatLoads = kElemsPerBlock / 8 / kQThreads;  // 16-byte loads per thread
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+__global__ __launch_bounds__(kQThreads) void amax_flat_kernel(const uint16_t* x, int64_t gsize,
+                                                              int64_t nbg, uint32_t* partial) {
+  const int64_t blk = blockIdx.x;
+  const int64_t g = blk / nbg;
+  const int64_t j = blk - g * nbg;
+  const int64_t start = g * gsize + j * kElemsPerBlock;
+  const int64_t n8 = (min((int64_t)kElemsPerBlock, gsize - j * kElemsPerBlock)) / 8;
+  const u32x4* src = reinterpret_cast<const u32x4*>(x + start);
+  u32x4 v[kFlatLoads];
+#pragma unroll
+  for (int i = 0; i < kFlatLoads; ++i) {
+    const int64_t idx = (int64_t)i * kQThreads + threadIdx.x;
+    v[i] = idx < n8 ? __builtin_nontemporal_load(src + idx) : u32x4{0u, 0u, 0u, 0u};
+  }
+  uint32_t m = 0;
+#pragma unroll
+  for (int i = 0; i < kFlatLoads; ++i) {
+    m = pk_umax16(m, v[i][0] & 0x7fff7fffu);
+    m = pk_umax16(m, v[i][1] & 0x7fff7fffu);
+    m = pk_umax16(m, v[i][2] & 0x7fff7fffu);
+    m = pk_umax16(m, v[i][3] & 0x7fff7fffu);
+  }
+  uint32_t m16 = umax32(m & 0xffffu, m >> 16);
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) m16 = umax32(m16, (uint32_t)shfl_xor((int)m16, o));
+  __shared__ uint32_t wmax[kQThreads / kWave];
+  if ((threadIdx.x & (kWave - 1)) == 0) wmax[threadIdx.x / kWave] = m16;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    uint32_t r = wmax[0];
+#pragma unroll
+    for (int w = 1; w < kQThreads / kWave; ++w) r = umax32(r, wmax[w]);
+    partial[blk] = r;
+  }
+}
+
+__global__ __launch_bounds__(kQThreads) void quant_flat_kernel(const uint16_t* x, int64_t gsize,
+                                                               int64_t nbg, const float* dequant,
+                                                               int per_bh, uint8_t* codes) {
+  const int64_t blk = blockIdx.x;
+  const int64_t g = blk / nbg;
+  const int64_t j = blk - g * nbg;
+  const int64_t start = g * gsize + j * kElemsPerBlock;
+  const int64_t n8 = (min((int64_t)kElemsPerBlock, gsize - j * kElemsPerBlock)) / 8;
+  const u32x4* src = reinterpret_cast<const u32x4*>(x + start);
+  uint2* dst = reinterpret_cast<uint2*>(codes + start);
+  const float qm = 1.0f / dequant[per_bh ? g : 0];
+  u32x4 v[kFlatLoads];
+#pragma unroll
+  for (int i = 0; i < kFlatLoads; ++i) {
+    const int64_t idx = (int64_t)i * kQThreads + threadIdx.x;
+    v[i] = idx < n8 ? __builtin_nontemporal_load(src + idx) : u32x4{0u, 0u, 0u, 0u};
+  }
+#pragma unroll
+  for (int i = 0; i < kFlatLoads; ++i) {
+    const int64_t idx = (int64_t)i * kQThreads + threadIdx.x;
+    if (idx < n8) {
+      uint2 o;
+      o.x = quant4(v[i][0], v[i][1], qm);
+      o.y = quant4(v[i][2], v[i][3], qm);
+      dst[idx] = o;
+    }
+  }
+}
+
 // BHSD output: codes[r*D + d] for global row r = bh*S + s.
 __global__ __launch_bounds__(kQThreads) void quant_apply_kernel(QParams p, const float* dequant,
                                                                 int per_bh, uint8_t* codes) {
@@ -244,6 +319,8 @@ struct Plan {
   QParams p;
   int per_bh;
   size_t ws_bytes;
+  bool flat;      // contiguous input: the flat kernels apply
+  int64_t gsize;  // elements per group when flat
 };
 
 bool is_pow2(int64_t v) { return v > 0 && (v & (v - 1)) == 0; }
@@ -298,6 +375,8 @@ int make_plan(const void* x, int64_t B, int64_t H, int64_t S, int64_t D, int64_t
   p.vpr_log2 = ilog2(p.D / 8);
   out->p = p;
   out->per_bh = granularity == RP_SCALE_PER_BH;
+  out->flat = contiguous;
+  out->gsize = B * H * S * D / p.ngroups;
   out->ws_bytes = (size_t)(p.ngroups * p.nbg) * sizeof(uint32_t);
   return RP_OK;
 }
@@ -318,8 +397,12 @@ int launch_scale(const Plan& pl, float* dequant_out, void* ws, size_t ws_bytes, 
   }
   uint32_t* partial = static_cast<uint32_t*>(ws);
   const int64_t nblocks = pl.p.ngroups * pl.p.nbg;
-  hipLaunchKernelGGL(amax_partial_kernel, dim3((unsigned)nblocks), dim3(kQThreads), 0, st, pl.p,
-                     partial);
+  if (pl.flat)
+    hipLaunchKernelGGL(amax_flat_kernel, dim3((unsigned)nblocks), dim3(kQThreads), 0, st, pl.p.x,
+                       pl.gsize, pl.p.nbg, partial);
+  else
+    hipLaunchKernelGGL(amax_partial_kernel, dim3((unsigned)nblocks), dim3(kQThreads), 0, st,
+                       pl.p, partial);
   int rc = check_launch("amax_partial");
   if (rc) return rc;
   hipLaunchKernelGGL(scale_finalize_kernel, dim3((unsigned)pl.p.ngroups), dim3(kQThreads), 0, st,
@@ -332,8 +415,12 @@ int launch_apply(const Plan& pl, const void* x, int64_t B, int64_t H, int64_t S,
                  int layout, int64_t ld, hipStream_t st) {
   if (layout == RP_LAYOUT_BHSD) {
     const int64_t nblocks = pl.p.ngroups * pl.p.nbg;
-    hipLaunchKernelGGL(quant_apply_kernel, dim3((unsigned)nblocks), dim3(kQThreads), 0, st, pl.p,
-                       dequant, pl.per_bh, codes);
+    if (pl.flat)
+      hipLaunchKernelGGL(quant_flat_kernel, dim3((unsigned)nblocks), dim3(kQThreads), 0, st,
+                         pl.p.x, pl.gsize, pl.p.nbg, dequant, pl.per_bh, codes);
+    else
+      hipLaunchKernelGGL(quant_apply_kernel, dim3((unsigned)nblocks), dim3(kQThreads), 0, st,
+                         pl.p, dequant, pl.per_bh, codes);
     return check_launch("quant_apply");
   }
   if (layout != RP_LAYOUT_BHDS) {
