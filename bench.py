@@ -267,7 +267,8 @@ def bench_gemm(args, cfg) -> dict:
         "config": {"workload": cfg.name, "M": cfg.M, "K": cfg.K, "N": cfg.N},
         "roofline": {"bound": "mfma", "achieved": round(tf, 2), "peak": FP8_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(tf / FP8_PEAK_TFLOPS, 4),
-                     "traffic": None, "kernel": "gemm_kernel", "kernel_ms": round(gemm_ms, 4)},
+                     "traffic": _traffic_from_profiles("gemm256_kernel", cfg.name),
+                     "kernel": "gemm256_kernel", "kernel_ms": round(gemm_ms, 4)},
         "quantize": {"ms": round(quant_ms, 4),
                      "achieved_GBps": round(5 * cfg.M * cfg.K / (quant_ms * 1e-3) / 1e9, 1)},
     }
