@@ -107,7 +107,8 @@ int rp_fp8_scale_quantize(const void* x, int64_t B, int64_t H, int64_t S, int64_
  *         ldv % 128 == 0, ldv >= Skv, columns [Skv, ldv) zero
  *   q/k/v_scale : dequant scales, element bh*scale_stride for head bh = b*H+h
  *         (scale_stride 1: per (b, h); 0: per tensor)
- *   sm_scale : softmax temperature (the reference default is 1/sqrt(D))
+ *   sm_scale : softmax temperature (the reference default is 1/sqrt(D)),
+ *         finite and >= 0
  *   out : (B, H, Sq, D) logical, element (b,h,s,d) at
  *         out + b*osb + h*osh + s*oss + d (elements of out_dtype)
  *   D in {64, 128}; mask per RP_MASK_*; Sq, Skv >= 1. */

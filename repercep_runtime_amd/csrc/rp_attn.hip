@@ -42,12 +42,14 @@
 //   wave's MFMAs overlap the other wave's softmax.  A single wave issues
 //   VALU instructions at about one per 5 cycles (v_exp_f32 and
 //   v_cvt_pk_fp8_f32 one per 9), so the softmax phase, not the matrix core,
-//   sets the pace; the MFMA phase reads its LDS operands two MFMAs ahead so
-//   that it stays well inside the softmax phase's length.
+//   sets the pace.  The MFMA phase therefore keeps its own VALU work small
+//   and tucked between its MFMAs, runs at raised wave priority, and reads
+//   its LDS operands two MFMAs ahead.
 // * K tiles of 128 keys are double-buffered and V^T tiles triple-buffered
 //   in LDS, loaded by the four waves of group 0 with global_load_lds_dwordx4
-//   (no VGPR staging); each LDS row carries one 16-byte pad granule so every
-//   16-lane ds_read_b128 group hits 16 distinct bank groups.
+//   (no VGPR staging; SGPR tile base + fixed per-lane offsets); each LDS row
+//   carries one 16-byte pad granule so every 16-lane ds_read_b128 group hits
+//   16 distinct bank groups.
 // * Grid: one workgroup per (head, query block), remapped so that the
 //   workgroups resident on one XCD (dispatch is round-robin over the 8
 //   XCDs) work on the same head and share its K/V through that XCD's L2.
@@ -115,8 +117,6 @@ struct Geo {
   static constexpr int V_BYTES = D * V_PITCH;
   static constexpr int K_BLKS = kBlockN * K_GRAN / 64;  // wave instructions per K tile
   static constexpr int V_BLKS = D * V_GRAN / 64;
-  static constexpr int K_LOADS_MAX = (K_BLKS + NW - 1) / NW;
-  static constexpr int V_LOADS_MAX = (V_BLKS + NW - 1) / NW;
   static constexpr int K_STAGES = 2;               // ping-pong layout:
   static constexpr int V_STAGES = 3;               // V^T lives one step longer
   static constexpr int LDS_BYTES = K_STAGES * K_BYTES + V_STAGES * V_BYTES;
@@ -151,6 +151,15 @@ __device__ __forceinline__ void gload_lds16(const void* src, uint32_t lds_block)
                : "v"(src), "s"(base)
                : "memory", "m0");
 }
+// The same load with a wave-uniform 64-bit base in SGPRs and a 32-bit
+// per-lane offset ("saddr" form): no per-lane address arithmetic.
+__device__ __forceinline__ void gload_lds16_s(const void* base, uint32_t voff, uint32_t lds_block) {
+  const uint32_t m0v = __builtin_amdgcn_readfirstlane(lds_block);
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
+               :
+               : "v"(voff), "s"(base), "s"(m0v)
+               : "memory", "m0");
+}
 #pragma clang diagnostic pop
 
 // Combine a lane's value with lane l^32's (the other half of the wave)
@@ -165,63 +174,93 @@ __device__ __forceinline__ float xhalf_sum(float x) {
 }
 
 // Direct-to-LDS loads of one (K, V^T) tile.  Each wave instruction fills one
-// contiguous KiB (64 granules) of LDS; granule p of a tile is row p / GRAN,
+// contiguous KiB (64 granules) of LDS; granule p of a block is row p / GRAN,
 // slot p % GRAN.  K rows are stored in S^T A-operand order (LDS row 32h + rho
 // holds key_of(h, rho)); V^T rows are d.  Pad slots re-load the row's first
-// granule (valid memory, never read).
-template <int D, int NW>
-struct TileOffsets {
-  uint32_t k[Geo<D, NW>::K_LOADS_MAX];  // relative to kh + kv0*D
-  int k_key[Geo<D, NW>::K_LOADS_MAX];   // key inside the tile
-  uint32_t v[Geo<D, NW>::V_LOADS_MAX];  // relative to vh + kv0
+// granule (valid memory, never read).  The tile's K_BLKS + V_BLKS blocks, K
+// first, are dealt round-robin to the NL loading waves; a wave left one block
+// short repeats its own previous block (same source, same destination).
+template <int D, int NL>
+struct TileLoads {
+  using G = Geo<D, 8>;
+  static constexpr int T = G::K_BLKS + G::V_BLKS;
+  static constexpr int N = (T + NL - 1) / NL;
+  uint32_t off[N];  // K: key*D + granule; V^T: d*ldv + granule (bytes, per lane)
+  int key[N];       // K: key inside the tile, for the tail clamp
+  int blk[N];       // block index (wave-uniform)
 };
 
-template <int D, int NW>
-__device__ __forceinline__ TileOffsets<D, NW> tile_offsets(int64_t ldv, int wave, int lane) {
-  using G = Geo<D, NW>;
-  TileOffsets<D, NW> o;
+template <int D, int NL>
+__device__ __forceinline__ TileLoads<D, NL> tile_loads(int64_t ldv, int wave, int lane) {
+  using G = Geo<D, 8>;
+  using TL = TileLoads<D, NL>;
+  TL o;
 #pragma unroll
-  for (int n = 0; n < G::K_LOADS_MAX; ++n) {
-    const int p = (n * NW + wave) * kWave + lane;
-    const int row = p / G::K_GRAN, slot = p % G::K_GRAN;
-    const int key = key_of(row >> 5, row & 31);
-    o.k_key[n] = key;
-    o.k[n] = (uint32_t)(key * D + (slot < D / 16 ? slot : 0) * 16);
-  }
-#pragma unroll
-  for (int n = 0; n < G::V_LOADS_MAX; ++n) {
-    const int p = (n * NW + wave) * kWave + lane;
-    const int d = p / G::V_GRAN, slot = p % G::V_GRAN;
-    o.v[n] = (uint32_t)(d * ldv + (slot < kBlockN / 16 ? slot : 0) * 16);
+  for (int n = 0; n < TL::N; ++n) {
+    int b = n * NL + wave;
+    if (b >= TL::T) b -= NL;
+    o.blk[n] = b;
+    if (b < G::K_BLKS) {
+      const int p = b * kWave + lane;
+      const int row = p / G::K_GRAN, slot = p % G::K_GRAN;
+      const int key = key_of(row >> 5, row & 31);
+      o.key[n] = key;
+      o.off[n] = (uint32_t)(key * D + (slot < D / 16 ? slot : 0) * 16);
+    } else {
+      const int p = (b - G::K_BLKS) * kWave + lane;
+      const int d = p / G::V_GRAN, slot = p % G::V_GRAN;
+      o.key[n] = 0;
+      o.off[n] = (uint32_t)(d * ldv + (slot < kBlockN / 16 ? slot : 0) * 16);
+    }
   }
   return o;
 }
 
-// Issue tile `kb`.  K rows past Skv (last tile only) re-read the last key --
-// their scores are masked; V^T is zero-padded to ldv.
-template <int D, int NW>
-__device__ __forceinline__ void issue_tile(const AttnArgs& a, const uint8_t* kh, const uint8_t* vh,
-                                           const TileOffsets<D, NW>& o, int kb, uint32_t kst,
-                                           uint32_t vst, int wave) {
-  using G = Geo<D, NW>;
-  const int kv0 = kb * kBlockN;
-  const uint8_t* kt = kh + (int64_t)kv0 * D;
-  const bool tail = kv0 + kBlockN > a.Skv;
-#pragma unroll
-  for (int n = 0; n < G::K_LOADS_MAX; ++n) {
-    const int blk = n * NW + wave;
-    if (blk < G::K_BLKS) {
-      uint32_t off = o.k[n];
-      if (tail && kv0 + o.k_key[n] >= a.Skv)
-        off = off - (uint32_t)((kv0 + o.k_key[n] - (a.Skv - 1)) * D);
-      gload_lds16(kt + off, kst + blk * 1024u);
+// Where the loads of one tile go.  A tile holds keys [kbeg, kbeg + 128).
+// The last tile, when Skv is not a multiple of 128, is shifted back to end
+// at key Skv-1 (kbeg = Skv - 128; the keys it repeats from the tile before
+// are masked), so that every load stays inside K without per-lane clamps.
+// Only a first tile shorter than 128 keys (Skv < 128) cannot shift: its rows
+// past Skv re-read key Skv-1 (CLAMP loads) and are masked.
+struct TileDst {
+  const uint8_t* kt;  // K rows of the tile in HBM
+  const uint8_t* vt;  // V^T columns of the tile in HBM
+  int klim;           // last valid key inside the tile, CLAMP loads only
+  uint32_t kst, vst;  // LDS stages
+};
+
+// Issue load slot n of the tile.  Called with a constant n (unrolled
+// loops), so whether the slot is a K or a V^T block folds at compile time,
+// except for the one slot shared by both, where a wave-uniform select picks
+// it: no branches.
+template <int D, int NL, bool CLAMP>
+__device__ __forceinline__ void issue_slot(int n, const TileLoads<D, NL>& L, const TileDst& t) {
+  using G = Geo<D, 8>;
+  const bool any_k = n * NL < G::K_BLKS;
+  const bool any_v = n * NL + NL - 1 >= G::K_BLKS || (n + 1) * NL > TileLoads<D, NL>::T;
+  const int b = L.blk[n];
+  const uint32_t kdst = t.kst + (uint32_t)b * 1024u;
+  const uint32_t vdst = t.vst + (uint32_t)(b - G::K_BLKS) * 1024u;
+  if constexpr (CLAMP) {
+    const uint8_t* ksrc = t.kt + (L.off[n] - (uint32_t)(max(L.key[n] - t.klim, 0) * D));
+    const uint8_t* vsrc = t.vt + L.off[n];
+    if (any_k && !any_v) {
+      gload_lds16(ksrc, kdst);
+    } else if (!any_k) {
+      gload_lds16(vsrc, vdst);
+    } else {
+      const bool is_k = b < G::K_BLKS;
+      gload_lds16(is_k ? ksrc : vsrc, is_k ? kdst : vdst);
     }
-  }
-  const uint8_t* vt = vh + kv0;
-#pragma unroll
-  for (int n = 0; n < G::V_LOADS_MAX; ++n) {
-    const int blk = n * NW + wave;
-    if (blk < G::V_BLKS) gload_lds16(vt + o.v[n], vst + blk * 1024u);
+  } else {
+    if (any_k && !any_v) {
+      gload_lds16_s(t.kt, L.off[n], kdst);
+    } else if (!any_k) {
+      gload_lds16_s(t.vt, L.off[n], vdst);
+    } else {
+      const bool is_k = b < G::K_BLKS;
+      gload_lds16_s(is_k ? t.kt : t.vt, L.off[n], is_k ? kdst : vdst);
+    }
   }
 }
 
@@ -236,27 +275,39 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
 }
 
 // Two LDS reads (32 bytes per lane) of one MFMA operand.
-__device__ __forceinline__ i32x8 lds_op(const uint8_t* p) {
-  return cat8(*reinterpret_cast<const i32x4*>(p), *reinterpret_cast<const i32x4*>(p + 16));
+__device__ __forceinline__ i32x8 lds_op(uint32_t lds_addr) {
+  typedef const i32x4 __attribute__((address_space(3)))* lds_i32x4_p;
+  const lds_i32x4_p p = (lds_i32x4_p)(uintptr_t)lds_addr;
+  const i32x4 lo = p[0], hi = p[1];
+  return cat8(lo, hi);
 }
 
-// One MFMA phase: S^T = K(i) . Q^T (DO_S) and O^T += V^T(i-1) . P^T(i-1)
-// (DO_PV), as one stream of MFMAs whose operands are read from LDS through a
-// ring of kRing registers sets, kRing-1 MFMAs ahead of their use, so LDS
-// latency overlaps the matrix core instead of stalling it.  Consecutive
-// MFMAs write different accumulators (key tiles / head-dim tiles inner), so
-// none waits for its predecessor's result.
+// One MFMA phase: S^T = K(i) . Q^T, then O^T += V^T(i-1) . P^T(i-1), as one
+// stream of MFMAs whose operands are read from LDS through a ring of kRing
+// register sets, kRing-1 MFMAs ahead of their use.  Consecutive MFMAs write
+// different accumulators, so none waits for its predecessor's result.
+//
+// Before the stream, O^T *= alpha(i-1): the rescale owed since the previous
+// phase's row max, skipped when no row of the wave raised its max.  Between
+// the MFMAs the wave issues the phase's other work, which would otherwise
+// wait for the stream to drain:
+//   during S^T:  the loads of tile i+1 (LOADS);
+//   during PV:   partial row maxima of S^T(i) (MAX), 64 / NP scores per step.
 constexpr int kRing = 3;
 
-template <int D, bool DO_S, bool DO_PV>
-__device__ __forceinline__ void mfma_phase(const uint8_t* kl, const uint8_t* vl,
+template <int D, bool LOADS, bool MAX>
+__device__ __forceinline__ void mfma_phase(uint32_t kl, uint32_t vl,
                                            const i32x8 (&qop)[D / 64], const i32x8 (&pop)[2],
-                                           f32x16 (&s)[4], f32x16 (&acc)[D / 32]) {
+                                           f32x16 (&s)[4], f32x16 (&acc)[D / 32], float alpha_prev,
+                                           float (&mh)[8], const TileLoads<D, 4>& L,
+                                           const TileDst& dst) {
   using G = Geo<D, 8>;
-  constexpr int NS = DO_S ? 4 * G::KSTEPS : 0;   // S^T steps: ks outer, key tile hh inner
-  constexpr int NP = DO_PV ? 2 * G::ETILES : 0;  // PV steps: k-half m outer, d tile e inner
+  constexpr int NS = 4 * G::KSTEPS;   // S^T steps: ks outer, key tile hh inner
+  constexpr int NP = 2 * G::ETILES;   // PV steps: k-half m outer, d tile e inner
   constexpr int N = NS + NP;
-  auto addr = [&](int t) -> const uint8_t* {
+  constexpr int NLD = TileLoads<D, 4>::N;
+  constexpr int MX = 64 / NP;              // scores per partial max
+  auto addr = [&](int t) -> uint32_t {
     if (t < NS) {
       const int hh = t & 3, ks = t >> 2;
       return kl + 32 * hh * G::K_PITCH + 64 * ks;
@@ -264,9 +315,13 @@ __device__ __forceinline__ void mfma_phase(const uint8_t* kl, const uint8_t* vl,
     const int u = t - NS, e = u % G::ETILES, m = u / G::ETILES;
     return vl + 32 * e * G::V_PITCH + 64 * m;
   };
+  if (__any(alpha_prev != 1.0f)) {
+#pragma unroll
+    for (int e = 0; e < G::ETILES; ++e) acc[e] *= alpha_prev;
+  }
   i32x8 ring[kRing];
 #pragma unroll
-  for (int t = 0; t < kRing - 1 && t < N; ++t) ring[t] = lds_op(addr(t));
+  for (int t = 0; t < kRing - 1; ++t) ring[t] = lds_op(addr(t));
 #pragma unroll
   for (int t = 0; t < N; ++t) {
     if (t + kRing - 1 < N) ring[(t + kRing - 1) % kRing] = lds_op(addr(t + kRing - 1));
@@ -275,20 +330,28 @@ __device__ __forceinline__ void mfma_phase(const uint8_t* kl, const uint8_t* vl,
       const int hh = t & 3, ks = t >> 2;
       // the first k-step starts from the inline constant 0
       s[hh] = mfma_32x32x64(op, qop[ks], ks == 0 ? f32x16{} : s[hh]);
+      if constexpr (LOADS) {
+#pragma unroll
+        for (int n = t * NLD / NS; n < (t + 1) * NLD / NS; ++n) issue_slot<D, 4, false>(n, L, dst);
+      }
     } else {
       const int u = t - NS, e = u % G::ETILES, m = u / G::ETILES;
       acc[e] = mfma_32x32x64(op, pop[m], acc[e]);
-    }
-  }
-  // Pin that order for the machine scheduler, which would otherwise sink
-  // every read next to its MFMA to save registers: the first kRing-1
-  // operands' reads, then per step one MFMA followed by the reads of the
-  // operand kRing-1 steps ahead.
-  __builtin_amdgcn_sched_group_barrier(0x100, 2 * (kRing - 1), 0);
+      if constexpr (MAX) {
+        const int f0 = u * MX;
+        float x = max3f(s[f0 >> 4][f0 & 15], s[(f0 + 1) >> 4][(f0 + 1) & 15],
+                        s[(f0 + 2) >> 4][(f0 + 2) & 15]);
 #pragma unroll
-  for (int t = 0; t < N; ++t) {
-    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-    if (t + kRing - 1 < N) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+        for (int j = 3; j + 1 < MX; j += 2)
+          x = max3f(x, s[(f0 + j) >> 4][(f0 + j) & 15], s[(f0 + j + 1) >> 4][(f0 + j + 1) & 15]);
+        if constexpr (MX % 2 == 0) x = max3f(x, s[(f0 + MX - 1) >> 4][(f0 + MX - 1) & 15], x);
+        mh[u] = x;
+      }
+    }
+    // Fence each step: the machine scheduler would otherwise sink the
+    // operand reads next to their MFMAs and pull VALU work next to the
+    // MFMA that produces its input, stalling the wave.
+    __builtin_amdgcn_sched_barrier(0);
   }
 }
 
@@ -300,10 +363,16 @@ __device__ __forceinline__ void mfma_phase(const uint8_t* kl, const uint8_t* vl,
 //   slot 2i   : group 0  MFMA(i)        group 1  SOFTMAX(i-1)
 //   slot 2i+1 : group 0  SOFTMAX(i)     group 1  MFMA(i)
 //
-//   MFMA(i)    = S^T(i) = K(i) . Q^T   and   O^T += V^T(i-1) . P^T(i-1),
-//                then, on the VALU while those drain: mask, running max and
-//                alpha(i) of tile i, O^T *= alpha(i)
+//   MFMA(i)    = O^T *= alpha(i-1), then S^T(i) = K(i) . Q^T and
+//                O^T += V^T(i-1) . P^T(i-1), with the running max and
+//                alpha(i) of tile i taken between and after those MFMAs
 //   SOFTMAX(i) = P(i) = e4m3(p * 448) and the row sums
+//
+// One softmax wave keeps the SIMD's VALU nearly saturated, and the
+// arbiter favours the older wave (group 0), so group 1's MFMA phase, whose
+// few VALU instructions gate a whole stream of MFMAs, would wait behind
+// group 0's softmax.  Group 1 therefore raises its priority for its MFMA
+// phase (s_setprio); group 0's MFMA phase already wins by age.
 //
 // Numbering the workgroup barriers from the prologue's (0), group 0 runs
 // MFMA(j) between barriers 2j and 2j+1 and group 1 between 2j+1 and 2j+2.
@@ -313,7 +382,7 @@ __device__ __forceinline__ void mfma_phase(const uint8_t* kl, const uint8_t* vl,
 // before barrier 2j.  Only group 0 loads: the slot in which a group issues
 // loads costs its SIMD VALU time, and in this slot the MFMA group, not the
 // softmax group, has VALU time to spare.
-template <int D, bool OUT_F32>
+template <int D, bool OUT_F32, bool WINDOW>
 __global__ __launch_bounds__(512, 1)
 void attn_fwd_kernel(AttnArgs a) {
   constexpr int NW = 8;
@@ -338,7 +407,7 @@ void attn_fwd_kernel(AttnArgs a) {
 
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
   const int group = wave >> 2;
   const int lq = lane & 31;  // query column / operand row inside a 32x32 tile
   const int lg = lane >> 5;  // k-slot group (32 bytes)
@@ -366,9 +435,28 @@ void attn_fwd_kernel(AttnArgs a) {
 
   // Group 0's four waves issue every tile (see the schedule below); their
   // per-lane load offsets are fixed for the whole kernel.
-  constexpr int NL = 4;
-  const TileOffsets<D, NL> toff = tile_offsets<D, NL>(a.ldv, wave & 3, lane);
-  if (group == 0) issue_tile<D, NL>(a, kh, vh, toff, 0, kbuf_lds, vbuf_lds, wave);
+  const TileLoads<D, 4> tl = tile_loads<D, 4>(a.ldv, wave & 3, lane);
+  // first key of tile j (see TileDst)
+  auto tile_begin = [&](int j) {
+    const int kv0 = j * kBlockN;
+    return (j > 0 && kv0 + kBlockN > a.Skv) ? a.Skv - kBlockN : kv0;
+  };
+  // loads of tile `src` into the LDS stages of tile `stage`
+  auto tile_dst = [&](int src, int stage) {
+    TileDst t;
+    const int kbeg = tile_begin(src);
+    t.kt = kh + (int64_t)kbeg * D;
+    t.vt = vh + kbeg;
+    t.klim = a.Skv - 1 - kbeg;
+    t.kst = kbuf_lds + (stage & 1) * G::K_BYTES;
+    t.vst = vbuf_lds + (stage % 3) * G::V_BYTES;
+    return t;
+  };
+  if (group == 0) {
+    const TileDst t0 = tile_dst(0, 0);
+#pragma unroll
+    for (int n = 0; n < TileLoads<D, 4>::N; ++n) issue_slot<D, 4, true>(n, tl, t0);
+  }
   // V^T stage 2 is read (times P = 0) by the first MFMA phase before tile 2
   // lands there: clear it so that no stale NaN code can reach the accumulator.
   for (int o = tid * 16; o < G::V_BYTES; o += G::THREADS * 16)
@@ -398,101 +486,124 @@ void attn_fwd_kernel(AttnArgs a) {
   __syncthreads();
   if (group == 1) __syncthreads();  // group 1 starts half a step behind
 
-  float alpha = 1.0f, moff = 0.0f;  // of the tile whose softmax comes next
-  for (int i = 0; i <= n_kb; ++i) {
-    // ================= MFMA(i) =================
-    // Tile j is issued by group 0 at the start of MFMA(j-1), right after
-    // workgroup barrier 2j-2, and waited for at the end of SOFTMAX(j-1),
-    // before barrier 2j (the prologue's barrier is number 0).
-    if (group == 0 && i + 1 < n_kb)
-      issue_tile<D, NL>(a, kh, vh, toff, i + 1, kbuf_lds + ((i + 1) & 1) * G::K_BYTES,
-                        vbuf_lds + ((i + 1) % 3) * G::V_BYTES, wave);
-    // Every MFMA phase runs both products: in the first one P is zero and
-    // V^T stage 2 holds zeros (cleared in the prologue), in the last one the
-    // S^T result is never used.
-    mfma_phase<D, true, true>(kbuf + (i & 1) * G::K_BYTES + k_base,
-                              vbuf + ((i + 2) % 3) * G::V_BYTES + v_base, qop, pop, s, acc);
-    // The rest of the MFMA phase is softmax work that the VALU of this wave
-    // can do while its MFMAs drain (the softmax phase of the other wave on
-    // the SIMD is the critical path): mask, row max and alpha of tile i once
-    // S^T(i) has landed, then O^T *= alpha(i) once O^T += V^T(i-1) . P^T(i-1)
-    // has landed.
-    if (i < n_kb) {
+  // The two groups run separate copies of the loop, so that each MFMA phase
+  // is one branch-free block: group 0 issues the tile loads, group 1 none.
+  auto run = [&](auto loads_c) {
+    constexpr bool LOADS = decltype(loads_c)::value;
+    // alpha: rescale of tile i's row statistics, applied to l in SOFTMAX(i)
+    // and to O^T in MFMA(i+1), before PV(i) accumulates
+    float alpha = 1.0f, moff = 0.0f;
+    for (int i = 0; i <= n_kb; ++i) {
+      // ================= MFMA(i) =================
+      if (!LOADS) __builtin_amdgcn_s_setprio(1);  // the MFMA phase issues first on its SIMD
+      // Tile j is issued by group 0 during MFMA(j-1), after workgroup barrier
+      // 2j-2, and waited for at the end of SOFTMAX(j-1), before barrier 2j
+      // (the prologue's barrier is number 0).  Every MFMA phase runs both
+      // products: in the first one P is zero and V^T stage 2 holds zeros
+      // (cleared in the prologue), in the last one the S^T result is unused.
       const int kv0 = i * kBlockN;
-      bool need_mask = kv0 + kBlockN > a.Skv;
-      if (a.mask == RP_MASK_CAUSAL) need_mask |= kv0 + kBlockN - 1 > q_wave0;
-      if (a.mask == RP_MASK_SHARED_PREFIX) need_mask |= kv0 + kBlockN > a.prefix;
-      if (need_mask) {
-        // every supported mask is "kv < pre_end, or lo <= kv <= hi" with a
-        // per-query window; bitwise predicates, one select per score
-        const float ninf = -__builtin_inff();
-        int lo = 0, hi = a.Skv - 1;
-        if (a.mask == RP_MASK_CAUSAL) hi = min(q, hi);
-        if (a.mask == RP_MASK_SHARED_PREFIX) {
-          lo = a.prefix + q - q % a.suffix;
-          hi = min(a.prefix + q, hi);
-        }
-        const int pre_end = a.mask == RP_MASK_SHARED_PREFIX ? min(a.prefix, a.Skv) : 0;
-        const int kvl = kv0 + 32 * lg;
-        const int lo_t = lo - kvl, hi_t = hi - kvl, pe_t = pre_end - kvl;
-#pragma unroll
-        for (int hh = 0; hh < 4; ++hh)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const int o = 64 * (hh >> 1) + 16 * (hh & 1) + r;  // key - kvl
-            const int vis = ((o >= lo_t) & (o <= hi_t)) | (o < pe_t);
-            s[hh][r] = vis ? s[hh][r] : ninf;
+      const bool tail = kv0 + kBlockN > a.Skv;
+      // operand base addresses of this phase's K and V^T stages; opaque to
+      // the compiler, so every read is one register plus an immediate
+      uint32_t kl = kbuf_lds + (i & 1) * G::K_BYTES + k_base;
+      uint32_t vl = vbuf_lds + ((i + 2) % 3) * G::V_BYTES + v_base;
+      asm("" : "+v"(kl), "+v"(vl));
+      // group 0 issues tile i+1; past the last tile it re-reads the last one
+      // into the stages tile i+1 would use, which are free (see above)
+      const TileDst nxt = tile_dst(min(i + 1, n_kb - 1), i + 1);
+      // Without a window mask the row max is taken between the PV MFMAs, over
+      // the raw scores: key rows past Skv duplicate key Skv-1, so the tail
+      // tile's max already equals the max over its valid keys.  With a window
+      // mask, a tile the window cuts takes its max after the phase, from the
+      // masked scores.
+      float mh[8];
+      mfma_phase<D, LOADS, !WINDOW>(kl, vl, qop, pop, s, acc, alpha, mh, tl, nxt);
+      if (i < n_kb) {
+        bool masked = tail;
+        if (a.mask == RP_MASK_CAUSAL) masked |= kv0 + kBlockN - 1 > q_wave0;
+        if (a.mask == RP_MASK_SHARED_PREFIX) masked |= kv0 + kBlockN > a.prefix;
+        if (masked) {
+          // every supported mask is "kv < pre_end, or lo <= kv <= hi" with a
+          // per-query window; bitwise predicates, one select per score
+          const float ninf = -__builtin_inff();
+          int lo = 0, hi = a.Skv - 1;
+          if (a.mask == RP_MASK_CAUSAL) hi = min(q, hi);
+          if (a.mask == RP_MASK_SHARED_PREFIX) {
+            lo = a.prefix + q - q % a.suffix;
+            hi = min(a.prefix + q, hi);
           }
-      }
-      // row max over the lane's 64 scores: four independent v_max3 chains
-      // (one per key tile), then combine
-      float mt[4];
-#pragma unroll
-      for (int hh = 0; hh < 4; ++hh) {
-        float x = max3f(s[hh][0], s[hh][1], s[hh][2]);
-#pragma unroll
-        for (int r = 3; r < 15; r += 2) x = max3f(x, s[hh][r], s[hh][r + 1]);
-        mt[hh] = max3f(x, s[hh][15], s[hh][15]);
-      }
-      float mx = max3f(mt[0], mt[1], max3f(mt[2], mt[3], mt[3]));
-      mx = xhalf_max(mx);
-      const float m_new = max3f(m_run, mx * c2, mx * c2);
-      const float m_use = (m_new == -__builtin_inff()) ? 0.0f : m_new;
-      alpha = __builtin_amdgcn_exp2f(m_run - m_use);
-      m_run = m_new;
-      moff = m_use - kLog2PMax;
-      if (__any(alpha != 1.0f)) {
-#pragma unroll
-        for (int e = 0; e < G::ETILES; ++e) acc[e] *= alpha;
-      }
-    }
-    __syncthreads();
-
-    // ================= SOFTMAX(i) =================
-    if (i < n_kb) {
-      float ps[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-      for (int m = 0; m < 2; ++m) {
-        int pw[8];
-#pragma unroll
-        for (int wd = 0; wd < 8; ++wd) {
-          const int hh = 2 * m + (wd >> 2);
-          const int r = 4 * (wd & 3);
-          const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[hh][r + 0], c2, -moff));
-          const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[hh][r + 1], c2, -moff));
-          const float p2 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[hh][r + 2], c2, -moff));
-          const float p3 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[hh][r + 3], c2, -moff));
-          ps[wd & 3] += (p0 + p1) + (p2 + p3);
-          pw[wd] = (int)pack4_e4m3(p0, p1, p2, p3);
+          const int pre_end = a.mask == RP_MASK_SHARED_PREFIX ? min(a.prefix, a.Skv) : 0;
+          // keys before kv0 are the shifted last tile's repeats
+          const int kvl = tile_begin(i) + 32 * lg;
+          const int lo_t = lo - kvl, hi_t = hi - kvl, pe_t = pre_end - kvl, new_t = kv0 - kvl;
+  #pragma unroll
+          for (int hh = 0; hh < 4; ++hh)
+  #pragma unroll
+            for (int r = 0; r < 16; ++r) {
+              const int o = 64 * (hh >> 1) + 16 * (hh & 1) + r;  // key - kvl
+              const int vis = (o >= new_t) & (((o >= lo_t) & (o <= hi_t)) | (o < pe_t));
+              s[hh][r] = vis ? s[hh][r] : ninf;
+            }
         }
-        pop[m] = i32x8{pw[0], pw[1], pw[2], pw[3], pw[4], pw[5], pw[6], pw[7]};
+        float mx;
+        if constexpr (!WINDOW) {
+          constexpr int NP = 2 * G::ETILES;
+          mx = max3f(mh[0], mh[1], mh[2]);
+  #pragma unroll
+          for (int j = 3; j + 1 < NP; j += 2) mx = max3f(mx, mh[j], mh[j + 1]);
+          if constexpr (NP % 2 == 0) mx = max3f(mx, mh[NP - 1], mh[NP - 1]);
+        } else {
+          float mt[4];
+  #pragma unroll
+          for (int hh = 0; hh < 4; ++hh) {
+            float x = max3f(s[hh][0], s[hh][1], s[hh][2]);
+  #pragma unroll
+            for (int r = 3; r < 15; r += 2) x = max3f(x, s[hh][r], s[hh][r + 1]);
+            mt[hh] = max3f(x, s[hh][15], s[hh][15]);
+          }
+          mx = max3f(mt[0], mt[1], max3f(mt[2], mt[3], mt[3]));
+        }
+        mx = xhalf_max(mx);
+        const float m_new = max3f(m_run, mx * c2, mx * c2);
+        const float m_use = (m_new == -__builtin_inff()) ? 0.0f : m_new;
+        alpha = __builtin_amdgcn_exp2f(m_run - m_use);
+        m_run = m_new;
+        moff = m_use - kLog2PMax;
       }
-      l_run = l_run * alpha + ((ps[0] + ps[1]) + (ps[2] + ps[3]));
+      if (!LOADS) __builtin_amdgcn_s_setprio(0);
+      __syncthreads();
+
+      // ================= SOFTMAX(i) =================
+      if (i < n_kb) {
+        float ps[4] = {-0.0f, -0.0f, -0.0f, -0.0f};  // x + -0 == x: no first add
+  #pragma unroll
+        for (int m = 0; m < 2; ++m) {
+          int pw[8];
+  #pragma unroll
+          for (int wd = 0; wd < 8; ++wd) {
+            const int hh = 2 * m + (wd >> 2);
+            const int r = 4 * (wd & 3);
+            const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[hh][r + 0], c2, -moff));
+            const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[hh][r + 1], c2, -moff));
+            const float p2 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[hh][r + 2], c2, -moff));
+            const float p3 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[hh][r + 3], c2, -moff));
+            ps[wd & 3] += (p0 + p1) + (p2 + p3);
+            pw[wd] = (int)pack4_e4m3(p0, p1, p2, p3);
+          }
+          pop[m] = i32x8{pw[0], pw[1], pw[2], pw[3], pw[4], pw[5], pw[6], pw[7]};
+        }
+        l_run = l_run * alpha + ((ps[0] + ps[1]) + (ps[2] + ps[3]));
+      }
+      if (LOADS) wait_vmem_all();
+      __syncthreads();
     }
-    if (group == 0) wait_vmem_all();
-    __syncthreads();
+  };
+  if (group == 0) {
+    run(std::true_type{});
+    __syncthreads();  // balance group 1's extra opening barrier
+  } else {
+    run(std::false_type{});
   }
-  if (group == 0) __syncthreads();  // balance group 1's extra opening barrier
 
   // ---- epilogue: out = acc * v_scale / l  (acc carries P*448, l sums P*448)
   const float l = xhalf_sum(l_run);
@@ -530,10 +641,18 @@ int launch_attn(const AttnArgs& base, bool out_f32, hipStream_t st) {
     return RP_ERR_UNSUPPORTED;
   }
   a.n_work = (int)work;
-  if (out_f32)
-    hipLaunchKernelGGL((attn_fwd_kernel<D, true>), dim3(a.n_work), dim3(512), 0, st, a);
-  else
-    hipLaunchKernelGGL((attn_fwd_kernel<D, false>), dim3(a.n_work), dim3(512), 0, st, a);
+  const dim3 grid(a.n_work), block(512);
+  if (a.mask != RP_MASK_NONE) {
+    if (out_f32)
+      hipLaunchKernelGGL((attn_fwd_kernel<D, true, true>), grid, block, 0, st, a);
+    else
+      hipLaunchKernelGGL((attn_fwd_kernel<D, false, true>), grid, block, 0, st, a);
+  } else {
+    if (out_f32)
+      hipLaunchKernelGGL((attn_fwd_kernel<D, true, false>), grid, block, 0, st, a);
+    else
+      hipLaunchKernelGGL((attn_fwd_kernel<D, false, false>), grid, block, 0, st, a);
+  }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) {
     rp_set_error("attn: launch failed: %s", hipGetErrorString(e));
@@ -568,6 +687,12 @@ extern "C" int rp_fp8_attn_fwd(const uint8_t* q8, const uint8_t* k8, const uint8
   if (ldv < Skv || ldv % kBlockN != 0) {
     rp_set_error("attn: ldv=%lld must be a multiple of %d and >= Skv=%d", (long long)ldv,
                  kBlockN, Skv);
+    return RP_ERR_INVALID_ARGUMENT;
+  }
+  // the row max is taken over the raw dot products and scaled afterwards,
+  // which is the max of the scaled scores only for a non-negative factor
+  if (!(sm_scale >= 0.0f) || sm_scale == __builtin_inff()) {
+    rp_set_error("attn: sm_scale=%g must be finite and >= 0", (double)sm_scale);
     return RP_ERR_INVALID_ARGUMENT;
   }
   if (scale_stride != 0 && scale_stride != 1) {

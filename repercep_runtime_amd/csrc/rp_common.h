@@ -45,7 +45,12 @@ __device__ __forceinline__ int cvt_pk_e4m3(float a, float b, int old) {
 
 // Four fp32 -> one dword of codes, element 0 in the low byte.
 __device__ __forceinline__ uint32_t pack4_e4m3(float a, float b, float c, float d) {
-  int r = cvt_pk_e4m3<false>(a, b, 0);
+  // The low-half conversion as asm with a write-only destination: the
+  // builtin keeps the destination's high half, which would cost a register
+  // initialisation per dword although the high-half conversion below
+  // overwrites it.
+  int r;
+  asm("v_cvt_pk_fp8_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
   r = cvt_pk_e4m3<true>(c, d, r);
   return (uint32_t)r;
 }

@@ -91,6 +91,8 @@ def _attn(L, **kw) -> int:
     (dict(odt=5), 1, "out_dtype"),
     (dict(stride=3), 1, "scale_stride"),
     (dict(k8=FAKE + 8), 2, "aligned"),
+    (dict(sm=-0.125), 1, "sm_scale"),
+    (dict(sm=float("nan")), 1, "sm_scale"),
 ])
 def test_attention_argument_checks(kw: dict, status: int, msg: str) -> None:
     L = _capi.lib()
