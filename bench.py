@@ -25,6 +25,7 @@ import argparse
 import json
 import os
 import sys
+import tempfile
 import time
 from pathlib import Path
 
@@ -140,6 +141,13 @@ def bench_attention(args, cfg) -> dict:
     prefix = cfg.prefix
     out = torch.empty_like(q)
     st = torch.cuda.current_stream(dev)
+    # launch configuration as the op resolves it (a timed search on a cache
+    # miss for shapes too small to fill the GPU unsplit; see tuning.py)
+    ops.fp8_flash_attention(q, k, v, causal=cfg.causal, prefix_len=prefix,
+                            suffix_len=cfg.suffix, out=out)
+    splits = ops.tuned_kv_splits(cfg.B, cfg.H, cfg.Sq, cfg.Skv, cfg.D, cfg.causal, prefix,
+                                 cfg.suffix)
+    log(f"[bench] kv_splits {splits}")
 
     def step(ev=None):
         if ev is not None:
@@ -151,7 +159,7 @@ def bench_attention(args, cfg) -> dict:
             ev[1].record(st)
         ops.attention_fp8(q8.view(torch.uint8), k8.view(torch.uint8), vt8.view(torch.uint8),
                           qs, ks, vs, sm, out=out, causal=cfg.causal, prefix_len=prefix,
-                          suffix_len=cfg.suffix)
+                          suffix_len=cfg.suffix, kv_splits=splits)
         if ev is not None:
             ev[2].record(st)
 
@@ -200,7 +208,7 @@ def bench_attention(args, cfg) -> dict:
         "data": "synthetic: seeded N(0,1) bf16 Q/K/V generated on the GPU",
         "config": {"workload": cfg.name, "B": cfg.B, "H": cfg.H, "Sq": cfg.Sq, "Skv": cfg.Skv,
                    "D": cfg.D, "causal": cfg.causal, "scale_granularity": "per (b,h)",
-                   "flops_per_step": cfg.flops},
+                   "kv_splits": splits, "flops_per_step": cfg.flops},
         "roofline": {
             "bound": "mfma",
             "achieved": round(tflops_attn, 2),
@@ -296,6 +304,10 @@ def main() -> int:
               f"WORLD_SIZE={world}); the FP8 attention path shards over heads with no "
               f"collective -- see DESIGN.md", file=sys.stderr)
         return 2
+
+    # a run's own launch-configuration cache, unless the caller names one
+    os.environ.setdefault("REPERCEP_FP8_AUTOTUNE_CACHE", os.path.join(
+        tempfile.gettempdir(), f"repercep_bench_autotune_{os.getpid()}.json"))
 
     import torch
 

@@ -119,6 +119,27 @@ int rp_fp8_attn_fwd(const uint8_t* q8, const uint8_t* k8, const uint8_t* vt8, in
                     int B, int H, int Sq, int Skv, int D,
                     int mask, int prefix_len, int suffix_len, void* stream);
 
+/* Key-split variant of rp_fp8_attn_fwd: the key range is cut into
+ * `kv_splits` contiguous parts of whole 128-key tiles (fewer when Skv has
+ * fewer tiles), each run by its own workgroups with its own running max, and
+ * a second kernel merges the parts.  It raises the parallelism of short or
+ * few-head problems, which otherwise occupy a fraction of the GPU.  The
+ * reference has no such entry point; it stands for the tile configuration its
+ * wrapper resolves per shape (fp8_flash_attn.py:461-477, BLOCK_M/BLOCK_N),
+ * and like BLOCK_N there it moves P's quantization grid within the FP8
+ * tolerance.  kv_splits == 1 is rp_fp8_attn_fwd (workspace may be NULL).
+ *   workspace : >= rp_fp8_attn_workspace_bytes(B, H, Sq, D, kv_splits)
+ *               bytes of device memory, 256-byte aligned; not shared by calls
+ *               that may overlap. */
+size_t rp_fp8_attn_workspace_bytes(int B, int H, int Sq, int D, int kv_splits);
+int rp_fp8_attn_fwd_split(const uint8_t* q8, const uint8_t* k8, const uint8_t* vt8, int64_t ldv,
+                          const float* q_scale, const float* k_scale, const float* v_scale,
+                          int scale_stride, float sm_scale, void* out, int out_dtype,
+                          int64_t osb, int64_t osh, int64_t oss,
+                          int B, int H, int Sq, int Skv, int D,
+                          int mask, int prefix_len, int suffix_len, int kv_splits,
+                          void* workspace, size_t workspace_bytes, void* stream);
+
 /* --------------------------------------------------------------- GEMM
  * C (M, N) bf16 = bf16( fp32(A8 . B8) * (a_scale * b_scale) ).
  * Replaces fp8_gemm_launch, kernels/hip/fp8_attn/fp8_gemm.hip:162-179

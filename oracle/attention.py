@@ -23,6 +23,11 @@ sets P's quantization grid); callers match the kernel's tile width.
 ``mutation`` lets the tests plant a plausible mistake in the oracle and show
 that a pin catches it; it is never set outside tests.
 
+``emulate_key_splits`` restates this build's key-split launch (no reference
+counterpart) from ``emulate`` over sub-ranges; it is pinned by (f) equality
+with ``emulate`` for one range and (g) the P-quant-free merge against the exact
+softmax, with and without a causal mask.
+
 Parity: pinned.  tests/test_oracle_attention.py checks (a) the P-quant-free
 path against an exact fp64 softmax for multi-tile, ragged, causal and
 shared-prefix cases, (b) hand-derived answers for the P quantization and the
@@ -59,8 +64,14 @@ def visible(q: np.ndarray, kv: np.ndarray, mask: int, prefix: int = 0, suffix: i
 def emulate(q8: np.ndarray, k8: np.ndarray, v8: np.ndarray, q_scale: float, k_scale: float,
             v_scale: float, sm_scale: float, rows: np.ndarray | None = None, *,
             block_n: int = 128, mask: int = 0, prefix: int = 0, suffix: int = 1,
-            pquant: bool = True, mutation: str | None = None) -> np.ndarray:
-    """fp32 output rows (len(rows), D) for one (b, h) slice of e4m3fn codes."""
+            pquant: bool = True, mutation: str | None = None, kv_offset: int = 0,
+            state: bool = False):
+    """fp32 output rows (len(rows), D) for one (b, h) slice of e4m3fn codes.
+
+    ``kv_offset`` places k8/v8 at that absolute key position (for the masks);
+    ``state`` returns the unnormalised (acc, l, m) instead of acc / l, with a
+    row that sees no key in the range left at acc = l = 0, m = -inf (the
+    reference never meets such a row: its first tile always holds key 0)."""
     Sq, D = q8.shape
     Skv = k8.shape[0]
     rows = np.arange(Sq) if rows is None else np.asarray(rows)
@@ -81,14 +92,19 @@ def emulate(q8: np.ndarray, k8: np.ndarray, v8: np.ndarray, q_scale: float, k_sc
         valid = kv < Skv
         kvc = np.minimum(kv, Skv - 1)
         s = (Q @ K[kvc].T).astype(f32) * qk_scale
-        vis = visible(rows, kv, mask, prefix, suffix) & valid[None, :]
+        vis = visible(rows, kv + kv_offset, mask, prefix, suffix) & valid[None, :]
         if mutation == "causal_off_by_one" and mask == 1:
             vis = (kv[None, :] < rows[:, None]) & valid[None, :]
         s = np.where(vis, s, f32(-np.inf))
         with np.errstate(invalid="ignore"):
             m_new = np.maximum(m, s.max(axis=1))
-            alpha = np.exp(m - m_new).astype(f32)
-            p = np.exp(s - m_new[:, None]).astype(f32)
+            if state:  # rows with nothing visible yet keep alpha = 1, p = 0
+                m_ref = np.where(m_new == -np.inf, f32(0), m_new)
+                alpha = np.where(m == -np.inf, f32(1), np.exp(m - m_ref)).astype(f32)
+                p = np.exp(s - m_ref[:, None]).astype(f32)
+            else:
+                alpha = np.exp(m - m_new).astype(f32)
+                p = np.exp(s - m_new[:, None]).astype(f32)
         if mutation == "no_rescale":
             alpha = np.ones_like(alpha)
         if pquant:
@@ -106,7 +122,31 @@ def emulate(q8: np.ndarray, k8: np.ndarray, v8: np.ndarray, q_scale: float, k_sc
         pv = (p8.astype(np.float64) @ Vt).astype(f32)
         acc = acc + pv * pv_scale
         m = m_new
+    if state:
+        return acc, l, m
     return acc / l[:, None]
+
+
+def emulate_key_splits(q8: np.ndarray, k8: np.ndarray, v8: np.ndarray, q_scale: float,
+                       k_scale: float, v_scale: float, sm_scale: float,
+                       rows: np.ndarray | None = None, *, split_keys: int, block_n: int = 128,
+                       mask: int = 0, prefix: int = 0, suffix: int = 1,
+                       pquant: bool = True) -> np.ndarray:
+    """The key-split launch: ``emulate`` over each range of ``split_keys``
+    keys from its own running max, merged as out = sum_j w_j acc_j /
+    sum_j w_j l_j with w_j = exp(m_j - max_j m_j) over the ranges where the
+    row saw a key.  Not a reference function: the reference runs one range."""
+    Skv = k8.shape[0]
+    parts = [emulate(q8, k8[a:a + split_keys], v8[a:a + split_keys], q_scale, k_scale, v_scale,
+                     sm_scale, rows, block_n=block_n, mask=mask, prefix=prefix, suffix=suffix,
+                     pquant=pquant, kv_offset=a, state=True) for a in range(0, Skv, split_keys)]
+    ms = np.stack([p[2] for p in parts]).astype(np.float64)
+    seen = np.stack([p[1] for p in parts]) != 0
+    mmax = np.where(seen, ms, -np.inf).max(axis=0)
+    w = np.where(seen, np.exp(np.where(seen, ms, 0.0) - mmax), 0.0)
+    num = sum(w[j][:, None] * parts[j][0].astype(np.float64) for j in range(len(parts)))
+    den = sum(w[j] * parts[j][1].astype(np.float64) for j in range(len(parts)))
+    return (num / den[:, None]).astype(np.float32)
 
 
 def exact_softmax_attention(q: np.ndarray, k: np.ndarray, v: np.ndarray, sm_scale: float,

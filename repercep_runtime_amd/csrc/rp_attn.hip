@@ -79,7 +79,16 @@ struct AttnArgs {
   int mask, prefix, suffix;
   int n_qblocks;
   int n_work;
+  // key splits: split j covers keys [j*split_tiles*128, (j+1)*split_tiles*128)
+  // and writes partial results (running max, row sum, unnormalised O) to
+  // ws_ml / ws_acc, which attn_combine_kernel merges
+  int kv_splits, split_tiles;
+  float* ws_ml;   // [split][B*H][Sq] x {m, l}
+  float* ws_acc;  // [split][B*H][Sq][D]
 };
+
+// Output kinds of the attention kernel.
+constexpr int kOutBf16 = 0, kOutF32 = 1, kOutSplit = 2;
 
 __device__ __forceinline__ f32x16 mfma_32x32x64(const i32x8& a, const i32x8& b, const f32x16& c) {
   // cbsz = blgp = 0: both operands OCP e4m3; scale operands 0 select the
@@ -218,10 +227,10 @@ __device__ __forceinline__ TileLoads<D, NL> tile_loads(int64_t ldv, int wave, in
 
 // Where the loads of one tile go.  A tile holds keys [kbeg, kbeg + 128).
 // The last tile, when Skv is not a multiple of 128, is shifted back to end
-// at key Skv-1 (kbeg = Skv - 128; the keys it repeats from the tile before
+// at key Skv-1 (kbeg = Skv - 128; the keys it repeats from before its start
 // are masked), so that every load stays inside K without per-lane clamps.
-// Only a first tile shorter than 128 keys (Skv < 128) cannot shift: its rows
-// past Skv re-read key Skv-1 (CLAMP loads) and are masked.
+// Only a tile of a key range shorter than 128 (Skv < 128) cannot shift: its
+// rows past Skv re-read key Skv-1 (CLAMP loads) and are masked.
 struct TileDst {
   const uint8_t* kt;  // K rows of the tile in HBM
   const uint8_t* vt;  // V^T columns of the tile in HBM
@@ -382,7 +391,7 @@ __device__ __forceinline__ void mfma_phase(uint32_t kl, uint32_t vl,
 // before barrier 2j.  Only group 0 loads: the slot in which a group issues
 // loads costs its SIMD VALU time, and in this slot the MFMA group, not the
 // softmax group, has VALU time to spare.
-template <int D, bool OUT_F32, bool WINDOW>
+template <int D, int OUT, bool WINDOW>
 __global__ __launch_bounds__(512, 1)
 void attn_fwd_kernel(AttnArgs a) {
   constexpr int NW = 8;
@@ -401,8 +410,10 @@ void attn_fwd_kernel(AttnArgs a) {
   const int per = a.n_work >> 3, rem = a.n_work & 7;
   const int xcd = w & 7;
   const int L = xcd * per + min(xcd, rem) + (w >> 3);
-  const int bh = L / a.n_qblocks;
-  const int qb = L - bh * a.n_qblocks;
+  const int per_bh = a.n_qblocks * a.kv_splits;
+  const int bh = L / per_bh;
+  const int qb = (L - bh * per_bh) / a.kv_splits;
+  const int split = L - bh * per_bh - qb * a.kv_splits;
   const int b = bh / a.H, h = bh - b * a.H;
 
   const int tid = threadIdx.x;
@@ -426,20 +437,36 @@ void attn_fwd_kernel(AttnArgs a) {
   // exp2 domain: s2 = dot * c2 with c2 = sm_scale*q_scale*k_scale*log2(e)
   const float c2 = ((a.sm_scale * q_scale) * k_scale) * kLog2e;
 
-  // ---- key range: causal blocks past the block's last query are skipped
-  int n_kb = (a.Skv + kBlockN - 1) / kBlockN;
+  // ---- key range [kv_begin, kv_end): this workgroup's split; causal blocks
+  // past the block's last query are skipped
+  const int kv_begin = split * a.split_tiles * kBlockN;
+  const int kv_end = min(a.Skv, kv_begin + a.split_tiles * kBlockN);
+  int n_kb = (kv_end - kv_begin + kBlockN - 1) / kBlockN;
   if (a.mask == RP_MASK_CAUSAL) {
     const int q_last = min(q_block0 + BLOCK_M, a.Sq) - 1;
-    n_kb = min(n_kb, q_last / kBlockN + 1);
+    n_kb = q_last < kv_begin ? 0 : min(n_kb, (q_last - kv_begin) / kBlockN + 1);
+  }
+  if constexpr (OUT == kOutSplit) {
+    if (n_kb == 0) {  // a causal split wholly past this block's queries
+      const int q0 = q_block0 + tid;
+      if (tid < BLOCK_M && q0 < a.Sq) {
+        const int64_t row = ((int64_t)split * a.B * a.H + bh) * a.Sq + q0;
+        a.ws_ml[2 * row] = -__builtin_inff();
+        a.ws_ml[2 * row + 1] = 0.0f;
+        for (int d = 0; d < D; d += 4)
+          *reinterpret_cast<float4*>(a.ws_acc + row * D + d) = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+      }
+      return;
+    }
   }
 
   // Group 0's four waves issue every tile (see the schedule below); their
   // per-lane load offsets are fixed for the whole kernel.
   const TileLoads<D, 4> tl = tile_loads<D, 4>(a.ldv, wave & 3, lane);
-  // first key of tile j (see TileDst)
+  // first key of tile j of the range (see TileDst)
   auto tile_begin = [&](int j) {
-    const int kv0 = j * kBlockN;
-    return (j > 0 && kv0 + kBlockN > a.Skv) ? a.Skv - kBlockN : kv0;
+    const int kv0 = kv_begin + j * kBlockN;
+    return (kv0 + kBlockN > a.Skv && a.Skv >= kBlockN) ? a.Skv - kBlockN : kv0;
   };
   // loads of tile `src` into the LDS stages of tile `stage`
   auto tile_dst = [&](int src, int stage) {
@@ -501,7 +528,7 @@ void attn_fwd_kernel(AttnArgs a) {
       // (the prologue's barrier is number 0).  Every MFMA phase runs both
       // products: in the first one P is zero and V^T stage 2 holds zeros
       // (cleared in the prologue), in the last one the S^T result is unused.
-      const int kv0 = i * kBlockN;
+      const int kv0 = kv_begin + i * kBlockN;
       const bool tail = kv0 + kBlockN > a.Skv;
       // operand base addresses of this phase's K and V^T stages; opaque to
       // the compiler, so every read is one register plus an immediate
@@ -512,10 +539,12 @@ void attn_fwd_kernel(AttnArgs a) {
       // into the stages tile i+1 would use, which are free (see above)
       const TileDst nxt = tile_dst(min(i + 1, n_kb - 1), i + 1);
       // Without a window mask the row max is taken between the PV MFMAs, over
-      // the raw scores: key rows past Skv duplicate key Skv-1, so the tail
-      // tile's max already equals the max over its valid keys.  With a window
-      // mask, a tile the window cuts takes its max after the phase, from the
-      // masked scores.
+      // the raw scores: rows past Skv duplicate key Skv-1, and the keys a
+      // shifted last tile repeats were in the tile before, so the raw max is
+      // the max over the tile's visible keys.  It is not when a shifted tile
+      // opens a key split (its repeats belong to the previous split), nor
+      // under a window mask: such a tile takes its max after the phase, from
+      // the masked scores.
       float mh[8];
       mfma_phase<D, LOADS, !WINDOW>(kl, vl, qop, pop, s, acc, alpha, mh, tl, nxt);
       if (i < n_kb) {
@@ -546,7 +575,7 @@ void attn_fwd_kernel(AttnArgs a) {
             }
         }
         float mx;
-        if constexpr (!WINDOW) {
+        if (!WINDOW && !(i == 0 && tile_begin(0) != kv0)) {
           constexpr int NP = 2 * G::ETILES;
           mx = max3f(mh[0], mh[1], mh[2]);
   #pragma unroll
@@ -607,6 +636,21 @@ void attn_fwd_kernel(AttnArgs a) {
 
   // ---- epilogue: out = acc * v_scale / l  (acc carries P*448, l sums P*448)
   const float l = xhalf_sum(l_run);
+  if constexpr (OUT == kOutSplit) {
+    // partial result of this key split, relative to its own running max
+    if (q < a.Sq) {
+      const int64_t row = ((int64_t)split * a.B * a.H + bh) * a.Sq + q;
+      float* dst = a.ws_acc + row * D;
+#pragma unroll
+      for (int e = 0; e < G::ETILES; ++e)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          *reinterpret_cast<float4*>(dst + 32 * e + 8 * i + 4 * lg) =
+              make_float4(acc[e][4 * i], acc[e][4 * i + 1], acc[e][4 * i + 2], acc[e][4 * i + 3]);
+      if (lg == 0) *reinterpret_cast<float2*>(a.ws_ml + 2 * row) = make_float2(m_run, l);
+    }
+    return;
+  }
   const float inv = v_scale / l;
   if (q < a.Sq) {
     const int64_t obase = (int64_t)b * a.osb + (int64_t)h * a.osh + (int64_t)q * a.oss;
@@ -617,7 +661,7 @@ void attn_fwd_kernel(AttnArgs a) {
         const int d = 32 * e + 8 * i + 4 * lg;
         const float o0 = acc[e][4 * i + 0] * inv, o1 = acc[e][4 * i + 1] * inv;
         const float o2 = acc[e][4 * i + 2] * inv, o3 = acc[e][4 * i + 3] * inv;
-        if constexpr (OUT_F32) {
+        if constexpr (OUT == kOutF32) {
           *reinterpret_cast<float4*>(static_cast<float*>(a.out) + obase + d) =
               make_float4(o0, o1, o2, o3);
         } else {
@@ -630,28 +674,96 @@ void attn_fwd_kernel(AttnArgs a) {
   }
 }
 
+// Merge the key splits of one query row: with m_j, l_j, O_j the running
+// max, row sum and unnormalised output of split j (O_j and l_j relative to
+// m_j, in the exp2 domain), out = sum_j w_j O_j * v_scale / sum_j w_j l_j,
+// w_j = exp2(m_j - max_j m_j).  Splits that saw no visible key (l_j = 0)
+// are left out.  One thread per four head-dim elements of a row.
+template <int D, bool OUT_F32>
+__global__ __launch_bounds__(256)
+void attn_combine_kernel(AttnArgs a) {
+  constexpr int CH = D / 4;
+  const int64_t rows = (int64_t)a.B * a.H * a.Sq;
+  const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t row = t / CH;
+  if (row >= rows) return;
+  const int d = (int)(t - row * CH) * 4;
+  const float2* ml = reinterpret_cast<const float2*>(a.ws_ml);
+  float mmax = -__builtin_inff();
+#pragma unroll 8
+  for (int j = 0; j < a.kv_splits; ++j) {
+    const float2 v = ml[row + j * rows];
+    if (v.y != 0.0f) mmax = fmaxf(mmax, v.x);
+  }
+  float l = 0.0f;
+  float4 o = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll 8
+  for (int j = 0; j < a.kv_splits; ++j) {
+    const float2 v = ml[row + j * rows];
+    const float4 x = *reinterpret_cast<const float4*>(a.ws_acc + (row + j * rows) * D + d);
+    // a split that saw no key of this row has l = 0 and O = 0: weight 0
+    const float w = v.y != 0.0f ? __builtin_amdgcn_exp2f(v.x - mmax) : 0.0f;
+    l += w * v.y;
+    o.x += w * x.x; o.y += w * x.y; o.z += w * x.z; o.w += w * x.w;
+  }
+  const int bh = (int)(row / a.Sq), q = (int)(row - (int64_t)bh * a.Sq);
+  const int b = bh / a.H, h = bh - b * a.H;
+  const float inv = a.vs[bh * a.scale_stride] / l;
+  const int64_t obase = (int64_t)b * a.osb + (int64_t)h * a.osh + (int64_t)q * a.oss + d;
+  if constexpr (OUT_F32) {
+    *reinterpret_cast<float4*>(static_cast<float*>(a.out) + obase) =
+        make_float4(o.x * inv, o.y * inv, o.z * inv, o.w * inv);
+  } else {
+    uint2 pk;
+    pk.x = pack_bf16x2(o.x * inv, o.y * inv);
+    pk.y = pack_bf16x2(o.z * inv, o.w * inv);
+    *reinterpret_cast<uint2*>(static_cast<uint16_t*>(a.out) + obase) = pk;
+  }
+}
+
+template <int D, int OUT>
+void launch_fwd(const AttnArgs& a, hipStream_t st) {
+  const dim3 grid(a.n_work), block(512);
+  if (a.mask != RP_MASK_NONE)
+    hipLaunchKernelGGL((attn_fwd_kernel<D, OUT, true>), grid, block, 0, st, a);
+  else
+    hipLaunchKernelGGL((attn_fwd_kernel<D, OUT, false>), grid, block, 0, st, a);
+}
+
+constexpr int kBlockM = 32 * 8;  // query rows per workgroup
+
+// Key tiles per split and the number of non-empty splits for a request of
+// `kv_splits`.
+inline void split_plan(int Skv, int kv_splits, int* split_tiles, int* n_splits) {
+  const int n_kb = (Skv + kBlockN - 1) / kBlockN;
+  const int want = max(1, min(kv_splits, n_kb));
+  *split_tiles = (n_kb + want - 1) / want;
+  *n_splits = (n_kb + *split_tiles - 1) / *split_tiles;
+}
+
 template <int D>
 int launch_attn(const AttnArgs& base, bool out_f32, hipStream_t st) {
   AttnArgs a = base;
-  constexpr int BLOCK_M = 32 * 8;
-  a.n_qblocks = (a.Sq + BLOCK_M - 1) / BLOCK_M;
-  const int64_t work = (int64_t)a.n_qblocks * a.B * a.H;
-  if (work > 0x7fffffff) {
+  a.n_qblocks = (a.Sq + kBlockM - 1) / kBlockM;
+  const int64_t work = (int64_t)a.n_qblocks * a.B * a.H * a.kv_splits;
+  if (work > 0x7fffffff || (int64_t)a.B * a.H * a.Sq * (D / 4) > 0x7fffffffLL * 256) {
     rp_set_error("attn: grid too large");
     return RP_ERR_UNSUPPORTED;
   }
   a.n_work = (int)work;
-  const dim3 grid(a.n_work), block(512);
-  if (a.mask != RP_MASK_NONE) {
+  if (a.kv_splits == 1) {
     if (out_f32)
-      hipLaunchKernelGGL((attn_fwd_kernel<D, true, true>), grid, block, 0, st, a);
+      launch_fwd<D, kOutF32>(a, st);
     else
-      hipLaunchKernelGGL((attn_fwd_kernel<D, false, true>), grid, block, 0, st, a);
+      launch_fwd<D, kOutBf16>(a, st);
   } else {
+    launch_fwd<D, kOutSplit>(a, st);
+    const int64_t threads = (int64_t)a.B * a.H * a.Sq * (D / 4);
+    const dim3 cgrid((unsigned)((threads + 255) / 256)), cblock(256);
     if (out_f32)
-      hipLaunchKernelGGL((attn_fwd_kernel<D, true, false>), grid, block, 0, st, a);
+      hipLaunchKernelGGL((attn_combine_kernel<D, true>), cgrid, cblock, 0, st, a);
     else
-      hipLaunchKernelGGL((attn_fwd_kernel<D, false, false>), grid, block, 0, st, a);
+      hipLaunchKernelGGL((attn_combine_kernel<D, false>), cgrid, cblock, 0, st, a);
   }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) {
@@ -666,12 +778,14 @@ int launch_attn(const AttnArgs& base, bool out_f32, hipStream_t st) {
 
 using namespace rp;
 
-extern "C" int rp_fp8_attn_fwd(const uint8_t* q8, const uint8_t* k8, const uint8_t* vt8,
-                               int64_t ldv, const float* q_scale, const float* k_scale,
-                               const float* v_scale, int scale_stride, float sm_scale, void* out,
-                               int out_dtype, int64_t osb, int64_t osh, int64_t oss, int B, int H,
-                               int Sq, int Skv, int D, int mask, int prefix_len, int suffix_len,
-                               void* stream) {
+namespace {
+
+// Argument checks shared by the attention entry points; fills `a`.
+int attn_setup(AttnArgs& a, const uint8_t* q8, const uint8_t* k8, const uint8_t* vt8, int64_t ldv,
+               const float* q_scale, const float* k_scale, const float* v_scale,
+               int scale_stride, float sm_scale, void* out, int out_dtype, int64_t osb,
+               int64_t osh, int64_t oss, int B, int H, int Sq, int Skv, int D, int mask,
+               int prefix_len, int suffix_len) {
   if (!q8 || !k8 || !vt8 || !q_scale || !k_scale || !v_scale || !out) {
     rp_set_error("attn: null pointer");
     return RP_ERR_INVALID_ARGUMENT;
@@ -722,15 +836,79 @@ extern "C" int rp_fp8_attn_fwd(const uint8_t* q8, const uint8_t* k8, const uint8
     rp_set_error("attn: q8/k8/vt8 must be 16-byte aligned");
     return RP_ERR_UNSUPPORTED;
   }
-  AttnArgs a{};
+  a = AttnArgs{};
   a.q = q8; a.k = k8; a.vt = vt8;
   a.qs = q_scale; a.ks = k_scale; a.vs = v_scale;
   a.out = out; a.osb = osb; a.osh = osh; a.oss = oss;
   a.ldv = ldv; a.sm_scale = sm_scale; a.scale_stride = scale_stride;
   a.B = B; a.H = H; a.Sq = Sq; a.Skv = Skv;
   a.mask = mask; a.prefix = prefix_len; a.suffix = suffix_len > 0 ? suffix_len : 1;
+  a.kv_splits = 1;
+  a.split_tiles = (Skv + kBlockN - 1) / kBlockN;
+  return RP_OK;
+}
+
+int attn_run(const AttnArgs& a, int D, int out_dtype, void* stream) {
   hipStream_t st = static_cast<hipStream_t>(stream);
   const bool f32 = out_dtype == RP_OUT_F32;
   if (D == 128) return launch_attn<128>(a, f32, st);
   return launch_attn<64>(a, f32, st);
+}
+
+}  // namespace
+
+extern "C" int rp_fp8_attn_fwd(const uint8_t* q8, const uint8_t* k8, const uint8_t* vt8,
+                               int64_t ldv, const float* q_scale, const float* k_scale,
+                               const float* v_scale, int scale_stride, float sm_scale, void* out,
+                               int out_dtype, int64_t osb, int64_t osh, int64_t oss, int B, int H,
+                               int Sq, int Skv, int D, int mask, int prefix_len, int suffix_len,
+                               void* stream) {
+  AttnArgs a;
+  const int rc = attn_setup(a, q8, k8, vt8, ldv, q_scale, k_scale, v_scale, scale_stride,
+                            sm_scale, out, out_dtype, osb, osh, oss, B, H, Sq, Skv, D, mask,
+                            prefix_len, suffix_len);
+  return rc != RP_OK ? rc : attn_run(a, D, out_dtype, stream);
+}
+
+extern "C" size_t rp_fp8_attn_workspace_bytes(int B, int H, int Sq, int D, int kv_splits) {
+  if (B <= 0 || H <= 0 || Sq <= 0 || D <= 0 || kv_splits <= 1) return 0;
+  const size_t rows = (size_t)kv_splits * B * H * Sq;
+  const size_t ml = (rows * 2 * sizeof(float) + 255) / 256 * 256;
+  return ml + rows * (size_t)D * sizeof(float);
+}
+
+extern "C" int rp_fp8_attn_fwd_split(const uint8_t* q8, const uint8_t* k8, const uint8_t* vt8,
+                                     int64_t ldv, const float* q_scale, const float* k_scale,
+                                     const float* v_scale, int scale_stride, float sm_scale,
+                                     void* out, int out_dtype, int64_t osb, int64_t osh,
+                                     int64_t oss, int B, int H, int Sq, int Skv, int D, int mask,
+                                     int prefix_len, int suffix_len, int kv_splits,
+                                     void* workspace, size_t workspace_bytes, void* stream) {
+  AttnArgs a;
+  int rc = attn_setup(a, q8, k8, vt8, ldv, q_scale, k_scale, v_scale, scale_stride, sm_scale,
+                      out, out_dtype, osb, osh, oss, B, H, Sq, Skv, D, mask, prefix_len,
+                      suffix_len);
+  if (rc != RP_OK) return rc;
+  if (kv_splits < 1) {
+    rp_set_error("attn: kv_splits=%d must be >= 1", kv_splits);
+    return RP_ERR_INVALID_ARGUMENT;
+  }
+  int split_tiles = 0, n_splits = 1;
+  split_plan(Skv, kv_splits, &split_tiles, &n_splits);
+  if (n_splits > 1) {
+    const size_t need = rp_fp8_attn_workspace_bytes(B, H, Sq, D, n_splits);
+    if (!workspace || workspace_bytes < need ||
+        reinterpret_cast<uintptr_t>(workspace) % 256 != 0) {
+      rp_set_error("attn: workspace of %zu bytes (256-byte aligned) needed for %d key splits",
+                   need, n_splits);
+      return RP_ERR_INVALID_ARGUMENT;
+    }
+    const size_t rows = (size_t)n_splits * B * H * Sq;
+    a.kv_splits = n_splits;
+    a.split_tiles = split_tiles;
+    a.ws_ml = static_cast<float*>(workspace);
+    a.ws_acc = reinterpret_cast<float*>(static_cast<char*>(workspace) +
+                                        (rows * 2 * sizeof(float) + 255) / 256 * 256);
+  }
+  return attn_run(a, D, out_dtype, stream);
 }

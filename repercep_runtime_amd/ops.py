@@ -21,11 +21,12 @@ Numerics (OCP e4m3fn, FP8_MAX = 448):
 from __future__ import annotations
 
 import math
-from typing import Literal
+from typing import Callable, Literal
 
 import torch
 
 from repercep_runtime_amd import _capi as C
+from repercep_runtime_amd import tuning
 
 FP8_E4M3_MAX = 448.0
 #: head dims compiled into the attention kernel
@@ -158,14 +159,15 @@ def attention_fp8(q8: torch.Tensor, k8: torch.Tensor, vt8: torch.Tensor, q_scale
                   k_scale: torch.Tensor, v_scale: torch.Tensor, sm_scale: float, *,
                   out: torch.Tensor | None = None, out_dtype: torch.dtype = torch.bfloat16,
                   causal: bool = False, prefix_len: int | None = None,
-                  suffix_len: int | None = None) -> torch.Tensor:
+                  suffix_len: int | None = None, kv_splits: int = 1) -> torch.Tensor:
     """FP8 attention on already-quantized operands.
 
     q8 (B, H, Sq, D), k8 (B, H, Skv, D) contiguous codes; vt8 (B, H, D, ldv)
     transposed V codes; scales of length B*H (per head) or 1 (per tensor).
     ``out`` may be any (B, H, Sq, D)-shaped view with a contiguous last dim
     (e.g. a permuted (B, S, H, D) buffer).  ``prefix_len``/``suffix_len``
-    select the shared-prefix candidate mask.
+    select the shared-prefix candidate mask.  ``kv_splits`` > 1 runs the key
+    range in that many parts and merges them (``rp_fp8_attn_fwd_split``).
     """
     for name, t in (("q8", q8), ("k8", k8), ("vt8", vt8)):
         _check_cuda(name, t)
@@ -198,11 +200,16 @@ def attention_fp8(q8: torch.Tensor, k8: torch.Tensor, vt8: torch.Tensor, q_scale
     qs = q_scale.to(torch.float32).contiguous()
     ks = k_scale.to(torch.float32).contiguous()
     vs = v_scale.to(torch.float32).contiguous()
-    C.check(C.lib().rp_fp8_attn_fwd(
-        q8.data_ptr(), k8.data_ptr(), vt8.data_ptr(), ldv, qs.data_ptr(), ks.data_ptr(),
-        vs.data_ptr(), stride, float(sm_scale), out.data_ptr(), odt, out.stride(0),
-        out.stride(1), out.stride(2), B, H, Sq, Skv, D, mask, pre, suf, _stream(q8)),
-        "rp_fp8_attn_fwd")
+    args = (q8.data_ptr(), k8.data_ptr(), vt8.data_ptr(), ldv, qs.data_ptr(), ks.data_ptr(),
+            vs.data_ptr(), stride, float(sm_scale), out.data_ptr(), odt, out.stride(0),
+            out.stride(1), out.stride(2), B, H, Sq, Skv, D, mask, pre, suf)
+    if kv_splits == 1:
+        C.check(C.lib().rp_fp8_attn_fwd(*args, _stream(q8)), "rp_fp8_attn_fwd")
+    else:
+        nbytes = C.lib().rp_fp8_attn_workspace_bytes(B, H, Sq, D, int(kv_splits))
+        ws = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=q8.device)
+        C.check(C.lib().rp_fp8_attn_fwd_split(*args, int(kv_splits), ws.data_ptr(), ws.numel(),
+                                              _stream(q8)), "rp_fp8_attn_fwd_split")
     return out
 
 
@@ -210,7 +217,8 @@ def fp8_flash_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *,
                         causal: bool = False, scale: float | None = None,
                         granularity: Granularity = "bh", out: torch.Tensor | None = None,
                         out_dtype: torch.dtype | None = None, prefix_len: int | None = None,
-                        suffix_len: int | None = None) -> torch.Tensor:
+                        suffix_len: int | None = None, kv_splits: int | None = None
+                        ) -> torch.Tensor:
     """Fused FP8 flash attention, (B, H, S, D) bf16 in, (B, H, Sq, D) out.
 
     Mirrors the reference's ``fp8_flash_attention``
@@ -221,6 +229,12 @@ def fp8_flash_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *,
     (cross-attention), inputs may be strided (e.g. permuted (B, S, H, D)
     views -- no copies are made), and the output is written directly in
     bf16 (or into ``out``).
+
+    The launch configuration resolves as in the reference (:482-499):
+    ``kv_splits`` if given; else the fallback when
+    ``REPERCEP_FP8_DISABLE_AUTOTUNE`` is set; else the on-disk cache entry for
+    the shape; else a timed search over ``tuning.candidate_configs`` whose
+    winner is recorded (see ``repercep_runtime_amd.tuning``).
     """
     for name, t in (("q", q), ("k", k), ("v", v)):
         _check_bf16(name, t)
@@ -237,9 +251,60 @@ def fp8_flash_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *,
     qs, q8 = scale_quantize(q, granularity, "bhsd")
     ks, k8 = scale_quantize(k, granularity, "bhsd")
     vs, vt8 = scale_quantize(v, granularity, "bhds")
-    return attention_fp8(q8.view(torch.uint8), k8.view(torch.uint8), vt8.view(torch.uint8),
-                         qs, ks, vs, scale, out=out, out_dtype=out_dtype or q.dtype,
-                         causal=causal, prefix_len=prefix_len, suffix_len=suffix_len)
+
+    def run(splits: int) -> torch.Tensor:
+        return attention_fp8(q8.view(torch.uint8), k8.view(torch.uint8), vt8.view(torch.uint8),
+                             qs, ks, vs, scale, out=out, out_dtype=out_dtype or q.dtype,
+                             causal=causal, prefix_len=prefix_len, suffix_len=suffix_len,
+                             kv_splits=splits)
+
+    if kv_splits is None:
+        kv_splits = _resolve_kv_splits(B, H, Sq, k.shape[2], D, causal, prefix_len, suffix_len,
+                                       run)
+    return run(kv_splits)
+
+
+def _time_call(fn: Callable[[], object], reps: int = 10, rounds: int = 3) -> float:
+    """Seconds per call on the current stream: the best of ``rounds`` runs of
+    ``reps`` back-to-back calls (after one warmup), so that launch overhead
+    overlaps the GPU work it precedes."""
+    fn()
+    best = math.inf
+    for _ in range(rounds):
+        t0 = torch.cuda.Event(enable_timing=True)
+        t1 = torch.cuda.Event(enable_timing=True)
+        t0.record()
+        for _ in range(reps):
+            fn()
+        t1.record()
+        t1.synchronize()
+        best = min(best, t0.elapsed_time(t1) * 1e-3 / reps)
+    return best
+
+
+def tuned_kv_splits(B: int, H: int, Sq: int, Skv: int, D: int, causal: bool = False,
+                    prefix_len: int | None = None, suffix_len: int | None = None) -> int:
+    """The split count ``fp8_flash_attention`` uses for a shape without
+    searching: the fallback when autotuning is disabled, else the cached
+    entry (1 on a miss)."""
+    if tuning.autotune_disabled():
+        return int(tuning.FALLBACK_CONFIG["KV_SPLITS"])
+    cfg = tuning.resolve_config(B, H, Sq, Skv, D, causal, prefix_len, suffix_len)
+    return int(cfg.get("KV_SPLITS", 1)) if cfg else 1
+
+
+def _resolve_kv_splits(B: int, H: int, Sq: int, Skv: int, D: int, causal: bool,
+                       prefix_len: int | None, suffix_len: int | None,
+                       run: Callable[[int], torch.Tensor]) -> int:
+    """Key split count for a shape: fallback, cache, or timed search."""
+    if tuning.autotune_disabled():
+        return tuning.FALLBACK_CONFIG["KV_SPLITS"]
+    cfg = tuning.resolve_config(B, H, Sq, Skv, D, causal, prefix_len, suffix_len)
+    if not cfg:
+        cands = tuning.candidate_configs(B, H, Sq, Skv)
+        cfg = tuning.autotune(cands, lambda c: _time_call(lambda: run(c["KV_SPLITS"])))
+        tuning.record_config(B, H, Sq, Skv, D, causal, cfg, prefix_len, suffix_len)
+    return int(cfg.get("KV_SPLITS", 1))
 
 
 def transpose_fp8(x8: torch.Tensor) -> torch.Tensor:

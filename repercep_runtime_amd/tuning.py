@@ -1,0 +1,149 @@
+"""Per-shape launch configuration of the FP8 attention kernel, cached on disk.
+
+Keeps the reference's persistent autotune cache
+(kernels/triton_kernels/fp8_flash_attn.py:52-94, 453-477): a JSON object that
+maps ``B{B}_H{H}_Sq{Sq}_Skv{Skv}_D{D}_C{causal}`` to a launch configuration,
+written atomically (temporary file, then rename), with a missing, unreadable
+or corrupt file read as empty.  ``REPERCEP_FP8_AUTOTUNE_CACHE`` overrides the
+path and ``REPERCEP_FP8_DISABLE_AUTOTUNE`` selects the fixed fallback
+configuration, as in the reference (:482-499, :551-559).
+
+The gfx950 kernel has one tile shape: 256 query rows in eight waves
+(``BLOCK_M``) against 128-key tiles (``BLOCK_N``).  What varies per shape is
+``KV_SPLITS``: the number of contiguous key ranges run by separate
+workgroups and merged afterwards (``rp_fp8_attn_fwd_split``).  Splitting pays
+when the (query block, head) grid alone would leave most of the 256 compute
+units idle -- short sequences, few heads -- and costs a merge pass otherwise.
+Like the reference's BLOCK_N, the split count moves P's quantization grid
+(each range keeps its own running max) within the FP8 tolerance.
+
+Entries carry the reference's four keys with the values this kernel runs,
+so they also validate under the reference's resolver (:463-471); an absent
+``KV_SPLITS`` means 1, the way absent backend knobs mean "default" there.
+Shared-prefix calls, which the reference does not have, append
+``_P{prefix}S{suffix}`` to the key.
+"""
+
+from __future__ import annotations
+
+import json
+import os
+from pathlib import Path
+from typing import Callable
+
+_DEFAULT_CACHE_PATH = Path.home() / ".cache" / "repercep" / "fp8_hip_autotune.json"
+
+BLOCK_M = 256
+BLOCK_N = 128
+NUM_CUS = 256
+
+#: Used when autotuning is disabled, and the first candidate of every search.
+FALLBACK_CONFIG = {"BLOCK_M": BLOCK_M, "BLOCK_N": BLOCK_N, "num_warps": 8, "num_stages": 2,
+                   "KV_SPLITS": 1}
+
+_REQUIRED = ("BLOCK_M", "BLOCK_N", "num_warps", "num_stages")
+SPLIT_CHOICES = (1, 2, 4, 8, 16, 32)
+
+
+def cache_path() -> Path:
+    override = os.environ.get("REPERCEP_FP8_AUTOTUNE_CACHE")
+    return Path(override) if override else _DEFAULT_CACHE_PATH
+
+
+def cache_load() -> dict:
+    path = cache_path()
+    if not path.exists():
+        return {}
+    try:
+        with path.open("r") as fh:
+            data = json.load(fh)
+    except (OSError, ValueError):
+        return {}
+    return data if isinstance(data, dict) else {}
+
+
+def cache_save(cache: dict) -> None:
+    path = cache_path()
+    path.parent.mkdir(parents=True, exist_ok=True)
+    tmp = path.with_name(f"{path.name}.{os.getpid()}.tmp")
+    with tmp.open("w") as fh:
+        json.dump(cache, fh, indent=2, sort_keys=True)
+    tmp.replace(path)
+
+
+def cache_key(B: int, H: int, Sq: int, Skv: int, D: int, causal: bool,
+              prefix_len: int | None = None, suffix_len: int | None = None) -> str:
+    key = f"B{B}_H{H}_Sq{Sq}_Skv{Skv}_D{D}_C{int(bool(causal))}"
+    if prefix_len is not None:
+        key += f"_P{int(prefix_len)}S{int(suffix_len or 0)}"
+    return key
+
+
+def runnable(cfg: object) -> bool:
+    """Whether this kernel can launch ``cfg`` (entries written by the
+    reference's Triton autotuner may name other tile shapes)."""
+    if not isinstance(cfg, dict) or not all(k in cfg for k in _REQUIRED):
+        return False
+    splits = cfg.get("KV_SPLITS", 1)
+    return (cfg["BLOCK_M"] == BLOCK_M and cfg["BLOCK_N"] == BLOCK_N
+            and isinstance(splits, int) and not isinstance(splits, bool) and splits >= 1)
+
+
+def resolve_config(B: int, H: int, Sq: int, Skv: int, D: int, causal: bool,
+                   prefix_len: int | None = None, suffix_len: int | None = None) -> dict:
+    """The cached configuration for this shape, or {} on a miss."""
+    cfg = cache_load().get(cache_key(B, H, Sq, Skv, D, causal, prefix_len, suffix_len))
+    return dict(cfg) if runnable(cfg) else {}
+
+
+def record_config(B: int, H: int, Sq: int, Skv: int, D: int, causal: bool, cfg: dict,
+                  prefix_len: int | None = None, suffix_len: int | None = None) -> None:
+    cache = cache_load()
+    cache[cache_key(B, H, Sq, Skv, D, causal, prefix_len, suffix_len)] = dict(cfg)
+    cache_save(cache)
+
+
+def autotune_disabled() -> bool:
+    return os.environ.get("REPERCEP_FP8_DISABLE_AUTOTUNE", "") in ("1", "true", "on")
+
+
+def candidate_configs(B: int, H: int, Sq: int, Skv: int) -> list[dict]:
+    """Configurations worth timing for a shape: split counts that leave every
+    range at least one key tile (as the kernel plans them: equal whole-tile
+    ranges, so a request is rounded to the count it yields) and keep the grid
+    within a few workgroups per compute unit.  A shape whose unsplit grid
+    already covers the GPU twice gets the fallback alone."""
+    n_kb = -(-Skv // BLOCK_N)
+    work = -(-Sq // BLOCK_M) * B * H
+    if work >= 2 * NUM_CUS:
+        return [dict(FALLBACK_CONFIG)]
+    counts: list[int] = []
+    for want in sorted(set(SPLIT_CHOICES) | {n_kb}):
+        if want > n_kb:
+            continue
+        tiles = -(-n_kb // want)
+        s = -(-n_kb // tiles)
+        if s not in counts and (s == 1 or work * s <= 8 * NUM_CUS):
+            counts.append(s)
+    return [{**FALLBACK_CONFIG, "KV_SPLITS": s} for s in counts]
+
+
+#: A later (more split) candidate must beat the best earlier one by this
+#: factor: below it the difference is timing noise, and fewer splits keep the
+#: unsplit kernel's P grid and skip the merge pass.
+MIN_GAIN = 0.95
+
+
+def autotune(candidates: list[dict], timer: Callable[[dict], float]) -> dict:
+    """The fastest candidate by ``timer(cfg)`` (seconds per call), taking
+    candidates in order and moving on only for a gain beyond ``MIN_GAIN``."""
+    if not candidates:
+        raise ValueError("no candidate configurations")
+    if len(candidates) == 1:
+        return dict(candidates[0])
+    best, best_t = candidates[0], timer(candidates[0])
+    for c in candidates[1:]:
+        t = timer(c)
+        if t < best_t * MIN_GAIN:
+            best, best_t = c, t
+    return dict(best)

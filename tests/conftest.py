@@ -21,6 +21,17 @@ def pytest_configure(config: pytest.Config) -> None:
     config.addinivalue_line("markers", "gpu: needs an MI355X (gfx950) GPU and the built library")
 
 
+@pytest.fixture(autouse=True)
+def _fixed_launch_config(tmp_path_factory: pytest.TempPathFactory,
+                         monkeypatch: pytest.MonkeyPatch) -> None:
+    """Tests run the fallback launch configuration (one key split), the one
+    the tile-exact oracle comparisons assume, and never touch the user's
+    autotune cache; tests of the cache and of key splits opt out."""
+    monkeypatch.setenv("REPERCEP_FP8_DISABLE_AUTOTUNE", "1")
+    monkeypatch.setenv("REPERCEP_FP8_AUTOTUNE_CACHE",
+                       str(tmp_path_factory.mktemp("autotune") / "fp8_autotune.json"))
+
+
 @pytest.fixture(scope="session")
 def gpu() -> "object":
     import torch

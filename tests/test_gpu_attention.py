@@ -21,7 +21,7 @@ import numpy as np
 import pytest
 import torch
 
-from oracle import native
+from oracle import attention, native
 from repercep_runtime_amd import ops
 from repercep_runtime_amd.workloads import C1, C3_CROSS, C3_SELF, C5, AttnConfig, attn_inputs
 from tests._helpers import baseline_tolerance, bf16_bits, codes_np, err_stats, vt_to_bhsd
@@ -132,6 +132,87 @@ def test_shared_prefix_candidates_c5(gpu: torch.device) -> None:
     ref, _ = _oracle_rows(q, k, v, list(range(C5.H)), np.arange(C5.Sq),
                           sm_scale=C5.D ** -0.5, mask=2, prefix=C5.prefix, suffix=C5.suffix)
     _check(out.cpu().numpy()[0], ref, "c5 shared prefix")
+
+
+SPLIT_CASES = [
+    # name, B, H, Sq, Skv, D, causal, prefix, suffix, split counts
+    ("c1", 1, 8, 1024, 1024, 64, False, None, None, (2, 3, 8)),
+    # 8 tiles, the last shifted back; with 8 splits it opens its own range
+    ("ragged_cross", 1, 2, 700, 1000, 128, False, None, None, (2, 8)),
+    ("causal", 1, 2, 1000, 1000, 128, True, None, None, (2, 4, 8)),
+    ("c5_prefix", 1, 32, 128, 640, 128, False, 512, 8, (2, 3, 5)),
+    ("short_kv", 1, 2, 300, 100, 64, False, None, None, (4,)),   # one tile: no split
+    ("two_tiles_ragged", 2, 1, 257, 131, 128, False, None, None, (2,)),
+]
+
+
+@pytest.mark.parametrize("case", SPLIT_CASES, ids=[c[0] for c in SPLIT_CASES])
+def test_key_splits_vs_oracle(gpu: torch.device, case: tuple) -> None:
+    """Key-split launches (rp_fp8_attn_fwd_split) against the unsplit oracle:
+    each range keeps its own running max, which moves P's quantization grid
+    as the reference's BLOCK_N choice does, so the bound is the FP8
+    tolerance, not the unsplit kernel's bit pattern."""
+    name, B, H, Sq, Skv, D, causal, prefix, suffix, counts = case
+    g = torch.Generator().manual_seed(sum(map(ord, name)))
+    q = torch.randn(B, H, Sq, D, generator=g).to(torch.bfloat16)
+    k = torch.randn(B, H, Skv, D, generator=g).to(torch.bfloat16)
+    v = torch.randn(B, H, Skv, D, generator=g).to(torch.bfloat16)
+    mask = 2 if prefix is not None else (1 if causal else 0)
+    qg, kg, vg = q.to(gpu), k.to(gpu), v.to(gpu)
+    base = ops.fp8_flash_attention(qg, kg, vg, causal=causal, prefix_len=prefix,
+                                   suffix_len=suffix, out_dtype=torch.float32, kv_splits=1)
+    n_kb = -(-Skv // 128)
+    for n in counts:
+        out = ops.fp8_flash_attention(qg, kg, vg, causal=causal, prefix_len=prefix,
+                                      suffix_len=suffix, out_dtype=torch.float32,
+                                      kv_splits=n).cpu().numpy()
+        if Skv <= 128:   # a single key tile cannot split: the unsplit kernel's bits
+            assert np.array_equal(out, base.cpu().numpy()), name
+        # the kernel's plan: equal ranges of whole tiles (rp_attn.hip split_plan)
+        split_keys = -(-n_kb // min(n, n_kb)) * 128
+        for b in range(B):
+            sl = slice(b, b + 1)
+            qs8, ks8, vs8 = (native.quantize_groups(bf16_bits(t[sl]), H) for t in (q, k, v))
+            for h in range(H):
+                ref = attention.emulate_key_splits(
+                    qs8[1][0, h], ks8[1][0, h], vs8[1][0, h], qs8[0][h], ks8[0][h], vs8[0][h],
+                    D ** -0.5, split_keys=split_keys, mask=mask, prefix=prefix or 0,
+                    suffix=suffix or 1)
+                _check(out[b, h], ref, f"{name} kv_splits={n} b={b} h={h}")
+            # against the one-range oracle only the FP8 tolerance holds: each
+            # range quantizes P against its own running max
+            ref1, _ = _oracle_rows(q[sl], k[sl], v[sl], list(range(H)), np.arange(Sq),
+                                   sm_scale=D ** -0.5, mask=mask, prefix=prefix or 0,
+                                   suffix=suffix or 1)
+            _check(out[b], ref1, f"{name} kv_splits={n} b={b} vs one range", rel_tol=5e-2)
+
+
+def test_autotune_records_and_reuses_a_split_count(gpu: torch.device, tmp_path,
+                                                   monkeypatch: pytest.MonkeyPatch) -> None:
+    """Cache miss -> timed search over the candidates, winner recorded under
+    the reference's key; the next call reads it without timing anything."""
+    from repercep_runtime_amd import tuning
+
+    path = tmp_path / "cache.json"
+    monkeypatch.setenv("REPERCEP_FP8_AUTOTUNE_CACHE", str(path))
+    monkeypatch.delenv("REPERCEP_FP8_DISABLE_AUTOTUNE")
+    q, k, v = attn_inputs(C1)
+    qg, kg, vg = q.to(gpu), k.to(gpu), v.to(gpu)
+    out = ops.fp8_flash_attention(qg, kg, vg, out_dtype=torch.float32).cpu().numpy()[0]
+    cfg = tuning.resolve_config(1, C1.H, C1.Sq, C1.Skv, C1.D, False)
+    assert cfg["KV_SPLITS"] in (1, 2, 4, 8), cfg
+    assert "B1_H8_Sq1024_Skv1024_D64_C0" in tuning.cache_load()
+    ref, _ = _oracle_rows(q, k, v, list(range(C1.H)), np.arange(C1.Sq), sm_scale=C1.D ** -0.5)
+    _check(out, ref, f"c1 autotuned kv_splits={cfg['KV_SPLITS']}")
+
+    def no_timing(*_a, **_k):
+        raise AssertionError("cache hit must not time candidates")
+
+    monkeypatch.setattr(ops, "_time_call", no_timing)
+    again = ops.fp8_flash_attention(qg, kg, vg, out_dtype=torch.float32).cpu().numpy()[0]
+    direct = ops.fp8_flash_attention(qg, kg, vg, out_dtype=torch.float32,
+                                     kv_splits=cfg["KV_SPLITS"]).cpu().numpy()[0]
+    assert np.array_equal(again, direct)
 
 
 def test_output_into_strided_bshd_buffer(gpu: torch.device) -> None:

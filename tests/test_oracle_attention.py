@@ -213,3 +213,31 @@ def test_error_vs_sdpa_matches_published_magnitude() -> None:
     assert err.max() <= 0.014 and err.mean() <= 0.001
     assert 0.02 < rel_median < 0.06
     assert rel_mean < 0.10
+
+
+# ------------------------------------------------- key-split emulation pins
+def test_key_split_emulation_with_one_range_is_emulate() -> None:
+    (q8, qs), (k8, ks), (v8, vs) = _random_case(300, 50, 700, 64)
+    for mask in (0, 1):
+        one = attention.emulate_key_splits(q8, k8, v8, qs, ks, vs, 0.125, split_keys=700,
+                                           mask=mask)
+        ref = attention.emulate(q8, k8, v8, qs, ks, vs, 0.125, mask=mask)
+        assert np.array_equal(one, ref)
+
+
+@pytest.mark.parametrize("mask,Sq,Skv,split", [(0, 40, 700, 256), (1, 700, 700, 128),
+                                               (2, 24, 40, 16)])
+def test_key_split_merge_is_exact_softmax_without_pquant(mask: int, Sq: int, Skv: int,
+                                                         split: int) -> None:
+    """Without P quantization the merged ranges are the exact softmax: a wrong
+    merge weight, a dropped range or a causal row with nothing visible in a
+    range (it must contribute nothing) would show here."""
+    (q8, qs), (k8, ks), (v8, vs) = _random_case(310 + mask, Sq, Skv, 32)
+    prefix, suffix = (16, 8) if mask == 2 else (0, 1)
+    got = attention.emulate_key_splits(q8, k8, v8, qs, ks, vs, 0.3, split_keys=split,
+                                       block_n=min(split, 128), mask=mask, prefix=prefix,
+                                       suffix=suffix, pquant=False)
+    ref = attention.exact_softmax_attention(_deq(q8, qs), _deq(k8, ks), _deq(v8, vs), 0.3,
+                                            mask=mask, prefix=prefix, suffix=suffix)
+    assert np.isfinite(got).all()
+    assert np.abs(got - ref).max() / np.abs(ref).max() < 2e-5

@@ -1,0 +1,151 @@
+"""The launch-configuration cache (CPU only).
+
+Re-expresses the reference's cache tests (tests/test_attention_fp8.py:161-371:
+round trip, corruption, search-grid constraints, legacy entries) against
+``repercep_runtime_amd.tuning``, plus this build's own rules: entries naming
+tile shapes this kernel does not run are misses, and the split search is
+confined to shapes that leave the GPU idle.
+"""
+
+from __future__ import annotations
+
+import json
+from pathlib import Path
+
+import pytest
+
+from repercep_runtime_amd import _capi, ops, tuning
+from repercep_runtime_amd.workloads import C1, C3_CROSS, C3_SELF, C5
+
+
+@pytest.fixture()
+def cache_file(tmp_path: Path, monkeypatch: pytest.MonkeyPatch) -> Path:
+    path = tmp_path / "fp8_autotune.json"
+    monkeypatch.setenv("REPERCEP_FP8_AUTOTUNE_CACHE", str(path))
+    monkeypatch.delenv("REPERCEP_FP8_DISABLE_AUTOTUNE", raising=False)
+    return path
+
+
+def test_cache_roundtrip(cache_file: Path) -> None:
+    assert tuning.cache_load() == {}
+    assert tuning.resolve_config(2, 32, 109120, 109120, 128, False) == {}
+
+    cfg = {**tuning.FALLBACK_CONFIG, "KV_SPLITS": 4}
+    tuning.record_config(2, 32, 109120, 109120, 128, False, cfg)
+    assert cache_file.exists()
+    data = json.loads(cache_file.read_text())
+    assert "B2_H32_Sq109120_Skv109120_D128_C0" in data        # the reference's key encoding
+    assert tuning.resolve_config(2, 32, 109120, 109120, 128, False) == cfg
+
+    assert tuning.resolve_config(1, 8, 8192, 8192, 128, False) == {}   # other shape: miss
+    assert tuning.resolve_config(2, 32, 109120, 109120, 128, True) == {}  # causal differs
+
+    other = dict(tuning.FALLBACK_CONFIG)
+    tuning.record_config(1, 8, 8192, 8192, 128, False, other)
+    assert len(tuning.cache_load()) == 2                         # earlier entry kept
+    assert tuning.resolve_config(2, 32, 109120, 109120, 128, False) == cfg
+    assert tuning.resolve_config(1, 8, 8192, 8192, 128, False) == other
+    assert not list(cache_file.parent.glob("*.tmp"))             # atomic write left nothing
+
+
+def test_corrupt_cache_is_a_miss(cache_file: Path) -> None:
+    cache_file.write_text("{ this is not valid json")
+    assert tuning.cache_load() == {}
+    assert tuning.resolve_config(2, 32, 109120, 109120, 128, False) == {}
+    cache_file.write_text("[1, 2, 3]")                           # valid JSON, wrong type
+    assert tuning.cache_load() == {}
+    tuning.record_config(1, 1, 1, 1, 64, False, dict(tuning.FALLBACK_CONFIG))
+    assert tuning.resolve_config(1, 1, 1, 1, 64, False) == tuning.FALLBACK_CONFIG
+
+
+def test_foreign_and_legacy_entries(cache_file: Path) -> None:
+    key = tuning.cache_key(1, 8, 8192, 8192, 128, False)
+    # a Triton winner the reference recorded: a tile shape this kernel does not run
+    triton_cfg = {"BLOCK_M": 128, "BLOCK_N": 64, "num_warps": 4, "num_stages": 2}
+    cache_file.write_text(json.dumps({key: triton_cfg}))
+    assert tuning.resolve_config(1, 8, 8192, 8192, 128, False) == {}
+    # the reference's four keys with this kernel's tile shape and no split knob
+    legacy = {"BLOCK_M": 256, "BLOCK_N": 128, "num_warps": 8, "num_stages": 2}
+    cache_file.write_text(json.dumps({key: legacy}))
+    assert tuning.resolve_config(1, 8, 8192, 8192, 128, False) == legacy
+    assert ops.tuned_kv_splits(1, 8, 8192, 8192, 128) == 1
+    for bad in ({**legacy, "KV_SPLITS": 0}, {**legacy, "KV_SPLITS": "4"},
+                {**legacy, "KV_SPLITS": True}, {"BLOCK_M": 256}):
+        cache_file.write_text(json.dumps({key: bad}))
+        assert tuning.resolve_config(1, 8, 8192, 8192, 128, False) == {}
+
+
+def test_our_entries_satisfy_the_reference_grid_constraints() -> None:
+    """What the reference's resolver and grid test demand of an entry
+    (fp8_flash_attn.py:463-471, tests/test_attention_fp8.py:232-255)."""
+    for cfg in [tuning.FALLBACK_CONFIG] + tuning.candidate_configs(1, 8, 1024, 1024):
+        bm, bn = cfg["BLOCK_M"], cfg["BLOCK_N"]
+        assert bm >= 32 and bn >= 32 and bn <= 2 * bm and bm * bn <= 256 * 256
+        assert cfg["num_warps"] in (4, 8, 16) and cfg["num_stages"] in (2, 3)
+
+
+def test_prefix_key_and_disable_switch(cache_file: Path, monkeypatch: pytest.MonkeyPatch) -> None:
+    assert tuning.cache_key(1, 32, 128, 640, 128, False, 512, 8) == \
+        "B1_H32_Sq128_Skv640_D128_C0_P512S8"
+    tuning.record_config(1, 32, 128, 640, 128, False, {**tuning.FALLBACK_CONFIG, "KV_SPLITS": 5},
+                         512, 8)
+    assert ops.tuned_kv_splits(1, 32, 128, 640, 128, False, 512, 8) == 5
+    assert ops.tuned_kv_splits(1, 32, 128, 640, 128, False) == 1   # no prefix: other key
+    monkeypatch.setenv("REPERCEP_FP8_DISABLE_AUTOTUNE", "1")
+    assert tuning.autotune_disabled()
+    assert ops.tuned_kv_splits(1, 32, 128, 640, 128, False, 512, 8) == 1
+
+
+def test_candidates_only_split_small_grids() -> None:
+    big = tuning.candidate_configs(C3_SELF.B, C3_SELF.H, C3_SELF.Sq, C3_SELF.Skv)
+    assert big == [tuning.FALLBACK_CONFIG]                       # 11,840 workgroups: no search
+    assert tuning.candidate_configs(C3_CROSS.B, C3_CROSS.H, C3_CROSS.Sq,
+                                    C3_CROSS.Skv) == [tuning.FALLBACK_CONFIG]
+    small = tuning.candidate_configs(C1.B, C1.H, C1.Sq, C1.Skv)   # 32 workgroups, 8 key tiles
+    assert [c["KV_SPLITS"] for c in small] == [1, 2, 4, 8]
+    # 5 key tiles: requests 1, 2, 4, 5 give ranges of 5, 3, 2, 1 tiles
+    c5 = tuning.candidate_configs(1, C5.H, C5.Sq, C5.Skv)
+    assert [c["KV_SPLITS"] for c in c5] == [1, 2, 3, 5]
+    # 17 tiles: requests 8 and 16 give ranges of 3 and 2 tiles, i.e. 6 and 9 splits
+    assert [c["KV_SPLITS"] for c in tuning.candidate_configs(1, 1, 256, 17 * 128)] == \
+        [1, 2, 4, 6, 9, 17]
+    assert [c["KV_SPLITS"] for c in tuning.candidate_configs(1, 1, 256, 100)] == [1]
+
+
+def test_autotune_picks_the_fastest() -> None:
+    cands = [{**tuning.FALLBACK_CONFIG, "KV_SPLITS": s} for s in (1, 2, 4)]
+    times = {1: 3.0, 2: 1.0, 4: 2.0}
+    assert tuning.autotune(cands, lambda c: times[c["KV_SPLITS"]])["KV_SPLITS"] == 2
+    # within the noise margin the fewer-split candidate stays
+    times = {1: 1.0, 2: 0.97, 4: 0.96}
+    assert tuning.autotune(cands, lambda c: times[c["KV_SPLITS"]])["KV_SPLITS"] == 1
+    times = {1: 1.0, 2: 0.97, 4: 0.5}
+    assert tuning.autotune(cands, lambda c: times[c["KV_SPLITS"]])["KV_SPLITS"] == 4
+    calls = []
+    assert tuning.autotune(cands[:1], lambda c: calls.append(c) or 0.0) == cands[0]
+    assert calls == []                                            # nothing to time
+    with pytest.raises(ValueError):
+        tuning.autotune([], lambda c: 0.0)
+
+
+def _split_call(L, kv_splits: int, ws, nbytes: int) -> int:
+    fake = 1 << 20
+    return L.rp_fp8_attn_fwd_split(fake, fake, fake, 1024, fake, fake, fake, 1, 0.125, fake, 0,
+                                   8 * 1024 * 64, 1024 * 64, 64, 1, 8, 1024, 1024, 64, 0, 0, 1,
+                                   kv_splits, ws, nbytes, None)
+
+
+def test_split_entry_point_checks_and_sizing() -> None:
+    L = _capi.lib()
+    assert L.rp_fp8_attn_workspace_bytes(1, 8, 1024, 64, 1) == 0
+    n8 = L.rp_fp8_attn_workspace_bytes(1, 8, 1024, 64, 8)
+    rows = 8 * 8 * 1024
+    assert n8 == rows * 2 * 4 + rows * 64 * 4                    # (m, l) + fp32 O per row
+    assert L.rp_fp8_attn_workspace_bytes(0, 8, 1024, 64, 8) == 0
+    assert _split_call(L, 0, None, 0) == 1
+    assert "kv_splits" in L.rp_last_error().decode()
+    assert _split_call(L, 8, None, 0) == 1
+    assert "workspace" in L.rp_last_error().decode()
+    assert _split_call(L, 8, 1 << 20, n8 - 1) == 1                # one byte short
+    assert _split_call(L, 8, (1 << 20) + 64, n8) == 1             # misaligned
+    assert "256-byte" in L.rp_last_error().decode()
