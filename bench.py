@@ -136,15 +136,21 @@ def bench_attention(args, cfg) -> dict:
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
     log(f"[bench] generating {cfg.name} inputs on {dev}")
-    q, k, v = attn_inputs(cfg, device=dev)
+    # configs with QK RMSNorm take pre-norm Q/K: the norm runs fused into
+    # their quantizers inside the step (rmsnorm_scale_quantize)
+    fused_norm = cfg.rmsnorm_qk
+    q, k, v = attn_inputs(cfg, device=dev, normalize=not fused_norm)
     sm = cfg.D ** -0.5
     prefix = cfg.prefix
     out = torch.empty_like(q)
     st = torch.cuda.current_stream(dev)
     # launch configuration as the op resolves it (a timed search on a cache
     # miss for shapes too small to fill the GPU unsplit; see tuning.py)
-    ops.fp8_flash_attention(q, k, v, causal=cfg.causal, prefix_len=prefix,
-                            suffix_len=cfg.suffix, out=out)
+    if fused_norm:
+        ops.fp8_flash_attention_qknorm(q, k, v, causal=cfg.causal, out=out)
+    else:
+        ops.fp8_flash_attention(q, k, v, causal=cfg.causal, prefix_len=prefix,
+                                suffix_len=cfg.suffix, out=out)
     splits = ops.tuned_kv_splits(cfg.B, cfg.H, cfg.Sq, cfg.Skv, cfg.D, cfg.causal, prefix,
                                  cfg.suffix)
     log(f"[bench] kv_splits {splits}")
@@ -152,8 +158,12 @@ def bench_attention(args, cfg) -> dict:
     def step(ev=None):
         if ev is not None:
             ev[0].record(st)
-        qs, q8 = ops.scale_quantize(q, "bh", "bhsd")
-        ks, k8 = ops.scale_quantize(k, "bh", "bhsd")
+        if fused_norm:
+            qs, q8 = ops.rmsnorm_scale_quantize(q)
+            ks, k8 = ops.rmsnorm_scale_quantize(k)
+        else:
+            qs, q8 = ops.scale_quantize(q, "bh", "bhsd")
+            ks, k8 = ops.scale_quantize(k, "bh", "bhsd")
         vs, vt8 = ops.scale_quantize(v, "bh", "bhds")
         if ev is not None:
             ev[1].record(st)
@@ -225,7 +235,9 @@ def bench_attention(args, cfg) -> dict:
             "frac": round(q_gbps / HBM_PEAK_GBPS, 4),
             "ms": round(quant_ms, 4),
             "bytes": qbytes,
-            "note": "Q, K, V: amax pass + finalize + apply (V transposed), 5 B/element",
+            "note": ("Q, K: RMSNorm fused into amax pass + finalize + apply; V: amax pass + "
+                     "finalize + apply (transposed); 5 B/element" if fused_norm else
+                     "Q, K, V: amax pass + finalize + apply (V transposed), 5 B/element"),
         },
     }
     del q, k, v, out

@@ -48,6 +48,12 @@ extern "C" {
 #define RP_OUT_F32 1
 
 /* Mask kinds of rp_fp8_attn_fwd. */
+/* rotary-embedding layouts of rp_fp8_rmsnorm_scale_quantize, as diffusers'
+ * apply_rotary_emb(use_real=True) pairs elements */
+#define RP_ROPE_NONE 0
+#define RP_ROPE_HALF 1        /* d pairs with d +- D/2 (use_real_unbind_dim=-2) */
+#define RP_ROPE_INTERLEAVED 2 /* 2k pairs with 2k+1   (use_real_unbind_dim=-1) */
+
 #define RP_MASK_NONE 0
 #define RP_MASK_CAUSAL 1        /* key kv visible to query q iff kv <= q          */
 #define RP_MASK_SHARED_PREFIX 2 /* keys [0, prefix) visible to all queries; query */
@@ -139,6 +145,29 @@ int rp_fp8_attn_fwd_split(const uint8_t* q8, const uint8_t* k8, const uint8_t* v
                           int B, int H, int Sq, int Skv, int D,
                           int mask, int prefix_len, int suffix_len, int kv_splits,
                           void* workspace, size_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------- fused QK-norm prologue
+ * rp_fp8_scale_quantize of y instead of x, where per row of D elements
+ *   n = RMSNorm(x) = bf16(x * (1 / sqrt(mean(x^2) + eps)))   fp32 math
+ *   n = bf16(n * weight)                          when weight (bf16 [D]) != NULL
+ *   y = bf16(n * cos + rot(n) * sin)              when rope_mode != RP_ROPE_NONE,
+ *                                                 cos/sin fp32 [S, D] row s
+ * computed inside both quantizer passes, so Q and K are read twice and
+ * written once as codes -- the normalised tensor never reaches HBM.
+ * Replaces the attention processors' norm_q/norm_k + apply_rotary_emb
+ * ahead of the FP8 path (reference docs/walkthroughs/02-architecture.md:
+ * 114-123), the rank-4 item of the path's next steps.  codes are BHSD
+ * contiguous; D in {64, 128}; x, strides*2, weight, tables and codes
+ * 16-byte aligned; the sum of squares runs in the order the header of
+ * rp_prologue.hip states. */
+size_t rp_fp8_rmsnorm_quant_workspace_bytes(int64_t B, int64_t H, int64_t S, int64_t D,
+                                            int granularity);
+int rp_fp8_rmsnorm_scale_quantize(const void* x, int64_t B, int64_t H, int64_t S, int64_t D,
+                                  int64_t sb, int64_t sh, int64_t ss, const void* weight,
+                                  float eps, const float* rope_cos, const float* rope_sin,
+                                  int rope_mode, int granularity, float* dequant_out,
+                                  uint8_t* codes, void* workspace, size_t workspace_bytes,
+                                  void* stream);
 
 /* --------------------------------------------------------------- GEMM
  * C (M, N) bf16 = bf16( fp32(A8 . B8) * (a_scale * b_scale) ).

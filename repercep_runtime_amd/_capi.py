@@ -24,13 +24,17 @@ RP_OUT_F32 = 1
 RP_MASK_NONE = 0
 RP_MASK_CAUSAL = 1
 RP_MASK_SHARED_PREFIX = 2
+RP_ROPE_NONE = 0
+RP_ROPE_HALF = 1
+RP_ROPE_INTERLEAVED = 2
 
 #: Every function include/repercep_fp8.h declares.
 EXPORTS = (
     "rp_abi_version", "rp_status_string", "rp_last_error",
     "rp_fp8_quant_workspace_bytes", "rp_fp8_scale", "rp_fp8_quantize",
     "rp_fp8_scale_quantize", "rp_fp8_attn_fwd", "rp_fp8_attn_workspace_bytes",
-    "rp_fp8_attn_fwd_split", "rp_fp8_gemm", "rp_fp8_transpose",
+    "rp_fp8_attn_fwd_split", "rp_fp8_rmsnorm_quant_workspace_bytes",
+    "rp_fp8_rmsnorm_scale_quantize", "rp_fp8_gemm", "rp_fp8_transpose",
     "rp_selftest_e4m3", "rp_selftest_scale",
 )
 
@@ -76,6 +80,12 @@ def _declare(L: ctypes.CDLL) -> None:
     L.rp_fp8_attn_fwd_split.restype = _int
     L.rp_fp8_attn_fwd_split.argtypes = (list(L.rp_fp8_attn_fwd.argtypes[:-1])
                                         + [_int, _vp, _sz, _vp])
+    L.rp_fp8_rmsnorm_quant_workspace_bytes.restype = _sz
+    L.rp_fp8_rmsnorm_quant_workspace_bytes.argtypes = [_i64, _i64, _i64, _i64, _int]
+    L.rp_fp8_rmsnorm_scale_quantize.restype = _int
+    L.rp_fp8_rmsnorm_scale_quantize.argtypes = [_vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
+                                                _vp, _f32, _vp, _vp, _int, _int, _vp, _vp, _vp,
+                                                _sz, _vp]
     L.rp_fp8_gemm.restype = _int
     L.rp_fp8_gemm.argtypes = [_vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _f32, _f32,
                               _vp, _vp, _vp]

@@ -1,0 +1,315 @@
+// Fused QK-norm (+ rotary embedding) + amax scaling + e4m3fn quantization.
+//
+// The step right before the FP8 path in the Cosmos/Wan attention processors
+// (reference docs/walkthroughs/02-architecture.md:114-123) is
+//     q = norm_q(q); k = norm_k(k)                 RMSNorm over the head dim
+//     q, k = apply_rotary_emb(q, rope), ...(k)     optional
+// followed by the quantizer of rp_quant.hip.  As separate passes that is one
+// extra read and write of Q and K (4 B/element) per op.  Here the normalised
+// (and rotated) row is recomputed inside both quantizer passes from the raw
+// input, so the whole prologue moves 5 B/element, like the plain quantizer.
+//
+// Per row of D elements, in the operation order of torch's RMSNorm with
+// weight w (diffusers' RMSNorm: fp32 math, result cast to the weight dtype
+// before the weight multiply) and of diffusers' apply_rotary_emb(use_real):
+//   ss   = sum over d of x_d^2        fp32; each thread sums its 8 elements
+//                                     in order, then a butterfly over the
+//                                     row's D/8 threads (xor D/16 ... 1)
+//   r    = 1 / sqrt(ss * (1/D) + eps) IEEE sqrt and divide (two roundings)
+//   n_d  = bf16(x_d * r)              then, with a weight, bf16(n_d * w_d)
+//   y_d  = bf16(n_d * cos_d + rot(n)_d * sin_d)      three fp32 roundings
+//          rot(n) = (-n[D/2:], n[:D/2]) for RP_ROPE_HALF,
+//                   (-n_1, n_0, -n_3, n_2, ...) for RP_ROPE_INTERLEAVED
+// and y is then scaled and quantized exactly as rp_fp8_scale_quantize does
+// (dequant = bf16(max(amax|y|, bf16(1e-6)) / 425.6), code = e4m3fn RNE of
+// clamp(y * RN(1/dequant), +-448)).  No step is contracted into an FMA
+// (`#pragma clang fp contract(off)`), so every rounding above happens.
+
+#include "rp_common.h"
+
+namespace rp {
+namespace {
+
+constexpr int kPThreads = 256;
+constexpr int64_t kPElemsPerBlock = 16384;
+
+struct PParams {
+  const uint16_t* x;
+  int64_t B, H, S, D;
+  int64_t sb, sh, ss;
+  const uint16_t* weight;  // bf16 [D] or null
+  float eps;
+  const float* cosv;       // fp32 [S, D] or null
+  const float* sinv;
+  int64_t rows_per_group;  // S (per (b, h)) or B*H*S (per tensor)
+  int64_t rpb;             // rows per block
+  int64_t nbg;             // blocks per group
+};
+
+// fp32 -> nearest-even bf16 value, held in fp32 (v_cvt_pk_bf16_f32)
+__device__ __forceinline__ float bf16r(float f) { return (float)(__bf16)f; }
+
+// The normalised (and rotated) 8 elements [8c, 8c+8) of the row at `xrow`,
+// each exactly a bf16 value held in fp32.  All D/8 threads of the row call
+// this together (the sum of squares and the half rotation cross threads).
+// The rotary layout is a template parameter: with it as a runtime branch,
+// hipcc 7.2 merged the two layouts' code so that the interleaved path
+// skipped its own sign flips (rotated with stale registers).
+template <int D, int ROPE>
+__device__ __forceinline__ void prologue_row(const PParams& p, const uint16_t* xrow, int64_t s,
+                                             int c, float (&y)[8]) {
+#pragma clang fp contract(off)
+  const uint4 v = *reinterpret_cast<const uint4*>(xrow + 8 * c);
+  const uint32_t w4[4] = {v.x, v.y, v.z, v.w};
+  float x[8];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    x[2 * i] = bf16_to_f32(w4[i] & 0xffffu);
+    x[2 * i + 1] = bf16_to_f32(w4[i] >> 16);
+  }
+  float ss = x[0] * x[0];
+#pragma unroll
+  for (int i = 1; i < 8; ++i) ss = ss + x[i] * x[i];
+#pragma unroll
+  for (int o = D / 16; o >= 1; o >>= 1) ss = ss + shfl_xor(ss, o);
+  const float r = 1.0f / __builtin_sqrtf(ss * (1.0f / D) + p.eps);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) y[i] = bf16r(x[i] * r);
+  if (p.weight != nullptr) {
+    const uint4 wv = *reinterpret_cast<const uint4*>(p.weight + 8 * c);
+    const uint32_t ww[4] = {wv.x, wv.y, wv.z, wv.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      y[2 * i] = bf16r(y[2 * i] * bf16_to_f32(ww[i] & 0xffffu));
+      y[2 * i + 1] = bf16r(y[2 * i + 1] * bf16_to_f32(ww[i] >> 16));
+    }
+  }
+  if constexpr (ROPE == RP_ROPE_NONE) return;
+  float rot[8];
+  if constexpr (ROPE == RP_ROPE_HALF) {
+    // partner elements d +- D/2 live in thread c ^ (D/16)
+    const bool lo = c < D / 16;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float o = shfl_xor(y[i], D / 16);
+      rot[i] = lo ? -o : o;
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; i += 2) {
+      rot[i] = -y[i + 1];
+      rot[i + 1] = y[i];
+    }
+  }
+  const float4* cp = reinterpret_cast<const float4*>(p.cosv + s * D + 8 * c);
+  const float4* sp = reinterpret_cast<const float4*>(p.sinv + s * D + 8 * c);
+  const float4 c0 = cp[0], c1 = cp[1], s0 = sp[0], s1 = sp[1];
+  const float cs[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+  const float sn[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const float a = y[i] * cs[i];
+    const float b = rot[i] * sn[i];
+    y[i] = bf16r(a + b);
+  }
+}
+
+// Row iteration shared by both passes: block blk covers rows
+// [first, first + nrows) of group g; thread t works on row offset t / (D/8)
+// and 8-element chunk t % (D/8), stepping by the rows a block covers at once.
+template <int D, typename F>
+__device__ __forceinline__ void for_rows(const PParams& p, F&& fn) {
+  constexpr int TPR = D / 8;
+  constexpr int STEP = kPThreads / TPR;
+  const int64_t blk = blockIdx.x;
+  const int64_t g = blk / p.nbg;
+  const int64_t first = (blk - g * p.nbg) * p.rpb;
+  const int64_t nrows = min(p.rpb, p.rows_per_group - first);
+  const int c = threadIdx.x % TPR;
+  for (int64_t k = threadIdx.x / TPR; k < nrows; k += STEP) {
+    const int64_t r = g * p.rows_per_group + first + k;  // global row bh*S + s
+    const int64_t bh = r / p.S, s = r - bh * p.S;
+    const uint16_t* xrow = p.x + (bh / p.H) * p.sb + (bh % p.H) * p.sh + s * p.ss;
+    fn(r, bh, s, xrow, c);
+  }
+}
+
+template <int D, int ROPE>
+__global__ __launch_bounds__(kPThreads) void prologue_amax_kernel(PParams p, uint32_t* partial) {
+  uint32_t m = 0;
+  for_rows<D>(p, [&](int64_t, int64_t, int64_t s, const uint16_t* xrow, int c) {
+    float y[8];
+    prologue_row<D, ROPE>(p, xrow, s, c, y);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) m = umax32(m, (__float_as_uint(y[i]) >> 16) & 0x7fffu);
+  });
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) m = umax32(m, (uint32_t)shfl_xor((int)m, o));
+  __shared__ uint32_t wmax[kPThreads / kWave];
+  if ((threadIdx.x & (kWave - 1)) == 0) wmax[threadIdx.x / kWave] = m;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    uint32_t r = wmax[0];
+#pragma unroll
+    for (int w = 1; w < kPThreads / kWave; ++w) r = umax32(r, wmax[w]);
+    partial[blockIdx.x] = r;
+  }
+}
+
+__global__ __launch_bounds__(kPThreads) void prologue_finalize_kernel(const uint32_t* partial,
+                                                                      int64_t nbg,
+                                                                      float* dequant) {
+  const int64_t g = blockIdx.x;
+  uint32_t m = 0;
+  for (int64_t i = threadIdx.x; i < nbg; i += kPThreads) m = umax32(m, partial[g * nbg + i]);
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) m = umax32(m, (uint32_t)shfl_xor((int)m, o));
+  __shared__ uint32_t wmax[kPThreads / kWave];
+  if ((threadIdx.x & (kWave - 1)) == 0) wmax[threadIdx.x / kWave] = m;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    uint32_t r = wmax[0];
+#pragma unroll
+    for (int w = 1; w < kPThreads / kWave; ++w) r = umax32(r, wmax[w]);
+    dequant[g] = dequant_from_amax_bits(r);
+  }
+}
+
+template <int D, int ROPE>
+__global__ __launch_bounds__(kPThreads) void prologue_quant_kernel(PParams p,
+                                                                   const float* dequant,
+                                                                   int per_bh, uint8_t* codes) {
+  for_rows<D>(p, [&](int64_t r, int64_t bh, int64_t s, const uint16_t* xrow, int c) {
+    float y[8];
+    prologue_row<D, ROPE>(p, xrow, s, c, y);
+    const float qm = 1.0f / dequant[per_bh ? bh : 0];
+    uint2 o;
+    o.x = pack4_e4m3(clamp_e4m3(y[0] * qm), clamp_e4m3(y[1] * qm), clamp_e4m3(y[2] * qm),
+                     clamp_e4m3(y[3] * qm));
+    o.y = pack4_e4m3(clamp_e4m3(y[4] * qm), clamp_e4m3(y[5] * qm), clamp_e4m3(y[6] * qm),
+                     clamp_e4m3(y[7] * qm));
+    *reinterpret_cast<uint2*>(codes + r * D + 8 * c) = o;
+  });
+}
+
+int launch_check(const char* what) {
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) {
+    rp_set_error("%s: launch failed: %s", what, hipGetErrorString(e));
+    return RP_ERR_LAUNCH;
+  }
+  return RP_OK;
+}
+
+template <int D, int ROPE>
+int run_prologue(const PParams& p, int64_t ngroups, float* dequant, uint8_t* codes, int per_bh,
+                 uint32_t* partial, hipStream_t st) {
+  const unsigned blocks = (unsigned)(ngroups * p.nbg);
+  hipLaunchKernelGGL((prologue_amax_kernel<D, ROPE>), dim3(blocks), dim3(kPThreads), 0, st, p,
+                     partial);
+  int rc = launch_check("rmsnorm_quantize(amax)");
+  if (rc) return rc;
+  hipLaunchKernelGGL(prologue_finalize_kernel, dim3((unsigned)ngroups), dim3(kPThreads), 0, st,
+                     partial, p.nbg, dequant);
+  rc = launch_check("rmsnorm_quantize(finalize)");
+  if (rc) return rc;
+  hipLaunchKernelGGL((prologue_quant_kernel<D, ROPE>), dim3(blocks), dim3(kPThreads), 0, st, p,
+                     dequant, per_bh, codes);
+  return launch_check("rmsnorm_quantize(apply)");
+}
+
+}  // namespace
+}  // namespace rp
+
+using namespace rp;
+
+extern "C" size_t rp_fp8_rmsnorm_quant_workspace_bytes(int64_t B, int64_t H, int64_t S, int64_t D,
+                                                       int granularity) {
+  if (B <= 0 || H <= 0 || S <= 0 || (D != 64 && D != 128)) return 0;
+  if (granularity != RP_SCALE_PER_BH && granularity != RP_SCALE_PER_TENSOR) return 0;
+  const int64_t ngroups = granularity == RP_SCALE_PER_BH ? B * H : 1;
+  const int64_t rows = B * H * S / ngroups;
+  const int64_t rpb = kPElemsPerBlock / D;
+  return (size_t)(ngroups * ((rows + rpb - 1) / rpb)) * sizeof(uint32_t);
+}
+
+extern "C" int rp_fp8_rmsnorm_scale_quantize(const void* x, int64_t B, int64_t H, int64_t S,
+                                             int64_t D, int64_t sb, int64_t sh, int64_t ss,
+                                             const void* weight, float eps, const float* rope_cos,
+                                             const float* rope_sin, int rope_mode,
+                                             int granularity, float* dequant_out, uint8_t* codes,
+                                             void* workspace, size_t workspace_bytes,
+                                             void* stream) {
+  if (x == nullptr || dequant_out == nullptr || codes == nullptr) {
+    rp_set_error("rmsnorm_quantize: null pointer");
+    return RP_ERR_INVALID_ARGUMENT;
+  }
+  if (B <= 0 || H <= 0 || S <= 0) {
+    rp_set_error("rmsnorm_quantize: non-positive shape B=%lld H=%lld S=%lld", (long long)B,
+                 (long long)H, (long long)S);
+    return RP_ERR_INVALID_ARGUMENT;
+  }
+  if (D != 64 && D != 128) {
+    rp_set_error("rmsnorm_quantize: head dim %lld not in {64, 128}", (long long)D);
+    return RP_ERR_UNSUPPORTED;
+  }
+  if (granularity != RP_SCALE_PER_BH && granularity != RP_SCALE_PER_TENSOR) {
+    rp_set_error("rmsnorm_quantize: unknown granularity %d", granularity);
+    return RP_ERR_INVALID_ARGUMENT;
+  }
+  if (rope_mode != RP_ROPE_NONE && rope_mode != RP_ROPE_HALF && rope_mode != RP_ROPE_INTERLEAVED) {
+    rp_set_error("rmsnorm_quantize: unknown rope_mode %d", rope_mode);
+    return RP_ERR_INVALID_ARGUMENT;
+  }
+  if (rope_mode != RP_ROPE_NONE && (rope_cos == nullptr || rope_sin == nullptr)) {
+    rp_set_error("rmsnorm_quantize: rope_mode %d needs cos and sin tables", rope_mode);
+    return RP_ERR_INVALID_ARGUMENT;
+  }
+  if (!(eps >= 0.0f) || eps == __builtin_inff()) {
+    rp_set_error("rmsnorm_quantize: eps=%g must be finite and >= 0", (double)eps);
+    return RP_ERR_INVALID_ARGUMENT;
+  }
+  const uintptr_t align = reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(weight) |
+                          (uintptr_t)(sb * 2) | (uintptr_t)(sh * 2) | (uintptr_t)(ss * 2) |
+                          reinterpret_cast<uintptr_t>(rope_cos) |
+                          reinterpret_cast<uintptr_t>(rope_sin) |
+                          reinterpret_cast<uintptr_t>(codes);
+  if (align % 16 != 0) {
+    rp_set_error("rmsnorm_quantize: x, weight, strides, tables and codes must be 16-byte aligned");
+    return RP_ERR_UNSUPPORTED;
+  }
+  const size_t need = rp_fp8_rmsnorm_quant_workspace_bytes(B, H, S, D, granularity);
+  if (workspace == nullptr || workspace_bytes < need) {
+    rp_set_error("rmsnorm_quantize: workspace of %zu bytes needed, got %zu", need,
+                 workspace_bytes);
+    return RP_ERR_WORKSPACE;
+  }
+  const int64_t ngroups = granularity == RP_SCALE_PER_BH ? B * H : 1;
+  PParams p{};
+  p.x = static_cast<const uint16_t*>(x);
+  p.B = B; p.H = H; p.S = S; p.D = D; p.sb = sb; p.sh = sh; p.ss = ss;
+  p.weight = static_cast<const uint16_t*>(weight);
+  p.eps = eps;
+  p.cosv = rope_cos; p.sinv = rope_sin;
+  p.rows_per_group = B * H * S / ngroups;
+  p.rpb = kPElemsPerBlock / D;
+  p.nbg = (p.rows_per_group + p.rpb - 1) / p.rpb;
+  if (ngroups * p.nbg > 0x7fffffffLL) {
+    rp_set_error("rmsnorm_quantize: grid too large");
+    return RP_ERR_UNSUPPORTED;
+  }
+  uint32_t* partial = static_cast<uint32_t*>(workspace);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int per_bh = granularity == RP_SCALE_PER_BH;
+  auto run = [&](auto d_c) {
+    constexpr int DD = decltype(d_c)::value;
+    if (rope_mode == RP_ROPE_HALF)
+      return run_prologue<DD, RP_ROPE_HALF>(p, ngroups, dequant_out, codes, per_bh, partial, st);
+    if (rope_mode == RP_ROPE_INTERLEAVED)
+      return run_prologue<DD, RP_ROPE_INTERLEAVED>(p, ngroups, dequant_out, codes, per_bh,
+                                                   partial, st);
+    return run_prologue<DD, RP_ROPE_NONE>(p, ngroups, dequant_out, codes, per_bh, partial, st);
+  };
+  if (D == 128) return run(std::integral_constant<int, 128>{});
+  return run(std::integral_constant<int, 64>{});
+}

@@ -151,6 +151,93 @@ def scale_quantize(x: torch.Tensor, granularity: Granularity = "bh",
     return dq, codes
 
 
+_ROPE = {None: C.RP_ROPE_NONE, "half": C.RP_ROPE_HALF, "interleaved": C.RP_ROPE_INTERLEAVED}
+
+
+def rmsnorm_scale_quantize(x: torch.Tensor, weight: torch.Tensor | None = None,
+                           eps: float = 1e-6,
+                           rope: tuple[torch.Tensor, torch.Tensor] | None = None,
+                           rope_layout: Literal["half", "interleaved"] = "half",
+                           granularity: Granularity = "bh") -> tuple[torch.Tensor, torch.Tensor]:
+    """(dequant scales, BHSD codes) of RMSNorm(x) [* weight] [rotated], fused.
+
+    The attention processors' ``norm_q``/``norm_k`` (RMSNorm over the head
+    dim, fp32 math; reference docs/walkthroughs/02-architecture.md:114-123)
+    and, with ``rope = (cos, sin)`` fp32 (S, D) tables, diffusers'
+    ``apply_rotary_emb(use_real=True)`` ("half" pairs d with d +- D/2, as
+    ``use_real_unbind_dim=-2``; "interleaved" pairs 2k with 2k+1), computed
+    inside the quantizer's two passes: the normalised tensor never reaches
+    HBM.  ``x`` is (B, H, S, D) bf16 with a unit stride on D.
+    """
+    _check_bf16("x", x)
+    if x.dim() != 4:
+        raise ValueError("x must be (B, H, S, D)")
+    B, H, S, D, sb, sh, ss = _bhsd_view(x)
+    w_ptr = None
+    if weight is not None:
+        _check_bf16("weight", weight)
+        if weight.shape != (D,) or not weight.is_contiguous():
+            raise ValueError(f"weight must be a contiguous ({D},) bf16 vector")
+        w_ptr = weight.data_ptr()
+    mode = _ROPE[rope_layout if rope is not None else None]
+    cos_ptr = sin_ptr = None
+    if rope is not None:
+        cos, sin = rope
+        for name, t in (("cos", cos), ("sin", sin)):
+            _check_cuda(name, t)
+            if t.dtype != torch.float32 or t.shape != (S, D) or not t.is_contiguous():
+                raise ValueError(f"{name} must be a contiguous float32 ({S}, {D}) table")
+        cos_ptr, sin_ptr = cos.data_ptr(), sin.data_ptr()
+    g = _GRAN[granularity]
+    dq = torch.empty(B * H if granularity == "bh" else 1, dtype=torch.float32, device=x.device)
+    codes = torch.empty((B, H, S, D), dtype=torch.uint8, device=x.device)
+    ws_bytes = C.lib().rp_fp8_rmsnorm_quant_workspace_bytes(B, H, S, D, g)
+    ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=x.device)
+    C.check(C.lib().rp_fp8_rmsnorm_scale_quantize(
+        x.data_ptr(), B, H, S, D, sb, sh, ss, w_ptr, float(eps), cos_ptr, sin_ptr, mode, g,
+        dq.data_ptr(), codes.data_ptr(), ws.data_ptr(), ws.numel(), _stream(x)),
+        "rp_fp8_rmsnorm_scale_quantize")
+    return dq, codes.view(torch.float8_e4m3fn)
+
+
+def fp8_flash_attention_qknorm(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *,
+                               norm_q_weight: torch.Tensor | None = None,
+                               norm_k_weight: torch.Tensor | None = None, eps: float = 1e-6,
+                               rope_q: tuple[torch.Tensor, torch.Tensor] | None = None,
+                               rope_k: tuple[torch.Tensor, torch.Tensor] | None = None,
+                               rope_layout: Literal["half", "interleaved"] = "half",
+                               causal: bool = False, scale: float | None = None,
+                               granularity: Granularity = "bh", out: torch.Tensor | None = None,
+                               out_dtype: torch.dtype | None = None,
+                               kv_splits: int | None = None) -> torch.Tensor:
+    """``fp8_flash_attention`` on pre-norm Q and K: the attention processor's
+    QK-RMSNorm (and rotary embedding) runs fused into Q's and K's quantizers
+    (``rmsnorm_scale_quantize``); V is quantized as usual.  Same result as
+    normalising (and rotating) Q and K in torch first, up to the summation
+    order of the RMSNorm's mean (see rp_prologue.hip)."""
+    for name, t in (("q", q), ("k", k), ("v", v)):
+        _check_bf16(name, t)
+    if q.dim() != 4 or k.dim() != 4 or v.dim() != 4:
+        raise ValueError("q, k, v must be 4-D (B, H, S, D)")
+    B, H, Sq, D = q.shape
+    if k.shape != v.shape or k.shape[0] != B or k.shape[1] != H or k.shape[3] != D:
+        raise ValueError(f"shape mismatch: q {tuple(q.shape)}, k {tuple(k.shape)}, "
+                         f"v {tuple(v.shape)}")
+    if D not in SUPPORTED_HEAD_DIMS:
+        raise ValueError(f"head_dim {D} not in compiled tile shapes {sorted(SUPPORTED_HEAD_DIMS)}")
+    if scale is None:
+        scale = 1.0 / math.sqrt(D)
+    qs, q8 = rmsnorm_scale_quantize(q, norm_q_weight, eps, rope_q, rope_layout, granularity)
+    ks, k8 = rmsnorm_scale_quantize(k, norm_k_weight, eps, rope_k, rope_layout, granularity)
+    vs, vt8 = scale_quantize(v, granularity, "bhds")
+    Skv = k.shape[2]
+    if kv_splits is None:
+        kv_splits = tuned_kv_splits(B, H, Sq, Skv, D, causal)
+    return attention_fp8(q8.view(torch.uint8), k8.view(torch.uint8), vt8.view(torch.uint8),
+                         qs, ks, vs, scale, out=out, out_dtype=out_dtype or q.dtype,
+                         causal=causal, kv_splits=kv_splits)
+
+
 def _round_up(v: int, m: int) -> int:
     return (v + m - 1) // m * m
 

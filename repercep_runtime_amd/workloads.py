@@ -101,11 +101,14 @@ def rmsnorm_heads(x: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:
 
 
 def attn_inputs(cfg: AttnConfig, device: str | torch.device = "cpu",
-                heads: int | None = None) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+                heads: int | None = None, normalize: bool = True
+                ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
     """Seeded (Q, K, V) bf16 tensors in (B, H, S, D) layout on ``device``.
 
     ``heads`` limits H (the first heads of the same stream are *not*
     reproduced by a smaller H; use it only for standalone samples).
+    ``normalize=False`` leaves out the config's QK RMSNorm (for a caller
+    that fuses it into the quantizer).
     """
     dev = torch.device(device)
     gen = torch.Generator(device=dev).manual_seed(cfg.seed)
@@ -113,7 +116,7 @@ def attn_inputs(cfg: AttnConfig, device: str | torch.device = "cpu",
     q = _randn_bf16(gen, (cfg.B, H, cfg.Sq, cfg.D), dev)
     k = _randn_bf16(gen, (cfg.B, H, cfg.Skv, cfg.D), dev)
     v = _randn_bf16(gen, (cfg.B, H, cfg.Skv, cfg.D), dev)
-    if cfg.rmsnorm_qk:
+    if cfg.rmsnorm_qk and normalize:
         q = rmsnorm_heads(q)
         k = rmsnorm_heads(k)
     return q, k, v

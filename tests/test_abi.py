@@ -117,3 +117,38 @@ def test_quantizer_argument_checks() -> None:
     assert L.rp_fp8_scale(None, 1, 1, 16, 64, 1024, 1024, 64, 0, FAKE, FAKE, 4096, None) == 1
     assert L.rp_fp8_scale_quantize(FAKE, 1, 1, 16, 64, 1024, 1024, 64, 5, FAKE, FAKE, 0, 0,
                                    FAKE, 4096, None) != 0
+
+
+def _norm(L, **kw) -> int:
+    a = dict(x=FAKE, B=1, H=2, S=64, D=128, sb=2 * 64 * 128, sh=64 * 128, ss=128, w=None,
+             eps=1e-6, cos=None, sin=None, rope=0, gran=0, dq=FAKE, codes=FAKE, ws=FAKE,
+             nbytes=1 << 20, stream=None)
+    a.update(kw)
+    return L.rp_fp8_rmsnorm_scale_quantize(*a.values())
+
+
+@pytest.mark.parametrize("kw,status,msg", [
+    (dict(x=None), 1, "null pointer"),
+    (dict(D=96), 2, "head dim"),
+    (dict(S=0), 1, "non-positive"),
+    (dict(gran=5), 1, "granularity"),
+    (dict(rope=3), 1, "rope_mode"),
+    (dict(rope=1), 1, "cos and sin"),
+    (dict(eps=-1.0), 1, "eps"),
+    (dict(eps=float("inf")), 1, "eps"),
+    (dict(ss=127), 2, "aligned"),
+    (dict(nbytes=0), 3, "workspace"),
+])
+def test_rmsnorm_quantize_argument_checks(kw: dict, status: int, msg: str) -> None:
+    L = _capi.lib()
+    assert _norm(L, **kw) == status
+    assert msg in L.rp_last_error().decode()
+
+
+def test_rmsnorm_workspace_sizing() -> None:
+    L = _capi.lib()
+    # one partial per 16384 elements of a group: 64 rows x 128 per (b, h) -> 1 block each
+    assert L.rp_fp8_rmsnorm_quant_workspace_bytes(1, 2, 64, 128, 0) == 2 * 4
+    assert L.rp_fp8_rmsnorm_quant_workspace_bytes(1, 2, 64, 128, 1) == 1 * 4
+    assert L.rp_fp8_rmsnorm_quant_workspace_bytes(1, 40, 75600, 128, 0) == 40 * 591 * 4
+    assert L.rp_fp8_rmsnorm_quant_workspace_bytes(1, 2, 64, 96, 0) == 0
