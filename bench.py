@@ -277,6 +277,7 @@ def bench_gemm(args, cfg) -> dict:
     gemm_ms = sum(e[1].elapsed_time(e[2]) for e in evs) / len(evs)
     quant_ms = sum(e[0].elapsed_time(e[1]) for e in evs) / len(evs)
     tf = cfg.flops / (gemm_ms * 1e-3) / 1e12
+    library = _library_gemm(args, cfg, a, wt8, sw, out) if args.library_gemm else None
     return {
         "metric": "FP8 scaled GEMM TFLOP/s (Wan FFN up-projection)",
         "value": round(cfg.flops / (step_ms * 1e-3) / 1e12, 2), "unit": "TFLOP/s",
@@ -291,7 +292,39 @@ def bench_gemm(args, cfg) -> dict:
                      "kernel": "gemm256_kernel", "kernel_ms": round(gemm_ms, 4)},
         "quantize": {"ms": round(quant_ms, 4),
                      "achieved_GBps": round(5 * cfg.M * cfg.K / (quant_ms * 1e-3) / 1e9, 1)},
+        **({"library_gemm": library} if library else {}),
     }
+
+
+def _library_gemm(args, cfg, a, wt8, sw, out) -> dict:
+    """Time the vendor library's FP8 GEMM (torch._scaled_mm, hipBLASLt on
+    ROCm) on the same operands and scales, for comparison only; also report
+    how far its bf16 output is from this build's."""
+    import torch
+
+    from repercep_runtime_amd import ops
+
+    sa, a8 = ops.scale_quantize(a, "tensor", "bhsd")
+    ops.fp8_gemm(a8.view(torch.uint8), wt8, sa, sw, b_transposed=True, out=out)
+    A = a8.view(torch.float8_e4m3fn).reshape(cfg.M, cfg.K)
+    B = wt8.view(torch.float8_e4m3fn).t()
+    run = lambda: torch._scaled_mm(A, B, scale_a=sa.reshape(()), scale_b=sw.reshape(()),
+                                   out_dtype=torch.bfloat16)
+    for _ in range(args.warmup):
+        ref = run()
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+    torch.cuda.synchronize()
+    ev[0].record()
+    for _ in range(args.steps):
+        ref = run()
+    ev[1].record()
+    torch.cuda.synchronize()
+    ms = ev[0].elapsed_time(ev[1]) / args.steps
+    diff = (ref.float() - out.float()).abs()
+    return {"op": "torch._scaled_mm", "ms": round(ms, 4),
+            "TFLOPs": round(cfg.flops / (ms * 1e-3) / 1e12, 2),
+            "max_abs_diff_vs_ours": float(diff.max()),
+            "max_abs_out": float(out.float().abs().max())}
 
 
 def main() -> int:
@@ -306,6 +339,9 @@ def main() -> int:
                     help="run one device-to-device copy of this many MiB first, so a "
                          "rocprofv3 --pmc FETCH_SIZE/WRITE_SIZE run can scale the counters "
                          "against a plain copy of known size")
+    ap.add_argument("--library-gemm", action="store_true",
+                    help="c4_wan_ffn_up only: also time the vendor library's FP8 GEMM "
+                         "(torch._scaled_mm) on the same operands, for comparison")
     ap.add_argument("--cpu-budget", type=float, default=12.0,
                     help="seconds of CPU work for the cpu_baseline sample (0 disables)")
     args = ap.parse_args()

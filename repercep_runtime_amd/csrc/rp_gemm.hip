@@ -12,14 +12,16 @@
 //
 // * gemm256_kernel (K a multiple of 64, the production shapes): 256 x 256
 //   block tiles on v_mfma_f32_32x32x64_f8f6f4, four waves of 128 x 128 with
-//   their accumulators in AGPRs, operands streamed into a 4-stage LDS ring
-//   by direct-to-LDS loads three K slices ahead.
+//   their accumulators in AGPRs, operands streamed into two LDS stages of
+//   128-byte K slices by direct-to-LDS loads one slice ahead.
 // * gemm_kernel (any K multiple of 16): 256 x 128 block tiles on
 //   v_mfma_f32_16x16x128_f8f6f4, operands staged through VGPRs into a
 //   double-buffered, XOR-swizzled LDS tile, K tail zero-filled.
 //
 // Both remap workgroups so that those resident on one XCD cover a compact
 // patch of C and share operand rows in that XCD's L2.
+
+#include <type_traits>
 
 #include "rp_common.h"
 
@@ -195,21 +197,23 @@ void gemm_kernel(GemmArgs g) {
 // The kernel for K a multiple of 64: 256 x 256 block tiles on
 // v_mfma_f32_32x32x64_f8f6f4, four waves (one per SIMD) of 128 x 128 each,
 // accumulators in AGPRs.  Operands reach LDS by global_load_lds_dwordx4 (no
-// VGPR staging) through a ring of kG2Stages K slices of 64 bytes, issued
-// three slices ahead; each LDS row carries a 16-byte pad granule so the
-// 16-lane ds_read_b128 groups are conflict-free.  The MFMA computes C^T
-// tiles (A operand = rows of B^T, B operand = rows of A), so each lane ends
-// with 4 consecutive output columns of one row per register group: one
-// 8-byte bf16 store.
+// VGPR staging) in K slices of 128 bytes -- eight lanes read one row's whole
+// cache line -- double-buffered: slice k+2 loads while slices k and k+1 are
+// read, with one wait and barrier per slice.  Each slice is two MFMA depths
+// (sub-slices of 64 bytes); operands are double-buffered in registers a
+// sub-slice ahead.  LDS rows are unpadded; the eight 16-byte granules of a
+// row are XOR-swizzled by (row >> 1) & 7, so the 16-lane ds_read_b128 groups
+// are conflict-free.  The MFMA computes C^T tiles (A operand = rows of B^T,
+// B operand = rows of A), so each lane ends with 4 consecutive output
+// columns of one row per register group: one 8-byte bf16 store.
 constexpr int kG2Threads = 256;
 constexpr int kG2Tile = 256;                        // BM = BN
-constexpr int kG2K = 64;                            // K bytes per slice = MFMA depth
-constexpr int kG2Pitch = kG2K + 16;                 // LDS row pitch
-constexpr int kG2Gran = kG2Pitch / 16;              // 16-byte granules per row (odd)
+constexpr int kG2K = 128;                           // K bytes per slice (two MFMA depths)
+constexpr int kG2Sub = 64;                          // K bytes per MFMA (a sub-slice)
+constexpr int kG2Pitch = kG2K;                      // LDS row pitch (no pad)
 constexpr int kG2Half = kG2Tile * kG2Pitch;         // A (or B^T) part of a stage
 constexpr int kG2Stage = 2 * kG2Half;
-constexpr int kG2Stages = 4;
-constexpr int kG2Ahead = kG2Stages - 1;             // slices in flight
+constexpr int kG2Stages = 2;
 constexpr int kG2Loads = kG2Stage / 1024 / 4;       // 1 KiB loads per wave per slice
 constexpr int kG2ALoads = kG2Half / 1024 / 4;       // of which A
 static_assert(kG2Half % 4096 == 0, "A and B^T parts split evenly over the waves");
@@ -217,16 +221,27 @@ static_assert(kG2Stages * kG2Stage <= 160 * 1024, "LDS");
 
 #pragma clang diagnostic push
 #pragma clang diagnostic ignored "-Winline-asm"
-// 16 bytes global -> LDS (lane i lands at lds_block + 16*i; lds_block
-// wave-uniform).  Inline asm keeps the load out of the compiler's waitcnt
-// bookkeeping, which would otherwise order every later ds_read behind it;
-// the kernel waits for its loads explicitly (vmcnt) before the barrier that
-// precedes their first read.  Nothing else in this kernel uses M0.
-__device__ __forceinline__ void g2_gload_lds16(const void* src, uint32_t lds_block) {
-  const uint32_t base = __builtin_amdgcn_readfirstlane(lds_block);
-  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
+// 16 bytes global -> LDS: lane i reads base + voff_i and lands at
+// lds_block + 16*i.  base (64-bit) and lds_block are wave-uniform and go in
+// SGPRs ("saddr" form: no per-lane 64-bit address arithmetic per load).
+// Inline asm keeps the load out of the compiler's waitcnt bookkeeping,
+// which would otherwise order every later ds_read behind it; the kernel
+// waits for its loads explicitly (vmcnt) before the barrier that precedes
+// their first read.  Nothing else in this kernel uses M0.
+__device__ __forceinline__ void g2_gload_lds16_s(const void* base, uint32_t voff,
+                                                 uint32_t lds_block) {
+  // readfirstlane states the uniformity where the compiler cannot prove it
+  // (and folds away where it can).  It returns int: each half is widened
+  // through uint32_t, since a sign-extended low word would corrupt the
+  // high half of the address.
+  const uint64_t b = reinterpret_cast<uint64_t>(base);
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)b);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(b >> 32));
+  const uint64_t sb = ((uint64_t)hi << 32) | (uint64_t)lo;
+  const uint32_t m0v = (uint32_t)__builtin_amdgcn_readfirstlane((int)lds_block);
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
                :
-               : "v"(src), "s"(base)
+               : "v"(voff), "s"(reinterpret_cast<const void*>(sb)), "s"(m0v)
                : "memory", "m0");
 }
 #pragma clang diagnostic pop
@@ -242,8 +257,8 @@ __device__ __forceinline__ f32x16 mfma_32x32x64(const i32x8& a, const i32x8& b, 
   return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, 0, 0, 0, 0, 0, 0);
 }
 
-__device__ __forceinline__ i32x8 g2_op(const uint8_t* p) {
-  return cat8(*reinterpret_cast<const i32x4*>(p), *reinterpret_cast<const i32x4*>(p + 16));
+__device__ __forceinline__ i32x8 g2_op(const uint8_t* p, int h0, int h1) {
+  return cat8(*reinterpret_cast<const i32x4*>(p + h0), *reinterpret_cast<const i32x4*>(p + h1));
 }
 
 // two fp32 -> packed bf16 with v_cvt_pk_bf16_f32 (round to nearest even)
@@ -261,15 +276,16 @@ void gemm256_kernel(GemmArgs g) {
   __shared__ __attribute__((aligned(1024))) uint8_t smem[kG2Stages * kG2Stage];
   const uint32_t smem_lds = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)smem;
 
-  // XCD-aware remap, then a column-major walk over 8-tile-tall bands of C
-  // so that workgroups resident together share B^T rows (and A rows across
-  // neighbouring bands) in L2.
+  // XCD-aware remap, then a column-major walk over 4-tile-tall bands of C:
+  // the 32 workgroups resident on one XCD cover a 4 x 8 patch and share
+  // its A and B^T rows in that XCD's L2 (4-tall measured best of 1, 2, 4,
+  // 8 and 16 at the C4 shape).
   const int nwork = g.tiles_m * g.tiles_n;
   const int w = blockIdx.x;
   const int per = nwork >> 3, rem = nwork & 7;
   const int xcd = w & 7;
   const int L = xcd * per + min(xcd, rem) + (w >> 3);
-  constexpr int kBand = 8;
+  constexpr int kBand = 4;
   const int band_tiles = kBand * g.tiles_n;
   const int band = L / band_tiles;
   const int in_band = L - band * band_tiles;
@@ -285,8 +301,10 @@ void gemm256_kernel(GemmArgs g) {
   const int lq = lane & 31, lg = lane >> 5;
   const int wm = wave >> 1, wn = wave & 1;
 
-  // this lane's direct-to-LDS loads: load n fills LDS KiB block n*4 + wave
+  // This lane's direct-to-LDS loads: load n fills LDS KiB block n*4 + wave
   // of a stage; blocks [0, kG2Half/1024) hold A rows, the rest B^T rows.
+  // Eight consecutive lanes read one row's 128-byte K slice (a whole cache
+  // line).  LDS granule `slot` of row r holds K granule slot ^ ((r >> 1) & 7).
   // Rows past M or N re-read the last row (their results are not stored).
   const uint8_t* abase = g.a + m0 * g.lda;
   const uint8_t* bbase = g.bt + n0 * g.ldb;
@@ -296,8 +314,8 @@ void gemm256_kernel(GemmArgs g) {
     const int blk = n * 4 + wave;
     const bool is_a = n < kG2ALoads;
     const int p = (is_a ? blk : blk - kG2Half / 1024) * kWave + lane;
-    const int row = p / kG2Gran, slot = p % kG2Gran;
-    const int s16 = (slot < kG2K / 16 ? slot : 0) * 16;
+    const int row = p >> 3, slot = p & 7;
+    const int s16 = (slot ^ ((row >> 1) & 7)) * 16;
     if (is_a) {
       const int64_t r = min(m0 + row, g.M - 1) - m0;
       gofs[n] = (uint32_t)(r * g.lda + s16);
@@ -306,31 +324,33 @@ void gemm256_kernel(GemmArgs g) {
       gofs[n] = (uint32_t)(r * g.ldb + s16);
     }
   }
-  const int nk = (int)(g.K / kG2K);
-  // load n of slice kk (slices past the end are not issued)
+  // K in 64-byte sub-slices; slices are pairs of them.  With K % 128 == 64
+  // the last slice is a half: its lanes for K granules 4..7 re-read granules
+  // 0..3 (in bounds), and the sub-slice they fill is never used.
+  const int nsub = (int)(g.K / kG2Sub);
+  const int nslice = (nsub + 1) >> 1;
+  const int half_tail = nsub & 1;
+  // bit 2 of this lane's K granule is (slot bit 2) ^ (block parity), and a
+  // block's parity is the wave's: the same for all of its loads
+  const uint32_t tail_back = (uint32_t)(((lane >> 2) ^ wave) & 1) * 64;
   auto issue = [&](int n, int kk) __attribute__((always_inline)) {
-    const uint8_t* src = (n < kG2ALoads ? abase : bbase) + (int64_t)kk * kG2K + gofs[n];
-    g2_gload_lds16(src, smem_lds + (uint32_t)((kk % kG2Stages) * kG2Stage + (n * 4 + wave) * 1024));
-  };
-  // wait until slice kk has landed, with the slices after it (up to
-  // kG2Ahead - 1 of them, issued since) still in flight
-  auto wait_slice = [&](int kk) __attribute__((always_inline)) {
-    const int later = min(kG2Ahead - 1, nk - 1 - kk);
-    if (later >= 2) g2_wait_vmem<2 * kG2Loads>();
-    else if (later == 1) g2_wait_vmem<kG2Loads>();
-    else g2_wait_vmem<0>();
+    uint32_t off = gofs[n];
+    if (half_tail && kk == nslice - 1) off -= tail_back;
+    const uint8_t* src = (n < kG2ALoads ? abase : bbase) + (int64_t)kk * kG2K;
+    g2_gload_lds16_s(src, off,
+                     smem_lds + (uint32_t)((kk & 1) * kG2Stage + (n * 4 + wave) * 1024));
   };
 
-  // per-lane operand offsets inside a stage
-  const int a_off = (wm * 128 + lq) * kG2Pitch + 32 * lg;
-  const int b_off = kG2Half + (wn * 128 + lq) * kG2Pitch + 32 * lg;
-  auto read_ops = [&](G2Ops& o, int kk) __attribute__((always_inline)) {
-    const uint8_t* st = smem + (kk % kG2Stages) * kG2Stage;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) o.a[i] = g2_op(st + a_off + 32 * i * kG2Pitch);
-#pragma unroll
-    for (int j = 0; j < 4; ++j) o.b[j] = g2_op(st + b_off + 32 * j * kG2Pitch);
-  };
+  // Per-lane operand offsets inside a stage: row lq of each 32-row block,
+  // K granules 4h + 2lg and 4h + 2lg + 1 of sub-slice h at their swizzled
+  // slots (the swizzle term (row >> 1) & 7 depends on lq only, as block
+  // bases are multiples of 32 rows).  Sixteen consecutive lanes then hit
+  // sixteen distinct 16-byte bank groups.
+  const int swz = (lq >> 1) & 7;
+  const int h00 = ((2 * lg) ^ swz) * 16, h01 = ((2 * lg + 1) ^ swz) * 16;
+  const int h10 = ((4 + 2 * lg) ^ swz) * 16, h11 = ((4 + 2 * lg + 1) ^ swz) * 16;
+  const int a_off = (wm * 128 + lq) * kG2Pitch;
+  const int b_off = kG2Half + (wn * 128 + lq) * kG2Pitch;
 
   f32x16 acc[4][4];
 #pragma unroll
@@ -338,41 +358,58 @@ void gemm256_kernel(GemmArgs g) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = f32x16{};
 
-  for (int s = 0; s < kG2Ahead; ++s)
-    if (s < nk) {
+  // prologue: slices 0 and 1 in flight, wait for slice 0, read sub-slice 0
 #pragma unroll
-      for (int n = 0; n < kG2Loads; ++n) issue(n, s);
-    }
-  wait_slice(0);
+  for (int n = 0; n < kG2Loads; ++n) issue(n, 0);
+  if (nslice > 1) {
+#pragma unroll
+    for (int n = 0; n < kG2Loads; ++n) issue(n, 1);
+    g2_wait_vmem<kG2Loads>();
+  } else {
+    g2_wait_vmem<0>();
+  }
   __syncthreads();
+  G2Ops o0, o1;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) o0.a[i] = g2_op(smem + a_off + 32 * i * kG2Pitch, h00, h01);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) o0.b[j] = g2_op(smem + b_off + 32 * j * kG2Pitch, h00, h01);
 
-  // One slice: 16 MFMAs on `cur`; the loads of slice kk+3 go out between
-  // them; after the 12th MFMA the wave waits for slice kk+1 and meets the
-  // others at the barrier, then reads slice kk+1's operands into `nxt` while
-  // its last four MFMAs run.  Slice kk+3 overwrites the stage of slice kk-1,
-  // whose reads all finished before the previous iteration's barrier.
-  auto step = [&](int kk, G2Ops& cur, G2Ops& nxt) __attribute__((always_inline)) {
-    const bool load = kk + kG2Ahead < nk;
+  // Sub-step (kk, H): 16 MFMAs on `cur` (sub-slice 2kk + H) with the operand
+  // reads of the next sub-slice into `nxt` spread between them.  Sub-step
+  // (kk, 1) begins with the slice's one wait and barrier: slice kk+1 (read
+  // from here on) has landed, and every wave has finished reading slice kk,
+  // whose stage then takes slice kk+2's loads, one between consecutive MFMAs.
+  auto sub = [&](int kk, auto Hc, G2Ops& cur, G2Ops& nxt) __attribute__((always_inline)) {
+    constexpr int H = decltype(Hc)::value;
+    const int u = 2 * kk + H;
+    const bool more = u + 1 < nsub;
+    const bool load = H == 1 && kk + 2 < nslice;
+    if (H == 1) {
+      if (more) g2_wait_vmem<0>();
+      __syncthreads();
+    }
+    // the next sub-slice: (kk, 1) when H == 0, else (kk + 1, 0)
+    const uint8_t* st = smem + ((H == 0 ? kk : kk + 1) & 1) * kG2Stage;
+    const int r0 = H == 0 ? h10 : h00, r1 = H == 0 ? h11 : h01;
 #pragma unroll
     for (int t = 0; t < 16; ++t) {
       const int i = t >> 2, j = t & 3;
       acc[i][j] = mfma_32x32x64(cur.b[j], cur.a[i], acc[i][j]);
-      if (t < kG2Loads && load) issue(t, kk + kG2Ahead);
-      if (t == 11) {
-        if (kk + 1 < nk) wait_slice(kk + 1);
-        __syncthreads();
-        if (kk + 1 < nk) read_ops(nxt, kk + 1);
+      if (load) issue(t, kk + 2);
+      if ((t & 1) == 0 && more) {
+        const int v = t >> 2;
+        if ((t & 2) == 0) nxt.a[v] = g2_op(st + a_off + 32 * v * kG2Pitch, r0, r1);
+        else nxt.b[v] = g2_op(st + b_off + 32 * v * kG2Pitch, r0, r1);
       }
     }
   };
-  G2Ops o0, o1;
-  read_ops(o0, 0);
-  int kk = 0;
-  for (; kk + 1 < nk; kk += 2) {
-    step(kk, o0, o1);
-    step(kk + 1, o1, o0);
+  const int nfull = nsub >> 1;
+  for (int kk = 0; kk < nfull; ++kk) {
+    sub(kk, std::integral_constant<int, 0>{}, o0, o1);
+    sub(kk, std::integral_constant<int, 1>{}, o1, o0);
   }
-  if (kk < nk) step(kk, o0, o1);
+  if (half_tail) sub(nfull, std::integral_constant<int, 0>{}, o0, o1);
 
   // epilogue: C[m][n] = bf16(acc * a_scale * b_scale)
   const float scale = (g.a_dev ? *g.a_dev : g.a_scale) * (g.b_dev ? *g.b_dev : g.b_scale);
@@ -479,9 +516,9 @@ extern "C" int rp_fp8_gemm(const uint8_t* a8, const uint8_t* bt8, void* c, int64
   g.a = a8; g.bt = bt8; g.c = static_cast<uint16_t*>(c);
   g.M = M; g.N = N; g.K = K; g.lda = lda; g.ldb = ldb; g.ldc = ldc;
   g.a_scale = a_scale; g.b_scale = b_scale; g.a_dev = a_scale_dev; g.b_dev = b_scale_dev;
-  // the large-tile kernel reads whole 64-byte K slices and keeps tile
+  // the large-tile kernel reads whole 64-byte K sub-slices and keeps tile
   // offsets in 32 bits
-  if (K % kG2K == 0 && lda * (int64_t)kG2Tile < (int64_t)1 << 32 &&
+  if (K % kG2Sub == 0 && lda * (int64_t)kG2Tile < (int64_t)1 << 32 &&
       ldb * (int64_t)kG2Tile < (int64_t)1 << 32)
     return launch_gemm256(g, static_cast<hipStream_t>(stream));
   return launch_gemm<256, 128>(g, static_cast<hipStream_t>(stream));
