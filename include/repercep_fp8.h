@@ -88,7 +88,7 @@ int rp_fp8_scale(const void* x, int64_t B, int64_t H, int64_t S, int64_t D,
  * .contiguous() that follows it (fp8_flash_attn.py:526-528).
  * layout RP_LAYOUT_BHSD: codes (B, H, S, D) contiguous, ld ignored.
  * layout RP_LAYOUT_BHDS: codes (B, H, D, ld), ld >= S and ld % 128 == 0,
- *                        D % 64 == 0; columns [S, ld) are written as 0. */
+ *                        D % 32 == 0; columns [S, ld) are written as 0. */
 int rp_fp8_quantize(const void* x, int64_t B, int64_t H, int64_t S, int64_t D,
                     int64_t sb, int64_t sh, int64_t ss, int granularity,
                     const float* dequant, uint8_t* codes, int layout, int64_t ld,
@@ -117,7 +117,8 @@ int rp_fp8_scale_quantize(const void* x, int64_t B, int64_t H, int64_t S, int64_
  *         finite and >= 0
  *   out : (B, H, Sq, D) logical, element (b,h,s,d) at
  *         out + b*osb + h*osh + s*oss + d (elements of out_dtype)
- *   D in {64, 128}; mask per RP_MASK_*; Sq, Skv >= 1. */
+ *   D in {32, 64, 128, 256} (the reference's compiled set,
+ *   fp8_flash_attn.py:516); mask per RP_MASK_*; Sq, Skv >= 1. */
 int rp_fp8_attn_fwd(const uint8_t* q8, const uint8_t* k8, const uint8_t* vt8, int64_t ldv,
                     const float* q_scale, const float* k_scale, const float* v_scale,
                     int scale_stride, float sm_scale, void* out, int out_dtype,

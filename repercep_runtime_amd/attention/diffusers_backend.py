@@ -34,7 +34,7 @@ REPERCEP_FP8_BACKEND_NAME = "repercep_fp8"
 #: Sequence-length crossover below which the FP8 path is not taken
 #: (the reference's measured gfx942 crossover, diffusers_backend.py:44).
 _FP8_MIN_SEQ_LEN = int(os.environ.get("REPERCEP_FP8_MIN_SEQ_LEN", "4096"))
-_FP8_SUPPORTED_HEAD_DIMS = frozenset({64, 128})
+_FP8_SUPPORTED_HEAD_DIMS = frozenset({32, 64, 128, 256})   # diffusers_backend.py:49
 #: Shortest key sequence the cross-attention branch takes (text encoders
 #: give 512 tokens in Wan/Cosmos).
 _FP8_MIN_KV_LEN = 128

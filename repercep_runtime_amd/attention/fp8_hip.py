@@ -9,7 +9,7 @@ kernels in librepercep_fp8.so instead of the gfx942 Triton kernel.
 ``supports()`` differences, all widenings of what the hardware path can do:
 * cross-attention (seq_len_kv != seq_len_q) is accepted -- the reference
   gates it out (fp8_triton.py:90-91) although its kernel body handles it;
-* head dims are the ones compiled for gfx950 (64, 128);
+* head dims: the reference's set (32, 64, 128, 256);
 * dtype BF16 only (the quantizer reads bf16; FP16 callers stay on the floor).
 """
 

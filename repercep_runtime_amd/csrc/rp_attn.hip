@@ -77,6 +77,9 @@ struct AttnArgs {
   int scale_stride;
   int B, H, Sq, Skv;
   int mask, prefix, suffix;
+  int D;          // head dim: row length of Q and K, rows of V^T per head
+  int dv_halves;  // 2: each query block runs as two workgroups, one per half
+                  // of V^T / O (head dim 256), both computing the same S
   int n_qblocks;
   int n_work;
   // key splits: split j covers keys [j*split_tiles*128, (j+1)*split_tiles*128)
@@ -109,28 +112,35 @@ __device__ __forceinline__ float max3f(float a, float b, float c) {
   return r;
 }
 
-template <int D, int NW>
+// Tile geometry for QK depth DK (the head dim) and PV width DV (the O^T rows
+// one workgroup produces: DK, or half of it when a head of 256 is split over
+// two workgroups).
+template <int DK, int DV, int NW>
 struct Geo {
   static constexpr int THREADS = NW * kWave;
-  static constexpr int KCH = D / 16;                 // 16-byte chunks per K row
-  static constexpr int KSTEPS = D / 64;              // 64-deep MFMA steps over D
-  static constexpr int ETILES = D / 32;              // 32-row tiles of O^T
+  static constexpr int KSTEPS = DK >= 64 ? DK / 64 : 1;  // 64-deep MFMA steps over DK
+  static constexpr int KROW = 64 * KSTEPS;               // K bytes per LDS row (>= DK)
+  static constexpr int KVALID = DK / 16;                 // granules of a K row in HBM
+  static constexpr int ETILES = DV / 32;                 // 32-row tiles of O^T
   // LDS pitches carry one 16-byte pad granule per row: the granule count per
-  // row (9 or 5) is odd, so 16 consecutive rows start in 16 distinct 16-byte
-  // bank groups and every operand read is conflict-free without swizzling.
-  static constexpr int K_PITCH = D + 16;
+  // row (5, 9 or 17) is odd, so 16 consecutive rows start in 16 distinct
+  // 16-byte bank groups and every operand read is conflict-free without
+  // swizzling.  With DK = 32 the upper half of each K row is padding too.
+  static constexpr int K_PITCH = KROW + 16;
   static constexpr int V_PITCH = kBlockN + 16;
   static constexpr int K_GRAN = K_PITCH / 16;   // granules per K row
   static constexpr int V_GRAN = V_PITCH / 16;
   static constexpr int K_BYTES = kBlockN * K_PITCH;
-  static constexpr int V_BYTES = D * V_PITCH;
-  static constexpr int K_BLKS = kBlockN * K_GRAN / 64;  // wave instructions per K tile
-  static constexpr int V_BLKS = D * V_GRAN / 64;
+  static constexpr int K_BLKS = kBlockN * K_GRAN / 64;   // wave instructions per K tile
+  static constexpr int V_BLKS = (DV * V_GRAN + 63) / 64;
+  static constexpr int V_BYTES = V_BLKS * 1024;          // DV rows, rounded up to a KiB
   static constexpr int K_STAGES = 2;               // ping-pong layout:
   static constexpr int V_STAGES = 3;               // V^T lives one step longer
   static constexpr int LDS_BYTES = K_STAGES * K_BYTES + V_STAGES * V_BYTES;
-  static_assert(D == 64 || D == 128, "head dim");
-  static_assert(K_BLKS * 64 == kBlockN * K_GRAN && V_BLKS * 64 == D * V_GRAN, "whole KiB blocks");
+  static_assert(DK == 32 || DK == 64 || DK == 128 || DK == 256, "head dim");
+  static_assert(DV % 32 == 0 && DV <= 128 && DV <= DK, "PV width");
+  static_assert(K_BLKS * 64 == kBlockN * K_GRAN, "whole KiB K blocks");
+  static_assert(LDS_BYTES <= 160 * 1024, "LDS");
 };
 
 // Key (row inside the 128-key tile) that row rho of the S^T A operand of key
@@ -186,12 +196,15 @@ __device__ __forceinline__ float xhalf_sum(float x) {
 // contiguous KiB (64 granules) of LDS; granule p of a block is row p / GRAN,
 // slot p % GRAN.  K rows are stored in S^T A-operand order (LDS row 32h + rho
 // holds key_of(h, rho)); V^T rows are d.  Pad slots re-load the row's first
-// granule (valid memory, never read).  The tile's K_BLKS + V_BLKS blocks, K
-// first, are dealt round-robin to the NL loading waves; a wave left one block
-// short repeats its own previous block (same source, same destination).
-template <int D, int NL>
+// granule (valid memory; with DK = 32 the K pad slots are read, times the
+// zero upper half of Q, so they must hold finite codes, which the row's own
+// codes are).  V^T rows past DV in the last, rounded-up block re-load row
+// DV-1 and are never read.  The tile's K_BLKS + V_BLKS blocks, K first, are
+// dealt round-robin to the NL loading waves; a wave left one block short
+// repeats its own previous block (same source, same destination).
+template <int DK, int DV, int NL>
 struct TileLoads {
-  using G = Geo<D, 8>;
+  using G = Geo<DK, DV, 8>;
   static constexpr int T = G::K_BLKS + G::V_BLKS;
   static constexpr int N = (T + NL - 1) / NL;
   uint32_t off[N];  // K: key*D + granule; V^T: d*ldv + granule (bytes, per lane)
@@ -199,10 +212,10 @@ struct TileLoads {
   int blk[N];       // block index (wave-uniform)
 };
 
-template <int D, int NL>
-__device__ __forceinline__ TileLoads<D, NL> tile_loads(int64_t ldv, int wave, int lane) {
-  using G = Geo<D, 8>;
-  using TL = TileLoads<D, NL>;
+template <int DK, int DV, int NL>
+__device__ __forceinline__ TileLoads<DK, DV, NL> tile_loads(int64_t ldv, int wave, int lane) {
+  using G = Geo<DK, DV, 8>;
+  using TL = TileLoads<DK, DV, NL>;
   TL o;
 #pragma unroll
   for (int n = 0; n < TL::N; ++n) {
@@ -214,10 +227,10 @@ __device__ __forceinline__ TileLoads<D, NL> tile_loads(int64_t ldv, int wave, in
       const int row = p / G::K_GRAN, slot = p % G::K_GRAN;
       const int key = key_of(row >> 5, row & 31);
       o.key[n] = key;
-      o.off[n] = (uint32_t)(key * D + (slot < D / 16 ? slot : 0) * 16);
+      o.off[n] = (uint32_t)(key * DK + (slot < G::KVALID ? slot : 0) * 16);
     } else {
       const int p = (b - G::K_BLKS) * kWave + lane;
-      const int d = p / G::V_GRAN, slot = p % G::V_GRAN;
+      const int d = min(p / G::V_GRAN, DV - 1), slot = p % G::V_GRAN;
       o.key[n] = 0;
       o.off[n] = (uint32_t)(d * ldv + (slot < kBlockN / 16 ? slot : 0) * 16);
     }
@@ -242,16 +255,18 @@ struct TileDst {
 // loops), so whether the slot is a K or a V^T block folds at compile time,
 // except for the one slot shared by both, where a wave-uniform select picks
 // it: no branches.
-template <int D, int NL, bool CLAMP>
-__device__ __forceinline__ void issue_slot(int n, const TileLoads<D, NL>& L, const TileDst& t) {
-  using G = Geo<D, 8>;
+template <int DK, int DV, int NL, bool CLAMP>
+__device__ __forceinline__ void issue_slot(int n, const TileLoads<DK, DV, NL>& L,
+                                           const TileDst& t) {
+  using G = Geo<DK, DV, 8>;
   const bool any_k = n * NL < G::K_BLKS;
-  const bool any_v = n * NL + NL - 1 >= G::K_BLKS || (n + 1) * NL > TileLoads<D, NL>::T;
+  const bool any_v =
+      n * NL + NL - 1 >= G::K_BLKS || (n + 1) * NL > TileLoads<DK, DV, NL>::T;
   const int b = L.blk[n];
   const uint32_t kdst = t.kst + (uint32_t)b * 1024u;
   const uint32_t vdst = t.vst + (uint32_t)(b - G::K_BLKS) * 1024u;
   if constexpr (CLAMP) {
-    const uint8_t* ksrc = t.kt + (L.off[n] - (uint32_t)(max(L.key[n] - t.klim, 0) * D));
+    const uint8_t* ksrc = t.kt + (L.off[n] - (uint32_t)(max(L.key[n] - t.klim, 0) * DK));
     const uint8_t* vsrc = t.vt + L.off[n];
     if (any_k && !any_v) {
       gload_lds16(ksrc, kdst);
@@ -304,17 +319,18 @@ __device__ __forceinline__ i32x8 lds_op(uint32_t lds_addr) {
 //   during PV:   partial row maxima of S^T(i) (MAX), 64 / NP scores per step.
 constexpr int kRing = 3;
 
-template <int D, bool LOADS, bool MAX>
+template <int DK, int DV, bool LOADS, bool MAX>
 __device__ __forceinline__ void mfma_phase(uint32_t kl, uint32_t vl,
-                                           const i32x8 (&qop)[D / 64], const i32x8 (&pop)[2],
-                                           f32x16 (&s)[4], f32x16 (&acc)[D / 32], float alpha_prev,
-                                           float (&mh)[8], const TileLoads<D, 4>& L,
+                                           const i32x8 (&qop)[Geo<DK, DV, 8>::KSTEPS],
+                                           const i32x8 (&pop)[2], f32x16 (&s)[4],
+                                           f32x16 (&acc)[DV / 32], float alpha_prev,
+                                           float (&mh)[8], const TileLoads<DK, DV, 4>& L,
                                            const TileDst& dst) {
-  using G = Geo<D, 8>;
+  using G = Geo<DK, DV, 8>;
   constexpr int NS = 4 * G::KSTEPS;   // S^T steps: ks outer, key tile hh inner
   constexpr int NP = 2 * G::ETILES;   // PV steps: k-half m outer, d tile e inner
   constexpr int N = NS + NP;
-  constexpr int NLD = TileLoads<D, 4>::N;
+  constexpr int NLD = TileLoads<DK, DV, 4>::N;
   constexpr int MX = 64 / NP;              // scores per partial max
   auto addr = [&](int t) -> uint32_t {
     if (t < NS) {
@@ -341,7 +357,8 @@ __device__ __forceinline__ void mfma_phase(uint32_t kl, uint32_t vl,
       s[hh] = mfma_32x32x64(op, qop[ks], ks == 0 ? f32x16{} : s[hh]);
       if constexpr (LOADS) {
 #pragma unroll
-        for (int n = t * NLD / NS; n < (t + 1) * NLD / NS; ++n) issue_slot<D, 4, false>(n, L, dst);
+        for (int n = t * NLD / NS; n < (t + 1) * NLD / NS; ++n)
+          issue_slot<DK, DV, 4, false>(n, L, dst);
       }
     } else {
       const int u = t - NS, e = u % G::ETILES, m = u / G::ETILES;
@@ -391,11 +408,12 @@ __device__ __forceinline__ void mfma_phase(uint32_t kl, uint32_t vl,
 // before barrier 2j.  Only group 0 loads: the slot in which a group issues
 // loads costs its SIMD VALU time, and in this slot the MFMA group, not the
 // softmax group, has VALU time to spare.
-template <int D, int OUT, bool WINDOW>
+template <int DK, int DV, int OUT, bool WINDOW>
 __global__ __launch_bounds__(512, 1)
 void attn_fwd_kernel(AttnArgs a) {
   constexpr int NW = 8;
-  using G = Geo<D, NW>;
+  using G = Geo<DK, DV, NW>;
+  constexpr int D = DK;
   constexpr int QROWS = 32;
   constexpr int BLOCK_M = QROWS * NW;
   __shared__ __attribute__((aligned(1024))) uint8_t smem[G::LDS_BYTES];
@@ -409,7 +427,12 @@ void attn_fwd_kernel(AttnArgs a) {
   const int w = blockIdx.x;
   const int per = a.n_work >> 3, rem = a.n_work & 7;
   const int xcd = w & 7;
-  const int L = xcd * per + min(xcd, rem) + (w >> 3);
+  const int L2 = xcd * per + min(xcd, rem) + (w >> 3);
+  // the two halves of a split query block are neighbours: same XCD, same
+  // K tiles in its L2
+  const int half = DV < DK ? L2 & 1 : 0;
+  const int L = DV < DK ? L2 >> 1 : L2;
+  const int dv_off = half * DV;  // first O column / V^T row of this workgroup
   const int per_bh = a.n_qblocks * a.kv_splits;
   const int bh = L / per_bh;
   const int qb = (L - bh * per_bh) / a.kv_splits;
@@ -429,7 +452,7 @@ void attn_fwd_kernel(AttnArgs a) {
 
   const uint8_t* qh = a.q + (int64_t)bh * a.Sq * D;
   const uint8_t* kh = a.k + (int64_t)bh * a.Skv * D;
-  const uint8_t* vh = a.vt + (int64_t)bh * D * a.ldv;
+  const uint8_t* vh = a.vt + ((int64_t)bh * D + dv_off) * a.ldv;
 
   const float q_scale = a.qs[bh * a.scale_stride];
   const float k_scale = a.ks[bh * a.scale_stride];
@@ -451,10 +474,13 @@ void attn_fwd_kernel(AttnArgs a) {
       const int q0 = q_block0 + tid;
       if (tid < BLOCK_M && q0 < a.Sq) {
         const int64_t row = ((int64_t)split * a.B * a.H + bh) * a.Sq + q0;
-        a.ws_ml[2 * row] = -__builtin_inff();
-        a.ws_ml[2 * row + 1] = 0.0f;
-        for (int d = 0; d < D; d += 4)
-          *reinterpret_cast<float4*>(a.ws_acc + row * D + d) = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        if (half == 0) {
+          a.ws_ml[2 * row] = -__builtin_inff();
+          a.ws_ml[2 * row + 1] = 0.0f;
+        }
+        for (int d = 0; d < DV; d += 4)
+          *reinterpret_cast<float4*>(a.ws_acc + row * D + dv_off + d) =
+              make_float4(0.0f, 0.0f, 0.0f, 0.0f);
       }
       return;
     }
@@ -462,7 +488,7 @@ void attn_fwd_kernel(AttnArgs a) {
 
   // Group 0's four waves issue every tile (see the schedule below); their
   // per-lane load offsets are fixed for the whole kernel.
-  const TileLoads<D, 4> tl = tile_loads<D, 4>(a.ldv, wave & 3, lane);
+  const TileLoads<DK, DV, 4> tl = tile_loads<DK, DV, 4>(a.ldv, wave & 3, lane);
   // first key of tile j of the range (see TileDst)
   auto tile_begin = [&](int j) {
     const int kv0 = kv_begin + j * kBlockN;
@@ -482,7 +508,7 @@ void attn_fwd_kernel(AttnArgs a) {
   if (group == 0) {
     const TileDst t0 = tile_dst(0, 0);
 #pragma unroll
-    for (int n = 0; n < TileLoads<D, 4>::N; ++n) issue_slot<D, 4, true>(n, tl, t0);
+    for (int n = 0; n < TileLoads<DK, DV, 4>::N; ++n) issue_slot<DK, DV, 4, true>(n, tl, t0);
   }
   // V^T stage 2 is read (times P = 0) by the first MFMA phase before tile 2
   // lands there: clear it so that no stale NaN code can reach the accumulator.
@@ -491,7 +517,11 @@ void attn_fwd_kernel(AttnArgs a) {
 
   // ---- Q^T operand (B operand of S^T), resident for the whole kernel
   i32x8 qop[G::KSTEPS];
-  {
+  if constexpr (DK < 64) {
+    // one 64-deep step over a 32-byte row: k-slot group 1 is zero padding
+    const i32x4* src = reinterpret_cast<const i32x4*>(qh + (int64_t)min(q, a.Sq - 1) * D);
+    qop[0] = lg == 0 ? cat8(src[0], src[1]) : i32x8{};
+  } else {
     const i32x4* src = reinterpret_cast<const i32x4*>(qh + (int64_t)min(q, a.Sq - 1) * D + 32 * lg);
 #pragma unroll
     for (int ks = 0; ks < G::KSTEPS; ++ks) qop[ks] = cat8(src[4 * ks], src[4 * ks + 1]);
@@ -546,7 +576,7 @@ void attn_fwd_kernel(AttnArgs a) {
       // under a window mask: such a tile takes its max after the phase, from
       // the masked scores.
       float mh[8];
-      mfma_phase<D, LOADS, !WINDOW>(kl, vl, qop, pop, s, acc, alpha, mh, tl, nxt);
+      mfma_phase<DK, DV, LOADS, !WINDOW>(kl, vl, qop, pop, s, acc, alpha, mh, tl, nxt);
       if (i < n_kb) {
         bool masked = tail;
         if (a.mask == RP_MASK_CAUSAL) masked |= kv0 + kBlockN - 1 > q_wave0;
@@ -576,11 +606,15 @@ void attn_fwd_kernel(AttnArgs a) {
         }
         float mx;
         if (!WINDOW && !(i == 0 && tile_begin(0) != kv0)) {
-          constexpr int NP = 2 * G::ETILES;
-          mx = max3f(mh[0], mh[1], mh[2]);
+          constexpr int NP = 2 * G::ETILES;   // partial maxima mh[0 .. NP)
+          if constexpr (NP == 2) {
+            mx = max3f(mh[0], mh[1], mh[1]);
+          } else {
+            mx = max3f(mh[0], mh[1], mh[2]);
   #pragma unroll
-          for (int j = 3; j + 1 < NP; j += 2) mx = max3f(mx, mh[j], mh[j + 1]);
-          if constexpr (NP % 2 == 0) mx = max3f(mx, mh[NP - 1], mh[NP - 1]);
+            for (int j = 3; j + 1 < NP; j += 2) mx = max3f(mx, mh[j], mh[j + 1]);
+            if constexpr (NP % 2 == 0) mx = max3f(mx, mh[NP - 1], mh[NP - 1]);
+          }
         } else {
           float mt[4];
   #pragma unroll
@@ -640,20 +674,21 @@ void attn_fwd_kernel(AttnArgs a) {
     // partial result of this key split, relative to its own running max
     if (q < a.Sq) {
       const int64_t row = ((int64_t)split * a.B * a.H + bh) * a.Sq + q;
-      float* dst = a.ws_acc + row * D;
+      float* dst = a.ws_acc + row * D + dv_off;
 #pragma unroll
       for (int e = 0; e < G::ETILES; ++e)
 #pragma unroll
         for (int i = 0; i < 4; ++i)
           *reinterpret_cast<float4*>(dst + 32 * e + 8 * i + 4 * lg) =
               make_float4(acc[e][4 * i], acc[e][4 * i + 1], acc[e][4 * i + 2], acc[e][4 * i + 3]);
-      if (lg == 0) *reinterpret_cast<float2*>(a.ws_ml + 2 * row) = make_float2(m_run, l);
+      if (lg == 0 && half == 0)
+        *reinterpret_cast<float2*>(a.ws_ml + 2 * row) = make_float2(m_run, l);
     }
     return;
   }
   const float inv = v_scale / l;
   if (q < a.Sq) {
-    const int64_t obase = (int64_t)b * a.osb + (int64_t)h * a.osh + (int64_t)q * a.oss;
+    const int64_t obase = (int64_t)b * a.osb + (int64_t)h * a.osh + (int64_t)q * a.oss + dv_off;
 #pragma unroll
     for (int e = 0; e < G::ETILES; ++e)
 #pragma unroll
@@ -721,13 +756,18 @@ void attn_combine_kernel(AttnArgs a) {
   }
 }
 
+// O^T rows one workgroup produces for head dim D
+template <int D>
+constexpr int kPVWidth = D > 128 ? 128 : D;
+
 template <int D, int OUT>
 void launch_fwd(const AttnArgs& a, hipStream_t st) {
+  constexpr int DV = kPVWidth<D>;
   const dim3 grid(a.n_work), block(512);
   if (a.mask != RP_MASK_NONE)
-    hipLaunchKernelGGL((attn_fwd_kernel<D, OUT, true>), grid, block, 0, st, a);
+    hipLaunchKernelGGL((attn_fwd_kernel<D, DV, OUT, true>), grid, block, 0, st, a);
   else
-    hipLaunchKernelGGL((attn_fwd_kernel<D, OUT, false>), grid, block, 0, st, a);
+    hipLaunchKernelGGL((attn_fwd_kernel<D, DV, OUT, false>), grid, block, 0, st, a);
 }
 
 constexpr int kBlockM = 32 * 8;  // query rows per workgroup
@@ -745,7 +785,9 @@ template <int D>
 int launch_attn(const AttnArgs& base, bool out_f32, hipStream_t st) {
   AttnArgs a = base;
   a.n_qblocks = (a.Sq + kBlockM - 1) / kBlockM;
-  const int64_t work = (int64_t)a.n_qblocks * a.B * a.H * a.kv_splits;
+  a.D = D;
+  a.dv_halves = D / kPVWidth<D>;
+  const int64_t work = (int64_t)a.n_qblocks * a.B * a.H * a.kv_splits * a.dv_halves;
   if (work > 0x7fffffff || (int64_t)a.B * a.H * a.Sq * (D / 4) > 0x7fffffffLL * 256) {
     rp_set_error("attn: grid too large");
     return RP_ERR_UNSUPPORTED;
@@ -794,8 +836,8 @@ int attn_setup(AttnArgs& a, const uint8_t* q8, const uint8_t* k8, const uint8_t*
     rp_set_error("attn: non-positive shape B=%d H=%d Sq=%d Skv=%d", B, H, Sq, Skv);
     return RP_ERR_INVALID_ARGUMENT;
   }
-  if (D != 64 && D != 128) {
-    rp_set_error("attn: head dim %d not in {64, 128}", D);
+  if (D != 32 && D != 64 && D != 128 && D != 256) {
+    rp_set_error("attn: head dim %d not in {32, 64, 128, 256}", D);
     return RP_ERR_UNSUPPORTED;
   }
   if (ldv < Skv || ldv % kBlockN != 0) {
@@ -851,8 +893,12 @@ int attn_setup(AttnArgs& a, const uint8_t* q8, const uint8_t* k8, const uint8_t*
 int attn_run(const AttnArgs& a, int D, int out_dtype, void* stream) {
   hipStream_t st = static_cast<hipStream_t>(stream);
   const bool f32 = out_dtype == RP_OUT_F32;
-  if (D == 128) return launch_attn<128>(a, f32, st);
-  return launch_attn<64>(a, f32, st);
+  switch (D) {
+    case 32: return launch_attn<32>(a, f32, st);
+    case 64: return launch_attn<64>(a, f32, st);
+    case 128: return launch_attn<128>(a, f32, st);
+    default: return launch_attn<256>(a, f32, st);
+  }
 }
 
 }  // namespace

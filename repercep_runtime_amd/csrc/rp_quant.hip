@@ -242,7 +242,8 @@ __global__ __launch_bounds__(kQThreads) void quant_apply_kernel(QParams p, const
 }
 
 // BHDS output: per head, codes[(bh*D + d)*ld + s]; columns [S, ld) zeroed.
-// Tile: 128 rows (s) x 64 columns (d).  Thread t loads rows 4*(t&31)+i,
+// Tile: 128 rows (s) x 64 columns (d), or 32 for the last block of a head
+// dim that is an odd multiple of 32.  Thread t loads rows 4*(t&31)+i,
 // column chunk t>>5 (8 elements), transposes its 4x8 codes in registers and
 // writes 8 dwords [d][s..s+3] into LDS; the tile then leaves as 64 rows of
 // 128 contiguous codes.
@@ -252,6 +253,7 @@ __global__ __launch_bounds__(kQThreads) void quant_apply_t_kernel(QParams p, con
   __shared__ __attribute__((aligned(16))) uint8_t tile[64 * 128];
   const int64_t s0 = (int64_t)blockIdx.x * 128;
   const int64_t d0 = (int64_t)blockIdx.y * 64;
+  const int dcols = (int)min((int64_t)64, p.D - d0);  // 64 or 32
   const int64_t bh = blockIdx.z;
   const float qm = 1.0f / dequant[per_bh ? bh : 0];
   const int64_t base = (bh / p.H) * p.sb + (bh % p.H) * p.sh + d0;
@@ -262,7 +264,7 @@ __global__ __launch_bounds__(kQThreads) void quant_apply_t_kernel(QParams p, con
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int64_t s = s0 + 4 * r4 + i;
-    if (s < p.S) {
+    if (s < p.S && c * 8 < dcols) {
       const uint4 v = *reinterpret_cast<const uint4*>(p.x + base + s * p.ss + c * 8);
       w[i][0] = quant4(v.x, v.y, qm);
       w[i][1] = quant4(v.z, v.w, qm);
@@ -292,6 +294,7 @@ __global__ __launch_bounds__(kQThreads) void quant_apply_t_kernel(QParams p, con
 #pragma unroll
   for (int k = 0; k < 2; ++k) {
     const int dr = (threadIdx.x >> 3) + 32 * k;
+    if (dr >= dcols) break;
     const int ch = threadIdx.x & 7;
     const uint4 v = *reinterpret_cast<const uint4*>(&tile[dr * 128 + ch * 16]);
     *reinterpret_cast<uint4*>(codes + (bh * p.D + d0 + dr) * ld + s0 + ch * 16) = v;
@@ -427,8 +430,8 @@ int launch_apply(const Plan& pl, const void* x, int64_t B, int64_t H, int64_t S,
     rp_set_error("quantize: unknown layout %d", layout);
     return RP_ERR_INVALID_ARGUMENT;
   }
-  if (D % 64 != 0 || ld < S || ld % 128 != 0) {
-    rp_set_error("quantize(BHDS): needs D %% 64 == 0 and ld >= S with ld %% 128 == 0 "
+  if (D % 32 != 0 || ld < S || ld % 128 != 0) {
+    rp_set_error("quantize(BHDS): needs D %% 32 == 0 and ld >= S with ld %% 128 == 0 "
                  "(D=%lld S=%lld ld=%lld)", (long long)D, (long long)S, (long long)ld);
     return RP_ERR_UNSUPPORTED;
   }
@@ -439,7 +442,7 @@ int launch_apply(const Plan& pl, const void* x, int64_t B, int64_t H, int64_t S,
     rp_set_error("quantize(BHDS): B*H=%lld exceeds the grid limit", (long long)(B * H));
     return RP_ERR_UNSUPPORTED;
   }
-  dim3 grid((unsigned)(ld / 128), (unsigned)(D / 64), (unsigned)(B * H));
+  dim3 grid((unsigned)(ld / 128), (unsigned)((D + 63) / 64), (unsigned)(B * H));
   hipLaunchKernelGGL(quant_apply_t_kernel, grid, dim3(kQThreads), 0, st, q, dequant, pl.per_bh,
                      codes, ld);
   return check_launch("quant_apply_t");
@@ -504,8 +507,8 @@ extern "C" int rp_fp8_scale_quantize(const void* x, int64_t B, int64_t H, int64_
   Plan pl;
   int rc = make_plan(x, B, H, S, D, sb, sh, ss, granularity, &pl);
   if (rc) return rc;
-  if (layout == RP_LAYOUT_BHDS && (D % 64 != 0 || ld < S || ld % 128 != 0)) {
-    rp_set_error("scale_quantize(BHDS): needs D %% 64 == 0 and ld >= S with ld %% 128 == 0");
+  if (layout == RP_LAYOUT_BHDS && (D % 32 != 0 || ld < S || ld % 128 != 0)) {
+    rp_set_error("scale_quantize(BHDS): needs D %% 32 == 0 and ld >= S with ld %% 128 == 0");
     return RP_ERR_UNSUPPORTED;
   }
   hipStream_t st = static_cast<hipStream_t>(stream);

@@ -30,7 +30,7 @@ from repercep_runtime_amd import tuning
 
 FP8_E4M3_MAX = 448.0
 #: head dims compiled into the attention kernel
-SUPPORTED_HEAD_DIMS = frozenset({64, 128})
+SUPPORTED_HEAD_DIMS = frozenset({32, 64, 128, 256})
 #: keys per tile of the attention kernel.  Numerically significant: the
 #: running max after each tile sets the grid P is quantized on.
 BLOCK_N = 128

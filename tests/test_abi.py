@@ -84,6 +84,8 @@ def _attn(L, **kw) -> int:
 @pytest.mark.parametrize("kw,status,msg", [
     (dict(q8=None), 1, "null pointer"),
     (dict(D=96), 2, "head dim"),
+    (dict(D=512), 2, "head dim"),
+    (dict(D=16), 2, "head dim"),
     (dict(Sq=0), 1, "non-positive"),
     (dict(ldv=100), 1, "ldv"),
     (dict(mask=7), 1, "unknown mask"),

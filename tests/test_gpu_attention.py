@@ -84,6 +84,15 @@ CASES = [
     ("causal_d128", 1, 2, 700, 700, 128, True),
     ("causal_d64", 1, 2, 513, 513, 64, True),
     ("tiny", 1, 1, 5, 7, 64, False),
+    # head dim 32: one 64-deep QK step whose upper k-slots are zero padding
+    ("self_ragged_d32", 1, 2, 600, 600, 32, False),
+    ("causal_d32", 2, 1, 300, 300, 32, True),
+    ("tiny_d32", 1, 1, 5, 7, 32, False),
+    # head dim 256: two workgroups per query block, one per half of V^T / O
+    ("self_ragged_d256", 1, 2, 700, 700, 256, False),
+    ("cross_d256", 1, 1, 300, 450, 256, False),
+    ("causal_d256", 1, 2, 513, 513, 256, True),
+    ("tiny_d256", 1, 1, 5, 7, 256, False),
 ]
 
 
@@ -143,6 +152,9 @@ SPLIT_CASES = [
     ("c5_prefix", 1, 32, 128, 640, 128, False, 512, 8, (2, 3, 5)),
     ("short_kv", 1, 2, 300, 100, 64, False, None, None, (4,)),   # one tile: no split
     ("two_tiles_ragged", 2, 1, 257, 131, 128, False, None, None, (2,)),
+    ("d256", 1, 2, 300, 1000, 256, False, None, None, (2, 8)),
+    ("d256_causal", 1, 1, 600, 600, 256, True, None, None, (3,)),
+    ("d32", 1, 2, 300, 1000, 32, False, None, None, (3,)),
 ]
 
 
