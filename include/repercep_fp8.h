@@ -46,6 +46,11 @@ extern "C" {
 /* Output element type of rp_fp8_attn_fwd. */
 #define RP_OUT_BF16 0
 #define RP_OUT_F32 1
+#define RP_OUT_F16 2
+
+/* Input element type of the quantizer entry points (x_dtype). */
+#define RP_DTYPE_BF16 0
+#define RP_DTYPE_F16 1
 
 /* Mask kinds of rp_fp8_attn_fwd. */
 /* rotary-embedding layouts of rp_fp8_rmsnorm_scale_quantize, as diffusers'
@@ -60,24 +65,29 @@ extern "C" {
                                 /* q sees suffix key j = kv - prefix iff          */
                                 /* j / suffix == q / suffix and j <= q            */
 
+/* 2: the quantizer entry points take x_dtype; RP_OUT_F16. */
 int rp_abi_version(void);
 const char* rp_status_string(int status);
 const char* rp_last_error(void);
 
 /* ---------------------------------------------------------- quantize
- * Input x: bf16 viewed as (B, H, S, D) with element strides sb, sh, ss for
- * the first three axes and unit stride along D.  D must be a multiple of 8.
+ * Input x: bf16 or fp16 (x_dtype RP_DTYPE_*) viewed as (B, H, S, D) with
+ * element strides sb, sh, ss for the first three axes and unit stride along
+ * D.  D must be a multiple of 8.
  *
  * rp_fp8_quant_workspace_bytes: device scratch the two-pass quantizer needs
  * (per-block partial maxima plus per-group multipliers).
  */
 size_t rp_fp8_quant_workspace_bytes(int64_t B, int64_t H, int64_t S, int64_t D, int granularity);
 
-/* Per-group dequant scales, dequant = bf16(max(amax|x|, bf16(1e-6)) / 425.6).
+/* Per-group dequant scales, computed in the input dtype as the reference's
+ * torch expression evaluates on the GPU:
+ *   bf16: dequant = bf16(max(amax|x|, bf16(1e-6)) / 425.6)
+ *   fp16: dequant = fp16(max(amax|x|, fp16(1e-6)) * fp32(1 / 425.6))
  * Replaces _per_bh_scale, kernels/triton_kernels/fp8_flash_attn_hopper.py:374-385
  * (OCP sibling of kernels/triton_kernels/fp8_flash_attn.py:425-436).
  * dequant_out: float[B*H] (RP_SCALE_PER_BH) or float[1] (RP_SCALE_PER_TENSOR). */
-int rp_fp8_scale(const void* x, int64_t B, int64_t H, int64_t S, int64_t D,
+int rp_fp8_scale(const void* x, int x_dtype, int64_t B, int64_t H, int64_t S, int64_t D,
                  int64_t sb, int64_t sh, int64_t ss, int granularity,
                  float* dequant_out, void* workspace, size_t workspace_bytes, void* stream);
 
@@ -89,14 +99,14 @@ int rp_fp8_scale(const void* x, int64_t B, int64_t H, int64_t S, int64_t D,
  * layout RP_LAYOUT_BHSD: codes (B, H, S, D) contiguous, ld ignored.
  * layout RP_LAYOUT_BHDS: codes (B, H, D, ld), ld >= S and ld % 128 == 0,
  *                        D % 32 == 0; columns [S, ld) are written as 0. */
-int rp_fp8_quantize(const void* x, int64_t B, int64_t H, int64_t S, int64_t D,
+int rp_fp8_quantize(const void* x, int x_dtype, int64_t B, int64_t H, int64_t S, int64_t D,
                     int64_t sb, int64_t sh, int64_t ss, int granularity,
                     const float* dequant, uint8_t* codes, int layout, int64_t ld,
                     void* stream);
 
 /* rp_fp8_scale followed by rp_fp8_quantize in one stream-ordered call
  * (the pair _per_bh_scale + _quantize at fp8_flash_attn.py:522-528). */
-int rp_fp8_scale_quantize(const void* x, int64_t B, int64_t H, int64_t S, int64_t D,
+int rp_fp8_scale_quantize(const void* x, int x_dtype, int64_t B, int64_t H, int64_t S, int64_t D,
                           int64_t sb, int64_t sh, int64_t ss, int granularity,
                           float* dequant_out, uint8_t* codes, int layout, int64_t ld,
                           void* workspace, size_t workspace_bytes, void* stream);
@@ -106,7 +116,8 @@ int rp_fp8_scale_quantize(const void* x, int64_t B, int64_t H, int64_t S, int64_
  * products on gfx950 e4m3 MFMAs, P re-quantized as e4m3fn(p * 448).
  * Replaces the launch of _fp8_flash_attn_fwd_impl,
  * kernels/triton_kernels/fp8_flash_attn.py:251-391 (launch :604-644) plus the
- * fp32->input-dtype cast at :645 (written directly as bf16 here).
+ * fp32->input-dtype cast at :645 (written directly as bf16 or fp16 here,
+ * one round to nearest even of the fp32 result, as that cast does).
  *   q8  : (B, H, Sq, D)  codes, contiguous
  *   k8  : (B, H, Skv, D) codes, contiguous
  *   vt8 : (B, H, D, ldv) codes, V transposed per head (RP_LAYOUT_BHDS),
@@ -194,9 +205,10 @@ int rp_fp8_transpose(const uint8_t* src, uint8_t* dst, int64_t R, int64_t C,
  * Device routines exposed so the tests can pin them exhaustively against
  * the CPU oracle.  They run the same device functions the kernels above use.
  * rp_selftest_e4m3: out[i] = e4m3fn code of clamp(x[i], -448, 448).
- * rp_selftest_scale: dequant[i] / qmul[i] from bf16 amax bit patterns. */
+ * rp_selftest_scale: dequant[i] / qmul[i] from bf16 or fp16 (x_dtype) amax
+ * bit patterns. */
 int rp_selftest_e4m3(const float* x, uint8_t* out, int64_t n, void* stream);
-int rp_selftest_scale(const uint16_t* amax_bits, float* dequant, float* qmul, int64_t n,
+int rp_selftest_scale(const uint16_t* amax_bits, int x_dtype, float* dequant, float* qmul, int64_t n,
                       void* stream);
 
 #ifdef __cplusplus

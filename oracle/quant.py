@@ -8,6 +8,13 @@ with the same torch CPU operations, so they inherit torch's dtype flow:
 * ``x.abs().amax()`` of a bf16 tensor is bf16, ``clamp(min=1e-6)`` clamps in
   bf16, and ``amax / (0.95*448)`` divides in fp32 and rounds back to bf16
   before ``.to(float32)``: the dequant scale carries bf16 precision.
+* fp16 input follows the same dtype flow in fp16, with one difference of
+  evaluation: on the GPU, torch's true-divide kernel computes
+  ``tensor / cpu_scalar`` as ``tensor * (1 / scalar)`` with the reciprocal
+  rounded to fp32 (ATen's BinaryDivTrueKernel), while its CPU kernel
+  divides.  For bf16 both forms give the same scale for every amax value;
+  for fp16 they differ on two values, so the fp16 scale is written out as
+  the GPU evaluates it: fp16(max(amax, fp16(1e-6)) * RN(1/425.6)).
 * ``1.0 / dequant`` is a correctly rounded fp32 reciprocal; the product with
   ``x.float()`` is one fp32 multiply; ``.to(float8_e4m3fn)`` rounds to
   nearest even.
@@ -20,9 +27,12 @@ the format definition (bias 7, 3 mantissa bits, S.1111.111 = NaN, max 448).
 
 Parity: pinned.  tests/test_oracle_quant.py checks the encoder against torch's
 cast over every sign/exponent/top-mantissa pattern with all rounding-relevant
-low bits, the scale formula over every bf16 amax value, the C restatement
-against this module bit for bit, and closed-form cases (zero groups,
-power-of-two scale invariance, clamp, NaN/Inf propagation).
+low bits, the scale formula over every bf16 and fp16 amax value (both
+evaluation forms), the C restatement against this module bit for bit, and
+closed-form cases (zero groups, power-of-two scale invariance, clamp, NaN/Inf
+propagation).  tests/test_gpu_quant.py checks the fp16 and bf16 scales
+against the reference expression evaluated by torch on the GPU, for every
+amax value.
 """
 
 from __future__ import annotations
@@ -48,6 +58,12 @@ def per_group_dequant(x: torch.Tensor, granularity: str = "bh",
     else:
         raise ValueError(f"unknown granularity {granularity!r}")
     amax = flat.amax(dim=1).clamp(min=1e-6)
+    if x.dtype == torch.float16:
+        # the GPU's evaluation of `amax / (0.95 * fp8_max)`: multiply by the
+        # fp32 reciprocal of the scalar, round to fp16
+        inv = (torch.tensor(1.0, dtype=torch.float32)
+               / torch.tensor(0.95 * fp8_max, dtype=torch.float32)).to(amax.device)
+        return (amax.to(torch.float32) * inv).to(torch.float16).to(torch.float32)
     return (amax / (0.95 * fp8_max)).to(torch.float32)
 
 
@@ -68,7 +84,7 @@ def quantize(x: torch.Tensor, dequant: torch.Tensor, granularity: str = "bh",
 
 
 def quantize_codes(x: torch.Tensor, granularity: str = "bh") -> tuple[np.ndarray, np.ndarray]:
-    """(dequant scales fp32, uint8 codes) for a bf16 tensor, OCP e4m3fn."""
+    """(dequant scales fp32, uint8 codes) for a bf16 or fp16 tensor, OCP e4m3fn."""
     dq = per_group_dequant(x, granularity)
     codes = quantize(x, dq, granularity).view(torch.uint8)
     return dq.numpy(), codes.numpy()

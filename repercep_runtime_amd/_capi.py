@@ -21,6 +21,9 @@ RP_LAYOUT_BHSD = 0
 RP_LAYOUT_BHDS = 1
 RP_OUT_BF16 = 0
 RP_OUT_F32 = 1
+RP_OUT_F16 = 2
+RP_DTYPE_BF16 = 0
+RP_DTYPE_F16 = 1
 RP_MASK_NONE = 0
 RP_MASK_CAUSAL = 1
 RP_MASK_SHARED_PREFIX = 2
@@ -63,14 +66,14 @@ def _declare(L: ctypes.CDLL) -> None:
     L.rp_fp8_quant_workspace_bytes.restype = _sz
     L.rp_fp8_quant_workspace_bytes.argtypes = [_i64, _i64, _i64, _i64, _int]
     L.rp_fp8_scale.restype = _int
-    L.rp_fp8_scale.argtypes = [_vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _int, _vp, _vp,
-                               _sz, _vp]
+    L.rp_fp8_scale.argtypes = [_vp, _int, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _int, _vp,
+                               _vp, _sz, _vp]
     L.rp_fp8_quantize.restype = _int
-    L.rp_fp8_quantize.argtypes = [_vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _int, _vp, _vp,
-                                  _int, _i64, _vp]
+    L.rp_fp8_quantize.argtypes = [_vp, _int, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _int,
+                                  _vp, _vp, _int, _i64, _vp]
     L.rp_fp8_scale_quantize.restype = _int
-    L.rp_fp8_scale_quantize.argtypes = [_vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _int, _vp,
-                                        _vp, _int, _i64, _vp, _sz, _vp]
+    L.rp_fp8_scale_quantize.argtypes = [_vp, _int, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
+                                        _int, _vp, _vp, _int, _i64, _vp, _sz, _vp]
     L.rp_fp8_attn_fwd.restype = _int
     L.rp_fp8_attn_fwd.argtypes = [_vp, _vp, _vp, _i64, _vp, _vp, _vp, _int, _f32, _vp, _int,
                                   _i64, _i64, _i64, _int, _int, _int, _int, _int, _int, _int,
@@ -94,7 +97,7 @@ def _declare(L: ctypes.CDLL) -> None:
     L.rp_selftest_e4m3.restype = _int
     L.rp_selftest_e4m3.argtypes = [_vp, _vp, _i64, _vp]
     L.rp_selftest_scale.restype = _int
-    L.rp_selftest_scale.argtypes = [_vp, _vp, _vp, _i64, _vp]
+    L.rp_selftest_scale.argtypes = [_vp, _int, _vp, _vp, _i64, _vp]
 
 
 def lib() -> ctypes.CDLL:

@@ -43,14 +43,17 @@ _FP8_MIN_KV_LEN = 128
 def _route_should_use_fp8(query: Any, key: Any, value: Any) -> bool:
     """Whether one (B, S, H, D) call goes to the FP8 kernels.
 
-    Same rules as the reference (diffusers_backend.py:52-79) -- BF16, head
-    dim in the compiled set, query length past the crossover -- except that
+    Same rules as the reference (diffusers_backend.py:52-79) -- BF16 or
+    FP16, head dim in the compiled set, query length past the crossover --
+    except that
     cross-attention (K/V sequence length != Q's) qualifies too, since the
     gfx950 kernel supports it.
     """
     import torch
 
-    if query.dtype != torch.bfloat16 or key.dtype != query.dtype or value.dtype != query.dtype:
+    if query.dtype not in (torch.bfloat16, torch.float16):   # diffusers_backend.py:69
+        return False
+    if key.dtype != query.dtype or value.dtype != query.dtype:
         return False
     if query.dim() != 4 or key.shape != value.shape:
         return False

@@ -10,7 +10,7 @@ kernels in librepercep_fp8.so instead of the gfx942 Triton kernel.
 * cross-attention (seq_len_kv != seq_len_q) is accepted -- the reference
   gates it out (fp8_triton.py:90-91) although its kernel body handles it;
 * head dims: the reference's set (32, 64, 128, 256);
-* dtype BF16 only (the quantizer reads bf16; FP16 callers stay on the floor).
+* dtypes BF16 and FP16, as the reference's (fp8_triton.py:85).
 """
 
 from __future__ import annotations
@@ -52,7 +52,7 @@ class FP8HipAttention:
     def supports(self, shape: AttentionShape, dtype: DType) -> bool:
         return (
             self._fn is not None
-            and dtype == DType.BF16
+            and dtype in (DType.BF16, DType.FP16)
             and shape.head_dim in self._head_dims
             and shape.kind in _SUPPORTED_KINDS
             and shape.seq_len_q >= 1

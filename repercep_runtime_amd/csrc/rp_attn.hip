@@ -91,7 +91,7 @@ struct AttnArgs {
 };
 
 // Output kinds of the attention kernel.
-constexpr int kOutBf16 = 0, kOutF32 = 1, kOutSplit = 2;
+constexpr int kOutBf16 = 0, kOutF32 = 1, kOutSplit = 2, kOutF16 = 3;
 
 __device__ __forceinline__ f32x16 mfma_32x32x64(const i32x8& a, const i32x8& b, const f32x16& c) {
   // cbsz = blgp = 0: both operands OCP e4m3; scale operands 0 select the
@@ -701,8 +701,13 @@ void attn_fwd_kernel(AttnArgs a) {
               make_float4(o0, o1, o2, o3);
         } else {
           uint2 pk;
-          pk.x = pack_bf16x2(o0, o1);
-          pk.y = pack_bf16x2(o2, o3);
+          if constexpr (OUT == kOutF16) {
+            pk.x = pack_f16x2(o0, o1);
+            pk.y = pack_f16x2(o2, o3);
+          } else {
+            pk.x = pack_bf16x2(o0, o1);
+            pk.y = pack_bf16x2(o2, o3);
+          }
           *reinterpret_cast<uint2*>(static_cast<uint16_t*>(a.out) + obase + d) = pk;
         }
       }
@@ -713,8 +718,9 @@ void attn_fwd_kernel(AttnArgs a) {
 // max, row sum and unnormalised output of split j (O_j and l_j relative to
 // m_j, in the exp2 domain), out = sum_j w_j O_j * v_scale / sum_j w_j l_j,
 // w_j = exp2(m_j - max_j m_j).  Splits that saw no visible key (l_j = 0)
-// are left out.  One thread per four head-dim elements of a row.
-template <int D, bool OUT_F32>
+// are left out.  One thread per four head-dim elements of a row.  OUT is
+// kOutBf16, kOutF32 or kOutF16.
+template <int D, int OUT>
 __global__ __launch_bounds__(256)
 void attn_combine_kernel(AttnArgs a) {
   constexpr int CH = D / 4;
@@ -745,13 +751,18 @@ void attn_combine_kernel(AttnArgs a) {
   const int b = bh / a.H, h = bh - b * a.H;
   const float inv = a.vs[bh * a.scale_stride] / l;
   const int64_t obase = (int64_t)b * a.osb + (int64_t)h * a.osh + (int64_t)q * a.oss + d;
-  if constexpr (OUT_F32) {
+  if constexpr (OUT == kOutF32) {
     *reinterpret_cast<float4*>(static_cast<float*>(a.out) + obase) =
         make_float4(o.x * inv, o.y * inv, o.z * inv, o.w * inv);
   } else {
     uint2 pk;
-    pk.x = pack_bf16x2(o.x * inv, o.y * inv);
-    pk.y = pack_bf16x2(o.z * inv, o.w * inv);
+    if constexpr (OUT == kOutF16) {
+      pk.x = pack_f16x2(o.x * inv, o.y * inv);
+      pk.y = pack_f16x2(o.z * inv, o.w * inv);
+    } else {
+      pk.x = pack_bf16x2(o.x * inv, o.y * inv);
+      pk.y = pack_bf16x2(o.z * inv, o.w * inv);
+    }
     *reinterpret_cast<uint2*>(static_cast<uint16_t*>(a.out) + obase) = pk;
   }
 }
@@ -781,8 +792,14 @@ inline void split_plan(int Skv, int kv_splits, int* split_tiles, int* n_splits) 
   *n_splits = (n_kb + *split_tiles - 1) / *split_tiles;
 }
 
+// kOutBf16 / kOutF32 / kOutF16 for an RP_OUT_* value
+inline int out_kind(int out_dtype) {
+  return out_dtype == RP_OUT_F32 ? kOutF32 : out_dtype == RP_OUT_F16 ? kOutF16 : kOutBf16;
+}
+
 template <int D>
-int launch_attn(const AttnArgs& base, bool out_f32, hipStream_t st) {
+int launch_attn(const AttnArgs& base, int out_dtype, hipStream_t st) {
+  const int kind = out_kind(out_dtype);
   AttnArgs a = base;
   a.n_qblocks = (a.Sq + kBlockM - 1) / kBlockM;
   a.D = D;
@@ -794,18 +811,22 @@ int launch_attn(const AttnArgs& base, bool out_f32, hipStream_t st) {
   }
   a.n_work = (int)work;
   if (a.kv_splits == 1) {
-    if (out_f32)
+    if (kind == kOutF32)
       launch_fwd<D, kOutF32>(a, st);
+    else if (kind == kOutF16)
+      launch_fwd<D, kOutF16>(a, st);
     else
       launch_fwd<D, kOutBf16>(a, st);
   } else {
     launch_fwd<D, kOutSplit>(a, st);
     const int64_t threads = (int64_t)a.B * a.H * a.Sq * (D / 4);
     const dim3 cgrid((unsigned)((threads + 255) / 256)), cblock(256);
-    if (out_f32)
-      hipLaunchKernelGGL((attn_combine_kernel<D, true>), cgrid, cblock, 0, st, a);
+    if (kind == kOutF32)
+      hipLaunchKernelGGL((attn_combine_kernel<D, kOutF32>), cgrid, cblock, 0, st, a);
+    else if (kind == kOutF16)
+      hipLaunchKernelGGL((attn_combine_kernel<D, kOutF16>), cgrid, cblock, 0, st, a);
     else
-      hipLaunchKernelGGL((attn_combine_kernel<D, false>), cgrid, cblock, 0, st, a);
+      hipLaunchKernelGGL((attn_combine_kernel<D, kOutBf16>), cgrid, cblock, 0, st, a);
   }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) {
@@ -855,7 +876,7 @@ int attn_setup(AttnArgs& a, const uint8_t* q8, const uint8_t* k8, const uint8_t*
     rp_set_error("attn: scale_stride must be 0 or 1");
     return RP_ERR_INVALID_ARGUMENT;
   }
-  if (out_dtype != RP_OUT_BF16 && out_dtype != RP_OUT_F32) {
+  if (out_dtype != RP_OUT_BF16 && out_dtype != RP_OUT_F32 && out_dtype != RP_OUT_F16) {
     rp_set_error("attn: unknown out_dtype %d", out_dtype);
     return RP_ERR_INVALID_ARGUMENT;
   }
@@ -892,12 +913,11 @@ int attn_setup(AttnArgs& a, const uint8_t* q8, const uint8_t* k8, const uint8_t*
 
 int attn_run(const AttnArgs& a, int D, int out_dtype, void* stream) {
   hipStream_t st = static_cast<hipStream_t>(stream);
-  const bool f32 = out_dtype == RP_OUT_F32;
   switch (D) {
-    case 32: return launch_attn<32>(a, f32, st);
-    case 64: return launch_attn<64>(a, f32, st);
-    case 128: return launch_attn<128>(a, f32, st);
-    default: return launch_attn<256>(a, f32, st);
+    case 32: return launch_attn<32>(a, out_dtype, st);
+    case 64: return launch_attn<64>(a, out_dtype, st);
+    case 128: return launch_attn<128>(a, out_dtype, st);
+    default: return launch_attn<256>(a, out_dtype, st);
   }
 }
 

@@ -35,6 +35,35 @@ __device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
 
 __device__ __forceinline__ float bf16_round(float f) { return bf16_to_f32(f32_to_bf16_bits(f)); }
 
+// ------------------------------------------------------------------ fp16
+__device__ __forceinline__ float f16_to_f32(uint32_t h) {
+  return (float)__builtin_bit_cast(_Float16, (uint16_t)h);
+}
+// fp32 -> fp16 -> fp32, round to nearest even with fp16 subnormals kept
+// (v_cvt_f16_f32 under the default mode), overflow to inf, NaN stays NaN.
+// The empty asm makes the operand an opaque, already rounded fp32 value:
+// otherwise the compiler fuses a preceding multiply into the conversion
+// (v_fma_mixlo_f16, one rounding), where the reference rounds the fp32
+// product first and then converts.
+__device__ __forceinline__ float f16_round(float f) {
+  asm("" : "+v"(f));
+  return (float)(_Float16)f;
+}
+__device__ __forceinline__ uint32_t pack_f16x2(float lo, float hi) {
+  asm("" : "+v"(lo), "+v"(hi));
+  return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)lo) |
+         ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)hi) << 16);
+}
+
+// Quantizer input element types (RP_DTYPE_* of the C interface).
+constexpr int kInBf16 = 0, kInF16 = 1;
+
+template <int DT>
+__device__ __forceinline__ float in_to_f32(uint32_t bits16) {
+  if constexpr (DT == kInF16) return f16_to_f32(bits16);
+  else return bf16_to_f32(bits16);
+}
+
 // -------------------------------------------------------------- e4m3fn
 // Two fp32 -> two e4m3fn codes in bits [16*hi, 16*hi+16) of `old`, using the
 // gfx950 hardware conversion (round to nearest even).
@@ -78,6 +107,25 @@ __device__ __forceinline__ float dequant_from_amax_bits(uint32_t amax_bits) {
   float a = bf16_to_f32(amax_bits);
   if (!(a != a) && a < lo) a = lo;
   return bf16_round(a / kScaleDivisor);
+}
+
+// The same for fp16 input.  On the GPU torch evaluates `half_tensor / 425.6`
+// as a multiply by the fp32 reciprocal of the scalar (its true-divide kernel
+// takes a * (1/b) when b is a CPU scalar), and that differs from a division
+// for two fp16 maxima; for bf16 the two forms agree on every value.  Amax
+// values below ~1.3e-5 give a zero fp16 scale, as in the reference.
+__device__ __forceinline__ float dequant_from_amax_bits_f16(uint32_t amax_bits) {
+  const float lo = 17.0f * 0x1p-24f;                // fp16(1e-6) = 1.0132789611816406e-06
+  constexpr float inv = 1.0f / kScaleDivisor;       // RN(1 / 425.6f)
+  float a = f16_to_f32(amax_bits);
+  if (!(a != a) && a < lo) a = lo;
+  return f16_round(a * inv);
+}
+
+template <int DT>
+__device__ __forceinline__ float dequant_from_amax(uint32_t amax_bits) {
+  if constexpr (DT == kInF16) return dequant_from_amax_bits_f16(amax_bits);
+  else return dequant_from_amax_bits(amax_bits);
 }
 
 }  // namespace rp

@@ -1,10 +1,12 @@
-// Per-group amax scaling and BF16 -> OCP e4m3fn quantization for gfx950.
+// Per-group amax scaling and BF16/FP16 -> OCP e4m3fn quantization for gfx950.
 //
 // Behaviour follows the reference quantizer
 // (kernels/triton_kernels/fp8_flash_attn_hopper.py:374-398; gfx942 sibling
-// kernels/triton_kernels/fp8_flash_attn.py:425-448):
-//   dequant = bf16(max(amax|x|, bf16(1e-6)) / 425.6)       per group
-//   code    = e4m3fn(clamp(float(x) * (1/dequant), +-448))  round to nearest even
+// kernels/triton_kernels/fp8_flash_attn.py:425-448), whose scale arithmetic
+// runs in the input dtype:
+//   bf16: dequant = bf16(max(amax|x|, bf16(1e-6)) / 425.6)          per group
+//   fp16: dequant = fp16(max(amax|x|, fp16(1e-6)) * RN(1/425.6))    per group
+//   code  = e4m3fn(clamp(float(x) * (1/dequant), +-448))  round to nearest even
 // The reference runs this as six torch ops over fp32 temporaries (about
 // 33 B of HBM traffic per element).  Here it is two streaming passes plus a
 // tiny per-group finalize: 2 B/element to find the maximum, 2 B read + 1 B
@@ -111,6 +113,7 @@ __global__ __launch_bounds__(kQThreads) void amax_partial_kernel(QParams p, uint
   }
 }
 
+template <int DT>
 __global__ __launch_bounds__(kQThreads) void scale_finalize_kernel(const uint32_t* partial,
                                                                    int64_t nbg, float* dequant) {
   const int64_t g = blockIdx.x;
@@ -125,15 +128,16 @@ __global__ __launch_bounds__(kQThreads) void scale_finalize_kernel(const uint32_
     uint32_t r = wmax[0];
 #pragma unroll
     for (int w = 1; w < kQThreads / kWave; ++w) r = umax32(r, wmax[w]);
-    dequant[g] = dequant_from_amax_bits(r);
+    dequant[g] = dequant_from_amax<DT>(r);
   }
 }
 
+template <int DT>
 __device__ __forceinline__ uint32_t quant4(uint32_t lo_pair, uint32_t hi_pair, float qm) {
-  const float a = clamp_e4m3(bf16_to_f32(lo_pair & 0xffffu) * qm);
-  const float b = clamp_e4m3(bf16_to_f32(lo_pair >> 16) * qm);
-  const float c = clamp_e4m3(bf16_to_f32(hi_pair & 0xffffu) * qm);
-  const float d = clamp_e4m3(bf16_to_f32(hi_pair >> 16) * qm);
+  const float a = clamp_e4m3(in_to_f32<DT>(lo_pair & 0xffffu) * qm);
+  const float b = clamp_e4m3(in_to_f32<DT>(lo_pair >> 16) * qm);
+  const float c = clamp_e4m3(in_to_f32<DT>(hi_pair & 0xffffu) * qm);
+  const float d = clamp_e4m3(in_to_f32<DT>(hi_pair >> 16) * qm);
   return pack4_e4m3(a, b, c, d);
 }
 
@@ -181,6 +185,7 @@ __global__ __launch_bounds__(kQThreads) void amax_flat_kernel(const uint16_t* x,
   }
 }
 
+template <int DT>
 __global__ __launch_bounds__(kQThreads) void quant_flat_kernel(const uint16_t* x, int64_t gsize,
                                                                int64_t nbg, const float* dequant,
                                                                int per_bh, uint8_t* codes) {
@@ -203,14 +208,15 @@ __global__ __launch_bounds__(kQThreads) void quant_flat_kernel(const uint16_t* x
     const int64_t idx = (int64_t)i * kQThreads + threadIdx.x;
     if (idx < n8) {
       uint2 o;
-      o.x = quant4(v[i][0], v[i][1], qm);
-      o.y = quant4(v[i][2], v[i][3], qm);
+      o.x = quant4<DT>(v[i][0], v[i][1], qm);
+      o.y = quant4<DT>(v[i][2], v[i][3], qm);
       dst[idx] = o;
     }
   }
 }
 
 // BHSD output: codes[r*D + d] for global row r = bh*S + s.
+template <int DT>
 __global__ __launch_bounds__(kQThreads) void quant_apply_kernel(QParams p, const float* dequant,
                                                                 int per_bh, uint8_t* codes) {
   const int64_t blk = blockIdx.x;
@@ -233,8 +239,8 @@ __global__ __launch_bounds__(kQThreads) void quant_apply_kernel(QParams p, const
   for (int64_t k = roff; k < nrows; k += step) {
     const uint4 v = *reinterpret_cast<const uint4*>(p.x + cur.base + cur.s * p.ss + col * 8);
     uint2 o;
-    o.x = quant4(v.x, v.y, qm);
-    o.y = quant4(v.z, v.w, qm);
+    o.x = quant4<DT>(v.x, v.y, qm);
+    o.y = quant4<DT>(v.z, v.w, qm);
     *reinterpret_cast<uint2*>(codes + r * p.D + col * 8) = o;
     cur.advance(step, p);
     r += step;
@@ -247,6 +253,7 @@ __global__ __launch_bounds__(kQThreads) void quant_apply_kernel(QParams p, const
 // column chunk t>>5 (8 elements), transposes its 4x8 codes in registers and
 // writes 8 dwords [d][s..s+3] into LDS; the tile then leaves as 64 rows of
 // 128 contiguous codes.
+template <int DT>
 __global__ __launch_bounds__(kQThreads) void quant_apply_t_kernel(QParams p, const float* dequant,
                                                                   int per_bh, uint8_t* codes,
                                                                   int64_t ld) {
@@ -266,8 +273,8 @@ __global__ __launch_bounds__(kQThreads) void quant_apply_t_kernel(QParams p, con
     const int64_t s = s0 + 4 * r4 + i;
     if (s < p.S && c * 8 < dcols) {
       const uint4 v = *reinterpret_cast<const uint4*>(p.x + base + s * p.ss + c * 8);
-      w[i][0] = quant4(v.x, v.y, qm);
-      w[i][1] = quant4(v.z, v.w, qm);
+      w[i][0] = quant4<DT>(v.x, v.y, qm);
+      w[i][1] = quant4<DT>(v.z, v.w, qm);
     } else {
       w[i][0] = 0u;
       w[i][1] = 0u;
@@ -308,11 +315,12 @@ __global__ void selftest_e4m3_kernel(const float* x, uint8_t* out, int64_t n) {
   out[i] = (uint8_t)(cvt_pk_e4m3<false>(v, 0.0f, 0) & 0xff);
 }
 
+template <int DT>
 __global__ void selftest_scale_kernel(const uint16_t* amax_bits, float* dequant, float* qmul,
                                       int64_t n) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= n) return;
-  const float dq = dequant_from_amax_bits(amax_bits[i]);
+  const float dq = dequant_from_amax<DT>(amax_bits[i]);
   dequant[i] = dq;
   qmul[i] = 1.0f / dq;
 }
@@ -320,6 +328,7 @@ __global__ void selftest_scale_kernel(const uint16_t* amax_bits, float* dequant,
 // ------------------------------------------------------------------ host
 struct Plan {
   QParams p;
+  int dt;         // RP_DTYPE_* of x
   int per_bh;
   size_t ws_bytes;
   bool flat;      // contiguous input: the flat kernels apply
@@ -333,8 +342,12 @@ int ilog2(int64_t v) {
   return r;
 }
 
-int make_plan(const void* x, int64_t B, int64_t H, int64_t S, int64_t D, int64_t sb, int64_t sh,
-              int64_t ss, int granularity, Plan* out) {
+int make_plan(const void* x, int x_dtype, int64_t B, int64_t H, int64_t S, int64_t D, int64_t sb,
+              int64_t sh, int64_t ss, int granularity, Plan* out) {
+  if (x_dtype != RP_DTYPE_BF16 && x_dtype != RP_DTYPE_F16) {
+    rp_set_error("quantize: unknown input dtype %d", x_dtype);
+    return RP_ERR_INVALID_ARGUMENT;
+  }
   if (B <= 0 || H <= 0 || S <= 0 || D <= 0) {
     rp_set_error("quantize: non-positive shape (%lld, %lld, %lld, %lld)", (long long)B,
                  (long long)H, (long long)S, (long long)D);
@@ -377,6 +390,7 @@ int make_plan(const void* x, int64_t B, int64_t H, int64_t S, int64_t D, int64_t
   p.nbg = (p.rows_per_group + p.rpb - 1) / p.rpb;
   p.vpr_log2 = ilog2(p.D / 8);
   out->p = p;
+  out->dt = x_dtype;
   out->per_bh = granularity == RP_SCALE_PER_BH;
   out->flat = contiguous;
   out->gsize = B * H * S * D / p.ngroups;
@@ -408,21 +422,26 @@ int launch_scale(const Plan& pl, float* dequant_out, void* ws, size_t ws_bytes, 
                        pl.p, partial);
   int rc = check_launch("amax_partial");
   if (rc) return rc;
-  hipLaunchKernelGGL(scale_finalize_kernel, dim3((unsigned)pl.p.ngroups), dim3(kQThreads), 0, st,
-                     partial, pl.p.nbg, dequant_out);
+  if (pl.dt == RP_DTYPE_F16)
+    hipLaunchKernelGGL(scale_finalize_kernel<kInF16>, dim3((unsigned)pl.p.ngroups),
+                       dim3(kQThreads), 0, st, partial, pl.p.nbg, dequant_out);
+  else
+    hipLaunchKernelGGL(scale_finalize_kernel<kInBf16>, dim3((unsigned)pl.p.ngroups),
+                       dim3(kQThreads), 0, st, partial, pl.p.nbg, dequant_out);
   return check_launch("scale_finalize");
 }
 
-int launch_apply(const Plan& pl, const void* x, int64_t B, int64_t H, int64_t S, int64_t D,
-                 int64_t sb, int64_t sh, int64_t ss, const float* dequant, uint8_t* codes,
-                 int layout, int64_t ld, hipStream_t st) {
+template <int DT>
+int launch_apply_t(const Plan& pl, const void* x, int64_t B, int64_t H, int64_t S, int64_t D,
+                   int64_t sb, int64_t sh, int64_t ss, const float* dequant, uint8_t* codes,
+                   int layout, int64_t ld, hipStream_t st) {
   if (layout == RP_LAYOUT_BHSD) {
     const int64_t nblocks = pl.p.ngroups * pl.p.nbg;
     if (pl.flat)
-      hipLaunchKernelGGL(quant_flat_kernel, dim3((unsigned)nblocks), dim3(kQThreads), 0, st,
+      hipLaunchKernelGGL(quant_flat_kernel<DT>, dim3((unsigned)nblocks), dim3(kQThreads), 0, st,
                          pl.p.x, pl.gsize, pl.p.nbg, dequant, pl.per_bh, codes);
     else
-      hipLaunchKernelGGL(quant_apply_kernel, dim3((unsigned)nblocks), dim3(kQThreads), 0, st,
+      hipLaunchKernelGGL(quant_apply_kernel<DT>, dim3((unsigned)nblocks), dim3(kQThreads), 0, st,
                          pl.p, dequant, pl.per_bh, codes);
     return check_launch("quant_apply");
   }
@@ -443,9 +462,17 @@ int launch_apply(const Plan& pl, const void* x, int64_t B, int64_t H, int64_t S,
     return RP_ERR_UNSUPPORTED;
   }
   dim3 grid((unsigned)(ld / 128), (unsigned)((D + 63) / 64), (unsigned)(B * H));
-  hipLaunchKernelGGL(quant_apply_t_kernel, grid, dim3(kQThreads), 0, st, q, dequant, pl.per_bh,
-                     codes, ld);
+  hipLaunchKernelGGL(quant_apply_t_kernel<DT>, grid, dim3(kQThreads), 0, st, q, dequant,
+                     pl.per_bh, codes, ld);
   return check_launch("quant_apply_t");
+}
+
+int launch_apply(const Plan& pl, const void* x, int64_t B, int64_t H, int64_t S, int64_t D,
+                 int64_t sb, int64_t sh, int64_t ss, const float* dequant, uint8_t* codes,
+                 int layout, int64_t ld, hipStream_t st) {
+  if (pl.dt == RP_DTYPE_F16)
+    return launch_apply_t<kInF16>(pl, x, B, H, S, D, sb, sh, ss, dequant, codes, layout, ld, st);
+  return launch_apply_t<kInBf16>(pl, x, B, H, S, D, sb, sh, ss, dequant, codes, layout, ld, st);
 }
 
 }  // namespace
@@ -459,30 +486,33 @@ extern "C" size_t rp_fp8_quant_workspace_bytes(int64_t B, int64_t H, int64_t S, 
   // group, and its rows hold at least as many elements.
   Plan pl;
   const void* dummy = reinterpret_cast<const void*>(uintptr_t(256));
-  if (make_plan(dummy, B, H, S, D, H * S * D, S * D, D, granularity, &pl) != RP_OK) return 0;
+  if (make_plan(dummy, RP_DTYPE_BF16, B, H, S, D, H * S * D, S * D, D, granularity, &pl) != RP_OK)
+    return 0;
   Plan pl2;
   size_t strided = 0;
-  if (make_plan(dummy, B, H, S, D, H * S * D + 8, S * D + 8, D, granularity, &pl2) == RP_OK)
+  if (make_plan(dummy, RP_DTYPE_BF16, B, H, S, D, H * S * D + 8, S * D + 8, D, granularity,
+                &pl2) == RP_OK)
     strided = pl2.ws_bytes;
   return pl.ws_bytes > strided ? pl.ws_bytes : strided;
 }
 
-extern "C" int rp_fp8_scale(const void* x, int64_t B, int64_t H, int64_t S, int64_t D, int64_t sb,
-                            int64_t sh, int64_t ss, int granularity, float* dequant_out,
-                            void* workspace, size_t workspace_bytes, void* stream) {
+extern "C" int rp_fp8_scale(const void* x, int x_dtype, int64_t B, int64_t H, int64_t S,
+                            int64_t D, int64_t sb, int64_t sh, int64_t ss, int granularity,
+                            float* dequant_out, void* workspace, size_t workspace_bytes,
+                            void* stream) {
   if (x == nullptr || dequant_out == nullptr) {
     rp_set_error("scale: null pointer");
     return RP_ERR_INVALID_ARGUMENT;
   }
   Plan pl;
-  int rc = make_plan(x, B, H, S, D, sb, sh, ss, granularity, &pl);
+  int rc = make_plan(x, x_dtype, B, H, S, D, sb, sh, ss, granularity, &pl);
   if (rc) return rc;
   return launch_scale(pl, dequant_out, workspace, workspace_bytes,
                       static_cast<hipStream_t>(stream));
 }
 
-extern "C" int rp_fp8_quantize(const void* x, int64_t B, int64_t H, int64_t S, int64_t D,
-                               int64_t sb, int64_t sh, int64_t ss, int granularity,
+extern "C" int rp_fp8_quantize(const void* x, int x_dtype, int64_t B, int64_t H, int64_t S,
+                               int64_t D, int64_t sb, int64_t sh, int64_t ss, int granularity,
                                const float* dequant, uint8_t* codes, int layout, int64_t ld,
                                void* stream) {
   if (x == nullptr || dequant == nullptr || codes == nullptr) {
@@ -490,22 +520,23 @@ extern "C" int rp_fp8_quantize(const void* x, int64_t B, int64_t H, int64_t S, i
     return RP_ERR_INVALID_ARGUMENT;
   }
   Plan pl;
-  int rc = make_plan(x, B, H, S, D, sb, sh, ss, granularity, &pl);
+  int rc = make_plan(x, x_dtype, B, H, S, D, sb, sh, ss, granularity, &pl);
   if (rc) return rc;
   return launch_apply(pl, x, B, H, S, D, sb, sh, ss, dequant, codes, layout, ld,
                       static_cast<hipStream_t>(stream));
 }
 
-extern "C" int rp_fp8_scale_quantize(const void* x, int64_t B, int64_t H, int64_t S, int64_t D,
-                                     int64_t sb, int64_t sh, int64_t ss, int granularity,
-                                     float* dequant_out, uint8_t* codes, int layout, int64_t ld,
-                                     void* workspace, size_t workspace_bytes, void* stream) {
+extern "C" int rp_fp8_scale_quantize(const void* x, int x_dtype, int64_t B, int64_t H, int64_t S,
+                                     int64_t D, int64_t sb, int64_t sh, int64_t ss,
+                                     int granularity, float* dequant_out, uint8_t* codes,
+                                     int layout, int64_t ld, void* workspace,
+                                     size_t workspace_bytes, void* stream) {
   if (x == nullptr || dequant_out == nullptr || codes == nullptr) {
     rp_set_error("scale_quantize: null pointer");
     return RP_ERR_INVALID_ARGUMENT;
   }
   Plan pl;
-  int rc = make_plan(x, B, H, S, D, sb, sh, ss, granularity, &pl);
+  int rc = make_plan(x, x_dtype, B, H, S, D, sb, sh, ss, granularity, &pl);
   if (rc) return rc;
   if (layout == RP_LAYOUT_BHDS && (D % 32 != 0 || ld < S || ld % 128 != 0)) {
     rp_set_error("scale_quantize(BHDS): needs D %% 32 == 0 and ld >= S with ld %% 128 == 0");
@@ -529,15 +560,20 @@ extern "C" int rp_selftest_e4m3(const float* x, uint8_t* out, int64_t n, void* s
   return check_launch("selftest_e4m3");
 }
 
-extern "C" int rp_selftest_scale(const uint16_t* amax_bits, float* dequant, float* qmul, int64_t n,
-                                 void* stream) {
-  if (amax_bits == nullptr || dequant == nullptr || qmul == nullptr || n < 0) {
+extern "C" int rp_selftest_scale(const uint16_t* amax_bits, int x_dtype, float* dequant,
+                                 float* qmul, int64_t n, void* stream) {
+  if (amax_bits == nullptr || dequant == nullptr || qmul == nullptr || n < 0 ||
+      (x_dtype != RP_DTYPE_BF16 && x_dtype != RP_DTYPE_F16)) {
     rp_set_error("selftest_scale: bad arguments");
     return RP_ERR_INVALID_ARGUMENT;
   }
   if (n == 0) return RP_OK;
   const int64_t blocks = (n + 255) / 256;
-  hipLaunchKernelGGL(selftest_scale_kernel, dim3((unsigned)blocks), dim3(256), 0,
-                     static_cast<hipStream_t>(stream), amax_bits, dequant, qmul, n);
+  if (x_dtype == RP_DTYPE_F16)
+    hipLaunchKernelGGL(selftest_scale_kernel<kInF16>, dim3((unsigned)blocks), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), amax_bits, dequant, qmul, n);
+  else
+    hipLaunchKernelGGL(selftest_scale_kernel<kInBf16>, dim3((unsigned)blocks), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), amax_bits, dequant, qmul, n);
   return check_launch("selftest_scale");
 }

@@ -39,6 +39,9 @@ V_PAD = 128
 
 Granularity = Literal["bh", "tensor"]
 _GRAN = {"bh": C.RP_SCALE_PER_BH, "tensor": C.RP_SCALE_PER_TENSOR}
+_IN_DTYPES = {torch.bfloat16: C.RP_DTYPE_BF16, torch.float16: C.RP_DTYPE_F16}
+_OUT_DTYPES = {torch.bfloat16: C.RP_OUT_BF16, torch.float16: C.RP_OUT_F16,
+               torch.float32: C.RP_OUT_F32}
 
 
 def _stream(t: torch.Tensor) -> int:
@@ -75,20 +78,30 @@ def _check_bf16(name: str, x: torch.Tensor) -> None:
         raise TypeError(f"{name} must be bfloat16 (got {x.dtype})")
 
 
+def _in_dtype(name: str, x: torch.Tensor) -> int:
+    """RP_DTYPE_* of a quantizer input: bfloat16 or float16, on the GPU."""
+    _check_cuda(name, x)
+    dt = _IN_DTYPES.get(x.dtype)
+    if dt is None:
+        raise TypeError(f"{name} must be bfloat16 or float16 (got {x.dtype})")
+    return dt
+
+
 def per_bh_scale(x: torch.Tensor, granularity: Granularity = "bh") -> torch.Tensor:
     """Dequant scale per (batch, head) -- shape (B*H,) -- or per tensor -- shape (1,).
 
-    Same result as the reference's ``_per_bh_scale`` (bit for bit).  A 2-D
-    input is treated as one (1, 1, S, D) head.
+    Same result as the reference's ``_per_bh_scale`` on the GPU (bit for
+    bit), for bfloat16 or float16 ``x``.  A 2-D input is treated as one
+    (1, 1, S, D) head.
     """
-    _check_bf16("x", x)
+    dt = _in_dtype("x", x)
     x4 = _as4d(x)
     B, H, S, D, sb, sh, ss = _bhsd_view(x4)
     n = B * H if granularity == "bh" else 1
     out = torch.empty(n, dtype=torch.float32, device=x.device)
     ws_bytes = C.lib().rp_fp8_quant_workspace_bytes(B, H, S, D, _GRAN[granularity])
     ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=x.device)
-    C.check(C.lib().rp_fp8_scale(x4.data_ptr(), B, H, S, D, sb, sh, ss, _GRAN[granularity],
+    C.check(C.lib().rp_fp8_scale(x4.data_ptr(), dt, B, H, S, D, sb, sh, ss, _GRAN[granularity],
                                  out.data_ptr(), ws.data_ptr(), ws.numel(), _stream(x)),
             "rp_fp8_scale")
     return out
@@ -103,7 +116,7 @@ def quantize(x: torch.Tensor, dequant: torch.Tensor, granularity: Granularity = 
     ldv = S rounded up to 128 and zero padding -- V transposed per head, the
     operand layout of the attention kernel.
     """
-    _check_bf16("x", x)
+    dt = _in_dtype("x", x)
     _check_cuda("dequant", dequant)
     x4 = _as4d(x)
     B, H, S, D, sb, sh, ss = _bhsd_view(x4)
@@ -117,7 +130,7 @@ def quantize(x: torch.Tensor, dequant: torch.Tensor, granularity: Granularity = 
         ld = _round_up(S, V_PAD)
         codes = torch.empty((B, H, D, ld), dtype=torch.uint8, device=x.device)
         lay = C.RP_LAYOUT_BHDS
-    C.check(C.lib().rp_fp8_quantize(x4.data_ptr(), B, H, S, D, sb, sh, ss, _GRAN[granularity],
+    C.check(C.lib().rp_fp8_quantize(x4.data_ptr(), dt, B, H, S, D, sb, sh, ss, _GRAN[granularity],
                                     dq.data_ptr(), codes.data_ptr(), lay, ld, _stream(x)),
             "rp_fp8_quantize")
     codes = codes.view(torch.float8_e4m3fn)
@@ -127,7 +140,7 @@ def quantize(x: torch.Tensor, dequant: torch.Tensor, granularity: Granularity = 
 def scale_quantize(x: torch.Tensor, granularity: Granularity = "bh",
                    layout: Literal["bhsd", "bhds"] = "bhsd") -> tuple[torch.Tensor, torch.Tensor]:
     """(dequant scales, codes) in one stream-ordered call (amax, scale, apply)."""
-    _check_bf16("x", x)
+    dt = _in_dtype("x", x)
     x4 = _as4d(x)
     B, H, S, D, sb, sh, ss = _bhsd_view(x4)
     g = _GRAN[granularity]
@@ -141,7 +154,7 @@ def scale_quantize(x: torch.Tensor, granularity: Granularity = "bh",
         lay = C.RP_LAYOUT_BHDS
     ws_bytes = C.lib().rp_fp8_quant_workspace_bytes(B, H, S, D, g)
     ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=x.device)
-    C.check(C.lib().rp_fp8_scale_quantize(x4.data_ptr(), B, H, S, D, sb, sh, ss, g,
+    C.check(C.lib().rp_fp8_scale_quantize(x4.data_ptr(), dt, B, H, S, D, sb, sh, ss, g,
                                           dq.data_ptr(), codes.data_ptr(), lay, ld,
                                           ws.data_ptr(), ws.numel(), _stream(x)),
             "rp_fp8_scale_quantize")
@@ -274,12 +287,9 @@ def attention_fp8(q8: torch.Tensor, k8: torch.Tensor, vt8: torch.Tensor, q_scale
         out = torch.empty((B, H, Sq, D), dtype=out_dtype, device=q8.device)
     if out.shape != (B, H, Sq, D) or out.stride(3) != 1:
         raise ValueError("out must be (B, H, Sq, D) with a contiguous last dimension")
-    if out.dtype == torch.bfloat16:
-        odt = C.RP_OUT_BF16
-    elif out.dtype == torch.float32:
-        odt = C.RP_OUT_F32
-    else:
-        raise TypeError(f"out dtype {out.dtype} not supported (bfloat16 or float32)")
+    odt = _OUT_DTYPES.get(out.dtype)
+    if odt is None:
+        raise TypeError(f"out dtype {out.dtype} not supported (bfloat16, float16 or float32)")
     if prefix_len is not None:
         mask, pre, suf = C.RP_MASK_SHARED_PREFIX, int(prefix_len), int(suffix_len or 0)
     else:
@@ -306,7 +316,7 @@ def fp8_flash_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *,
                         out_dtype: torch.dtype | None = None, prefix_len: int | None = None,
                         suffix_len: int | None = None, kv_splits: int | None = None
                         ) -> torch.Tensor:
-    """Fused FP8 flash attention, (B, H, S, D) bf16 in, (B, H, Sq, D) out.
+    """Fused FP8 flash attention, (B, H, S, D) bf16 or fp16 in, (B, H, Sq, D) out.
 
     Mirrors the reference's ``fp8_flash_attention``
     (kernels/triton_kernels/fp8_flash_attn.py:480-645): quantize Q/K/V with
@@ -315,7 +325,7 @@ def fp8_flash_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *,
     the reference, K/V may have a different sequence length than Q
     (cross-attention), inputs may be strided (e.g. permuted (B, S, H, D)
     views -- no copies are made), and the output is written directly in
-    bf16 (or into ``out``).
+    q's dtype (or into ``out``) rather than cast from fp32.
 
     The launch configuration resolves as in the reference (:482-499):
     ``kv_splits`` if given; else the fallback when
@@ -324,7 +334,9 @@ def fp8_flash_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *,
     winner is recorded (see ``repercep_runtime_amd.tuning``).
     """
     for name, t in (("q", q), ("k", k), ("v", v)):
-        _check_bf16(name, t)
+        _in_dtype(name, t)
+    if not (q.dtype == k.dtype == v.dtype):
+        raise TypeError(f"q, k, v dtypes differ ({q.dtype}, {k.dtype}, {v.dtype})")
     if q.dim() != 4 or k.dim() != 4 or v.dim() != 4:
         raise ValueError("q, k, v must be 4-D (B, H, S, D)")
     B, H, Sq, D = q.shape
@@ -465,12 +477,15 @@ def selftest_e4m3(x: torch.Tensor) -> torch.Tensor:
     return out
 
 
-def selftest_scale(amax_bits: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
-    """Device dequant scale and multiplier for bf16 amax bit patterns (int16/uint16)."""
+def selftest_scale(amax_bits: torch.Tensor, dtype: torch.dtype = torch.bfloat16
+                   ) -> tuple[torch.Tensor, torch.Tensor]:
+    """Device dequant scale and multiplier for bf16 or fp16 (``dtype``) amax bit
+    patterns (int16/uint16)."""
     _check_cuda("amax_bits", amax_bits)
+    dt = _IN_DTYPES[dtype]
     a = amax_bits.contiguous()
     dq = torch.empty(a.shape, dtype=torch.float32, device=a.device)
     qm = torch.empty(a.shape, dtype=torch.float32, device=a.device)
-    C.check(C.lib().rp_selftest_scale(a.data_ptr(), dq.data_ptr(), qm.data_ptr(), a.numel(),
+    C.check(C.lib().rp_selftest_scale(a.data_ptr(), dt, dq.data_ptr(), qm.data_ptr(), a.numel(),
                                       _stream(a)), "rp_selftest_scale")
     return dq, qm

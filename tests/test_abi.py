@@ -56,7 +56,7 @@ def test_no_oracle_or_torch_symbols_in_library() -> None:
 
 def test_version_and_status_strings() -> None:
     L = _capi.lib()
-    assert L.rp_abi_version() == 1
+    assert L.rp_abi_version() == 2
     assert L.rp_status_string(0) == b"ok"
     assert L.rp_status_string(1) == b"invalid argument"
     assert L.rp_status_string(2) == b"unsupported shape or layout"
@@ -116,9 +116,19 @@ def test_gemm_argument_checks(args: tuple, status: int, msg: str) -> None:
 
 def test_quantizer_argument_checks() -> None:
     L = _capi.lib()
-    assert L.rp_fp8_scale(None, 1, 1, 16, 64, 1024, 1024, 64, 0, FAKE, FAKE, 4096, None) == 1
-    assert L.rp_fp8_scale_quantize(FAKE, 1, 1, 16, 64, 1024, 1024, 64, 5, FAKE, FAKE, 0, 0,
+    bf16, f16 = _capi.RP_DTYPE_BF16, _capi.RP_DTYPE_F16
+    assert L.rp_fp8_scale(None, bf16, 1, 1, 16, 64, 1024, 1024, 64, 0, FAKE, FAKE, 4096,
+                          None) == 1
+    assert L.rp_fp8_scale_quantize(FAKE, f16, 1, 1, 16, 64, 1024, 1024, 64, 5, FAKE, FAKE, 0, 0,
                                    FAKE, 4096, None) != 0
+    assert "granularity" in L.rp_last_error().decode()
+    for dt in (2, -1):   # fp32 and unknown inputs are refused before any launch
+        assert L.rp_fp8_scale(FAKE, dt, 1, 1, 16, 64, 1024, 1024, 64, 0, FAKE, FAKE, 4096,
+                              None) == 1
+        assert "input dtype" in L.rp_last_error().decode()
+        assert L.rp_fp8_quantize(FAKE, dt, 1, 1, 16, 64, 1024, 1024, 64, 0, FAKE, FAKE, 0, 0,
+                                 None) == 1
+        assert L.rp_selftest_scale(FAKE, dt, FAKE, FAKE, 4, None) == 1
 
 
 def _norm(L, **kw) -> int:

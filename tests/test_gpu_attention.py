@@ -113,6 +113,49 @@ def test_shapes_vs_oracle(gpu: torch.device, case: tuple) -> None:
         _check(out[b], ref, f"{name} b={b}")
 
 
+@pytest.mark.parametrize("out_dtype", [None, torch.float32, torch.bfloat16])
+def test_fp16_inputs_vs_oracle(gpu: torch.device, out_dtype: torch.dtype | None) -> None:
+    """fp16 Q/K/V (the reference accepts them: fp8_triton.py:85): fp16 scales
+    and codes, and the output in q's dtype by default."""
+    from oracle import quant
+
+    g = torch.Generator().manual_seed(16)
+    B, H, S, D = 1, 2, 700, 128
+    q, k, v = (torch.randn(B, H, S, D, generator=g).mul(m).to(torch.float16)
+               for m in (1.0, 2.0, 0.5))
+    out = ops.fp8_flash_attention(q.to(gpu), k.to(gpu), v.to(gpu), out_dtype=out_dtype)
+    assert out.dtype == (out_dtype or torch.float16)
+    qs, q8 = quant.quantize_codes(q)
+    ks, k8 = quant.quantize_codes(k)
+    vs, v8 = quant.quantize_codes(v)
+    for h in range(H):
+        ref = native.attn_rows(q8[0, h], k8[0, h], v8[0, h], qs[h], ks[h], vs[h], D ** -0.5,
+                               np.arange(S), block_n=ops.BLOCK_N)
+        if out.dtype != torch.float32:
+            ref = torch.from_numpy(ref).to(out.dtype).float().numpy()
+        _check(out[0, h].float().cpu().numpy(), ref, f"fp16 in, {out.dtype} out, h={h}")
+
+
+def test_fp16_and_bf16_outputs_are_one_rounding_of_fp32(gpu: torch.device) -> None:
+    """The 16-bit outputs, direct and through the split-merge kernel, are the
+    fp32 result rounded once to nearest even, like the reference's
+    ``out.to(q.dtype)`` (fp8_flash_attn.py:645)."""
+    g = torch.Generator().manual_seed(18)
+    q, k, v = (torch.randn(1, 2, 200, 64, generator=g).to(torch.float16) for _ in range(3))
+    qg, kg, vg = q.to(gpu), k.to(gpu), v.to(gpu)
+    o1 = ops.fp8_flash_attention(qg, kg, vg, out_dtype=torch.float32, kv_splits=1)
+    o4 = ops.fp8_flash_attention(qg, kg, vg, kv_splits=1)
+    assert o4.dtype == torch.float16
+    assert torch.equal(o4, o1.to(torch.float16))   # one RNE of the same fp32 value
+    s32 = ops.fp8_flash_attention(qg, kg, vg, out_dtype=torch.float32, kv_splits=4)
+    s16 = ops.fp8_flash_attention(qg, kg, vg, kv_splits=4)
+    assert torch.equal(s16, s32.to(torch.float16))
+    # likewise bf16 output: the reference's fp32 result cast once (:645)
+    for n, o32 in ((1, o1), (4, s32)):
+        ob = ops.fp8_flash_attention(qg, kg, vg, out_dtype=torch.bfloat16, kv_splits=n)
+        assert torch.equal(ob, o32.to(torch.bfloat16))
+
+
 def test_per_tensor_granularity(gpu: torch.device) -> None:
     g = torch.Generator().manual_seed(5)
     q, k, v = (torch.randn(1, 4, 600, 128, generator=g).mul(1 + i).to(torch.bfloat16)

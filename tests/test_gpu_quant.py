@@ -198,3 +198,73 @@ def test_quantize_wan_full_size_every_element(gpu: torch.device) -> None:
         del dq, codes, got, ref_c
     del q, k, v
     torch.cuda.empty_cache()
+
+
+# ------------------------------------------------------------- fp16 input
+def _all_nonneg(dtype: torch.dtype) -> torch.Tensor:
+    """Every non-negative value of a 16-bit float type from +0 to +inf, then a NaN."""
+    top, nan = (0x7C00, 0x7E00) if dtype == torch.float16 else (0x7F80, 0x7FC0)
+    bits = np.concatenate([np.arange(0, top + 1), [nan]]).astype(np.uint16)
+    return torch.from_numpy(bits.view(np.int16)).view(dtype)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_scale_every_amax_matches_torch_on_the_gpu(gpu: torch.device, dtype: torch.dtype) -> None:
+    """The kernel's scale function on every amax value against the reference's
+    expression (``amax.clamp(min=1e-6) / (0.95 * 448)`` in the input dtype,
+    fp8_flash_attn_hopper.py:381-385) evaluated by torch on this GPU, and
+    against the CPU oracle."""
+    from oracle import quant
+
+    vals = _all_nonneg(dtype)
+    dq, qm = ops.selftest_scale(vals.view(torch.int16).to(gpu), dtype)
+    ref = (vals.to(gpu).clamp(min=1e-6) / (0.95 * 448.0)).to(torch.float32).cpu().numpy()
+    _assert_scales_equal(dq.cpu().numpy(), ref)
+    orc = quant.per_group_dequant(vals.reshape(1, -1, 1, 1)).numpy()
+    _assert_scales_equal(dq.cpu().numpy(), orc)
+    # the multiplier is the correctly rounded fp32 reciprocal, as 1.0 / scale
+    qref = (1.0 / torch.from_numpy(ref)).numpy()
+    _assert_scales_equal(qm.cpu().numpy(), qref)
+
+
+def _f16_groups(seed: int, shape: tuple[int, ...]) -> torch.Tensor:
+    """fp16 heads spanning the format: subnormal-heavy, unit, and near-max scales."""
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(shape, generator=g)
+    mags = torch.tensor([2e-4, 1.0, 30.0, 3e4, 0.05, 600.0])
+    x = x * mags[torch.arange(shape[0] * shape[1]) % mags.numel()].reshape(shape[0], shape[1], 1, 1)
+    return x.clamp(-65504, 65504).to(torch.float16)
+
+
+@pytest.mark.parametrize("granularity", ["bh", "tensor"])
+@pytest.mark.parametrize("layout", ["bhsd", "bhds"])
+def test_fp16_quantize_bit_exact(gpu: torch.device, granularity: str, layout: str) -> None:
+    from oracle import quant
+
+    x = _f16_groups(21, (2, 3, 333, 64))
+    ref_s, ref_c = quant.quantize_codes(x, granularity)
+    dq, codes = ops.scale_quantize(x.to(gpu), granularity, layout)
+    _assert_scales_equal(dq.cpu().numpy(), ref_s)
+    c = codes_np(codes)
+    if layout == "bhds":
+        assert not c[..., 333:].any(), "padding columns must be zero"
+        c = vt_to_bhsd(c, 333)
+    _assert_codes_equal(c, ref_c)
+
+
+def test_fp16_zero_scale_group_matches_torch_on_the_gpu(gpu: torch.device) -> None:
+    """A head whose amax underflows the fp16 scale to zero: 1/0 = inf, so zeros
+    become NaN codes and everything else +-448, exactly as the reference's
+    own expression does on this GPU."""
+    from oracle import quant
+
+    x = torch.zeros(1, 2, 64, 64, dtype=torch.float16)
+    x[0, 0, 3, :5] = torch.tensor([3e-6, -5e-6, 1e-7, 0.0, 9e-6]).to(torch.float16)
+    x[0, 1] = _f16_groups(3, (1, 1, 64, 64))[0, 0]
+    xg = x.to(gpu)
+    dq, codes = ops.scale_quantize(xg, "bh", "bhsd")
+    assert dq[0].item() == 0.0
+    ref_dq = quant.per_group_dequant(xg)          # the reference's ops, on the GPU
+    ref_c = quant.quantize(xg, ref_dq).view(torch.uint8).cpu().numpy()
+    _assert_scales_equal(dq.cpu().numpy(), ref_dq.cpu().numpy())
+    _assert_codes_equal(codes_np(codes), ref_c)

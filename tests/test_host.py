@@ -65,7 +65,10 @@ def test_fp8_op_supports() -> None:
     assert not op.supports(AttentionShape(1, 2, 256, 256, 96), DType.BF16)        # head dim
     assert not op.supports(AttentionShape(1, 2, 256, 256, 64, AttentionKind.NEIGHBORHOOD),
                            DType.BF16)
-    assert not op.supports(ok, DType.FP16)
+    assert op.supports(ok, DType.FP16)                                            # as fp8_triton.py:85
+    assert not op.supports(ok, DType.FP32)
+    for d in (32, 256):                                                            # the full set
+        assert op.supports(AttentionShape(1, 2, 256, 256, d), DType.BF16)
 
 
 def test_fp8_op_raises_runtime_error_when_unavailable() -> None:
@@ -165,7 +168,10 @@ def test_bridge_routing_rules() -> None:
     q, k, v = _bshd(4096)
     assert db._route_should_use_fp8(q, k, v)
     assert not db._route_should_use_fp8(*_bshd(1024))                       # crossover
-    assert not db._route_should_use_fp8(*_bshd(4096, dtype=torch.float16))  # dtype
+    assert db._route_should_use_fp8(*_bshd(4096, dtype=torch.float16))      # fp16 (:69)
+    assert not db._route_should_use_fp8(*_bshd(4096, dtype=torch.float32))  # dtype
+    assert db._route_should_use_fp8(*_bshd(4096, D=256))                    # head dims (:49)
+    assert db._route_should_use_fp8(*_bshd(4096, D=32))
     assert not db._route_should_use_fp8(*_bshd(4096, D=96))                 # head dim
     assert db._route_should_use_fp8(*_bshd(4096, D=128, Skv=512))           # cross-attention
     assert not db._route_should_use_fp8(*_bshd(4096, Skv=64))               # short K/V

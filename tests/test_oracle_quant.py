@@ -136,6 +136,50 @@ def test_scale_formula_every_bf16_amax() -> None:
     assert not (ref[fin].view(np.uint32) & 0xFFFF).any()
 
 
+def test_bf16_scale_divide_and_reciprocal_forms_agree() -> None:
+    """torch's GPU kernel takes ``amax / 425.6`` as ``amax * RN(1/425.6f)``,
+    its CPU kernel divides; for bf16 the rounded scales agree on every amax
+    value, so the CPU restatement is the GPU's too."""
+    lo = torch.tensor(1e-6).to(torch.bfloat16).item()
+    vals = _all_bf16().abs().to(torch.float32)
+    vals = torch.where(vals.isnan(), vals, vals.clamp(min=lo))
+    a = vals.numpy()
+    inv = np.float32(1.0) / np.float32(425.6)
+    div = torch.from_numpy((a / np.float32(425.6)).astype(np.float32)).to(torch.bfloat16)
+    mul = torch.from_numpy((a * inv).astype(np.float32)).to(torch.bfloat16)
+    assert torch.equal(div.view(torch.int16), mul.view(torch.int16))
+
+
+def _all_f16() -> torch.Tensor:
+    """Every non-negative fp16 value from +0 to +inf, then one NaN."""
+    bits = np.concatenate([np.arange(0, 0x7C01), [0x7E00]]).astype(np.uint16)
+    return torch.from_numpy(bits.view(np.int16)).view(torch.float16)
+
+
+def test_fp16_scale_every_amax() -> None:
+    """The fp16 scale over every amax value against an independent numpy
+    restatement of the GPU's evaluation, fp16(max(a, fp16(1e-6)) * RN(1/425.6))."""
+    vals = _all_f16()
+    n = vals.numel()
+    got = quant.per_group_dequant(vals.reshape(1, n, 1, 1)).numpy()
+    a = vals.to(torch.float32).numpy()
+    lo = np.float32(np.float16(1e-6))
+    assert lo == np.float32(17 * 2.0 ** -24)
+    a = np.where(np.isnan(a), a, np.maximum(a, lo))
+    want = (a * (np.float32(1.0) / np.float32(425.6))).astype(np.float32)
+    want = want.astype(np.float16).astype(np.float32)
+    assert _scales_equal(got, want)
+    # the division form (torch's CPU kernel) departs from it on exactly two
+    # amax values: a restatement that divided would fail the GPU pin there
+    div = (vals.clamp(min=1e-6) / (0.95 * 448.0)).to(torch.float32).numpy()
+    differ = ~((div.view(np.uint32) == want.view(np.uint32)) | (np.isnan(div) & np.isnan(want)))
+    assert int(differ.sum()) == 2
+    # maxima below ~1.3e-5 underflow to a zero fp16 scale, as the reference's does
+    zero = want == 0
+    assert zero.any() and a[zero].max() < 1.3e-5 and a[~zero & np.isfinite(a)].min() > 1.2e-5
+    assert np.isinf(want[n - 2]) and np.isnan(want[n - 1])     # inf and NaN maxima propagate
+
+
 def _bf16_rne(x: np.float32) -> np.float32:
     u = np.array([x], dtype=np.float32).view(np.uint32)[0]
     u = (u + 0x7FFF + ((u >> 16) & 1)) & 0xFFFF0000
