@@ -137,6 +137,15 @@ int rp_fp8_attn_fwd(const uint8_t* q8, const uint8_t* k8, const uint8_t* vt8, in
                     int B, int H, int Sq, int Skv, int D,
                     int mask, int prefix_len, int suffix_len, void* stream);
 
+/* The launch plan rp_fp8_attn_fwd / rp_fp8_attn_fwd_split use for a shape:
+ * the number of consecutive query blocks (256 rows each) one workgroup
+ * runs.  Above 1, the kernel streams a workgroup's blocks through one tile
+ * pipeline (short unmasked key ranges, head dim <= 128, one key split).
+ * No counterpart in the reference (its Triton launch has one program per
+ * query block); exposed for tests and profiling.  0 on invalid sizes. */
+int rp_fp8_attn_blocks_per_workgroup(int B, int H, int Sq, int Skv, int D, int mask,
+                                     int kv_splits);
+
 /* Key-split variant of rp_fp8_attn_fwd: the key range is cut into
  * `kv_splits` contiguous parts of whole 128-key tiles (fewer when Skv has
  * fewer tiles), each run by its own workgroups with its own running max, and

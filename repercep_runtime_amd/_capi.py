@@ -36,6 +36,7 @@ EXPORTS = (
     "rp_abi_version", "rp_status_string", "rp_last_error",
     "rp_fp8_quant_workspace_bytes", "rp_fp8_scale", "rp_fp8_quantize",
     "rp_fp8_scale_quantize", "rp_fp8_attn_fwd", "rp_fp8_attn_workspace_bytes",
+    "rp_fp8_attn_blocks_per_workgroup",
     "rp_fp8_attn_fwd_split", "rp_fp8_rmsnorm_quant_workspace_bytes",
     "rp_fp8_rmsnorm_scale_quantize", "rp_fp8_gemm", "rp_fp8_transpose",
     "rp_selftest_e4m3", "rp_selftest_scale",
@@ -78,6 +79,8 @@ def _declare(L: ctypes.CDLL) -> None:
     L.rp_fp8_attn_fwd.argtypes = [_vp, _vp, _vp, _i64, _vp, _vp, _vp, _int, _f32, _vp, _int,
                                   _i64, _i64, _i64, _int, _int, _int, _int, _int, _int, _int,
                                   _int, _vp]
+    L.rp_fp8_attn_blocks_per_workgroup.restype = _int
+    L.rp_fp8_attn_blocks_per_workgroup.argtypes = [_int] * 7
     L.rp_fp8_attn_workspace_bytes.restype = _sz
     L.rp_fp8_attn_workspace_bytes.argtypes = [_int, _int, _int, _int, _int]
     L.rp_fp8_attn_fwd_split.restype = _int

@@ -80,6 +80,9 @@ struct AttnArgs {
   int D;          // head dim: row length of Q and K, rows of V^T per head
   int dv_halves;  // 2: each query block runs as two workgroups, one per half
                   // of V^T / O (head dim 256), both computing the same S
+  // multi-block launches: each workgroup runs qb_per_wg consecutive query
+  // blocks of one head (wg_per_bh workgroups per head)
+  int qb_per_wg, wg_per_bh;
   int n_qblocks;
   int n_work;
   // key splits: split j covers keys [j*split_tiles*128, (j+1)*split_tiles*128)
@@ -292,6 +295,13 @@ __device__ __forceinline__ void wait_vmem_all() {
   // s_waitcnt vmcnt(0): direct-to-LDS loads have landed
   __builtin_amdgcn_s_waitcnt(0x0F70);
 }
+// s_waitcnt vmcnt(N): all but this wave's N most recent vector memory
+// operations have completed
+template <int N>
+__device__ __forceinline__ void wait_vmem_n() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
 
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
   const __bf16 a = (__bf16)lo, b = (__bf16)hi;  // v_cvt_pk_bf16_f32, round to nearest even
@@ -408,20 +418,27 @@ __device__ __forceinline__ void mfma_phase(uint32_t kl, uint32_t vl,
 // before barrier 2j.  Only group 0 loads: the slot in which a group issues
 // loads costs its SIMD VALU time, and in this slot the MFMA group, not the
 // softmax group, has VALU time to spare.
-template <int DK, int DV, int OUT, bool WINDOW>
+template <int DK, int DV, int OUT, bool WINDOW, bool MULTI>
 __global__ __launch_bounds__(512, 1)
 void attn_fwd_kernel(AttnArgs a) {
   constexpr int NW = 8;
   using G = Geo<DK, DV, NW>;
   constexpr int D = DK;
+  static_assert(!MULTI || (OUT != kOutSplit && !WINDOW && DV == DK), "multi-block launches");
   constexpr int QROWS = 32;
   constexpr int BLOCK_M = QROWS * NW;
-  __shared__ __attribute__((aligned(1024))) uint8_t smem[G::LDS_BYTES];
+  // multi-block launches stage the next query block's Q in LDS: two buffers
+  // of BLOCK_M rows (the block being switched to, and the one after)
+  constexpr int Q_BYTES = MULTI ? BLOCK_M * DK : 0;
+  constexpr int Q_LOADS = Q_BYTES / 1024 / 4;   // per loading wave
+  static_assert(G::LDS_BYTES + 2 * Q_BYTES <= 160 * 1024, "LDS");
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[G::LDS_BYTES + 2 * Q_BYTES];
   uint8_t* const kbuf = smem;                              // K_STAGES x K_BYTES
   uint8_t* const vbuf = smem + G::K_STAGES * G::K_BYTES;   // V_STAGES x V_BYTES
   // the same two regions as LDS byte addresses, for the direct-to-LDS loads
   const uint32_t kbuf_lds = (uint32_t)(uintptr_t)(lds_ptr_t)smem;
   const uint32_t vbuf_lds = kbuf_lds + G::K_STAGES * G::K_BYTES;
+  const uint32_t qbuf_lds = kbuf_lds + G::LDS_BYTES;   // multi-block launches only
 
   // ---- work item (XCD-aware remap of the linear workgroup id)
   const int w = blockIdx.x;
@@ -433,10 +450,11 @@ void attn_fwd_kernel(AttnArgs a) {
   const int half = DV < DK ? L2 & 1 : 0;
   const int L = DV < DK ? L2 >> 1 : L2;
   const int dv_off = half * DV;  // first O column / V^T row of this workgroup
-  const int per_bh = a.n_qblocks * a.kv_splits;
+  const int per_bh = MULTI ? a.wg_per_bh : a.n_qblocks * a.kv_splits;
   const int bh = L / per_bh;
-  const int qb = (L - bh * per_bh) / a.kv_splits;
-  const int split = L - bh * per_bh - qb * a.kv_splits;
+  const int qb = MULTI ? (L - bh * per_bh) * a.qb_per_wg : (L - bh * per_bh) / a.kv_splits;
+  const int split = MULTI ? 0 : L - bh * per_bh - qb * a.kv_splits;
+  const int nblk = MULTI ? min(a.qb_per_wg, a.n_qblocks - qb) : 1;  // query blocks
   const int b = bh / a.H, h = bh - b * a.H;
 
   const int tid = threadIdx.x;
@@ -446,9 +464,11 @@ void attn_fwd_kernel(AttnArgs a) {
   const int lq = lane & 31;  // query column / operand row inside a 32x32 tile
   const int lg = lane >> 5;  // k-slot group (32 bytes)
 
-  const int q_block0 = qb * BLOCK_M;
-  const int q_wave0 = q_block0 + wave * QROWS;
-  const int q = q_wave0 + lq;  // this lane's query
+  // this workgroup's current query block, this wave's and this lane's first
+  // query in it (they advance at block boundaries of a multi-block launch)
+  int q_block0 = qb * BLOCK_M;
+  int q_wave0 = q_block0 + wave * QROWS;
+  int q = q_wave0 + lq;
 
   const uint8_t* qh = a.q + (int64_t)bh * a.Sq * D;
   const uint8_t* kh = a.k + (int64_t)bh * a.Skv * D;
@@ -516,16 +536,44 @@ void attn_fwd_kernel(AttnArgs a) {
     *reinterpret_cast<i32x4*>(vbuf + 2 * G::V_BYTES + o) = i32x4{0, 0, 0, 0};
 
   // ---- Q^T operand (B operand of S^T), resident for the whole kernel
-  i32x8 qop[G::KSTEPS];
-  if constexpr (DK < 64) {
-    // one 64-deep step over a 32-byte row: k-slot group 1 is zero padding
-    const i32x4* src = reinterpret_cast<const i32x4*>(qh + (int64_t)min(q, a.Sq - 1) * D);
-    qop[0] = lg == 0 ? cat8(src[0], src[1]) : i32x8{};
-  } else {
-    const i32x4* src = reinterpret_cast<const i32x4*>(qh + (int64_t)min(q, a.Sq - 1) * D + 32 * lg);
+  auto load_q = [&](i32x8 (&dst)[G::KSTEPS], int qrow) {
+    if constexpr (DK < 64) {
+      // one 64-deep step over a 32-byte row: k-slot group 1 is zero padding
+      const i32x4* src = reinterpret_cast<const i32x4*>(qh + (int64_t)min(qrow, a.Sq - 1) * D);
+      dst[0] = lg == 0 ? cat8(src[0], src[1]) : i32x8{};
+    } else {
+      const i32x4* src =
+          reinterpret_cast<const i32x4*>(qh + (int64_t)min(qrow, a.Sq - 1) * D + 32 * lg);
 #pragma unroll
-    for (int ks = 0; ks < G::KSTEPS; ++ks) qop[ks] = cat8(src[4 * ks], src[4 * ks + 1]);
-  }
+      for (int ks = 0; ks < G::KSTEPS; ++ks) dst[ks] = cat8(src[4 * ks], src[4 * ks + 1]);
+    }
+  };
+  i32x8 qop[G::KSTEPS];
+  load_q(qop, q);
+  // Multi-block launches: the loading waves fetch block k+1's Q into LDS
+  // buffer (k+1) % 2 while block k runs (direct-to-LDS, like the tiles; one
+  // KiB of rows per instruction, rows past Sq re-read row Sq-1), and every
+  // wave reads its Q^T operand from there at the switch.
+  auto issue_q = [&](int blk_next) __attribute__((always_inline)) {
+    const int row0 = (qb + blk_next) * BLOCK_M;   // < Sq: blk_next < nblk
+    const uint8_t* base = qh + (int64_t)row0 * D;
+    const uint32_t dst = qbuf_lds + (uint32_t)((blk_next & 1) * Q_BYTES);
+#pragma unroll
+    for (int n = 0; n < Q_LOADS; ++n) {
+      const int p = ((n * 4 + (wave & 3)) * 1024 + 16 * lane);   // byte in the buffer
+      const int row = min(row0 + p / D, a.Sq - 1) - row0;
+      gload_lds16_s(base, (uint32_t)(row * D + p % D), dst + (uint32_t)((n * 4 + (wave & 3)) * 1024));
+    }
+  };
+  auto read_q = [&](int blk) __attribute__((always_inline)) {
+    const uint32_t src = qbuf_lds + (uint32_t)((blk & 1) * Q_BYTES) + (uint32_t)((wave * QROWS + lq) * D);
+    if constexpr (DK < 64) {
+      qop[0] = lg == 0 ? lds_op(src) : i32x8{};
+    } else {
+#pragma unroll
+      for (int ks = 0; ks < G::KSTEPS; ++ks) qop[ks] = lds_op(src + 32 * lg + 64 * ks);
+    }
+  };
 
   // per-lane LDS byte offsets of the operand reads (inside one stage): row
   // lq of each 32-row operand block, k-slot group lg; the rest is immediate
@@ -543,6 +591,65 @@ void attn_fwd_kernel(AttnArgs a) {
   __syncthreads();
   if (group == 1) __syncthreads();  // group 1 starts half a step behind
 
+  // out = acc * v_scale / l for query row qrow (acc carries P*448, l sums
+  // P*448); every lane takes part (the row sum combines lane pairs)
+  auto store_out = [&](int qrow, float l_lane) __attribute__((always_inline)) {
+    const float l = xhalf_sum(l_lane);
+    const float inv = v_scale / l;
+    uint2 pend = make_uint2(0u, 0u);
+    if (qrow < a.Sq) {
+      const int64_t obase =
+          (int64_t)b * a.osb + (int64_t)h * a.osh + (int64_t)qrow * a.oss + dv_off;
+#pragma unroll
+      for (int e = 0; e < G::ETILES; ++e)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int d = 32 * e + 8 * i + 4 * lg;
+          const float o0 = acc[e][4 * i + 0] * inv, o1 = acc[e][4 * i + 1] * inv;
+          const float o2 = acc[e][4 * i + 2] * inv, o3 = acc[e][4 * i + 3] * inv;
+          if constexpr (OUT == kOutF32) {
+            *reinterpret_cast<float4*>(static_cast<float*>(a.out) + obase + d) =
+                make_float4(o0, o1, o2, o3);
+          } else {
+            uint2 pk;
+            if constexpr (OUT == kOutF16) {
+              pk.x = pack_f16x2(o0, o1);
+              pk.y = pack_f16x2(o2, o3);
+            } else {
+              pk.x = pack_bf16x2(o0, o1);
+              pk.y = pack_bf16x2(o2, o3);
+            }
+            // Chunk c = 4e + i (columns 8c .. 8c+7) of this row is split
+            // over the lane pair (l, l+32): columns 8c..8c+3 here when
+            // lg = 0, 8c+4..8c+7 when lg = 1.  For the chunk pair (c, c+1),
+            // i even, swapping chunk c+1's low half of the lower lane with
+            // chunk c's high half of the upper lane leaves lane lg = 0 with
+            // all of chunk c and lane lg = 1 with all of chunk c+1: one
+            // 16-byte store each, the pair writing 32 contiguous bytes.
+            if (i % 2 == 0) {
+              pend = pk;
+            } else {
+              // pend: chunk c (= 4e + i - 1) part, pk: chunk c+1 part
+              const auto x = __builtin_amdgcn_permlane32_swap(pend.x, pk.x, false, false);
+              const auto y = __builtin_amdgcn_permlane32_swap(pend.y, pk.y, false, false);
+              const uint4 v = make_uint4(x[0], y[0], x[1], y[1]);
+              const int c = 4 * e + i - 1 + lg;   // the chunk this lane now holds
+              *reinterpret_cast<uint4*>(static_cast<uint16_t*>(a.out) + obase + 8 * c) = v;
+            }
+          }
+        }
+    }
+  };
+
+  // Tiles of the workgroup, in stream order: n_kb per query block.  A
+  // multi-block launch runs its blocks as one stream: at the first tile of a
+  // block the wave switches to that block's Q^T (loaded one block ahead) and
+  // restarts the running max at -inf, so alpha of that tile is exp2(-inf) = 0
+  // and clears O^T and l; the finished block's output is stored first, at
+  // the start of the following softmax phase, when its last PV is done.
+  const int T = MULTI ? nblk * n_kb : n_kb;
+  float l_done = 0.0f;   // multi-block: row sum of the block awaiting its store
+
   // The two groups run separate copies of the loop, so that each MFMA phase
   // is one branch-free block: group 0 issues the tile loads, group 1 none.
   auto run = [&](auto loads_c) {
@@ -550,15 +657,30 @@ void attn_fwd_kernel(AttnArgs a) {
     // alpha: rescale of tile i's row statistics, applied to l in SOFTMAX(i)
     // and to O^T in MFMA(i+1), before PV(i) accumulates
     float alpha = 1.0f, moff = 0.0f;
-    for (int i = 0; i <= n_kb; ++i) {
+    for (int i = 0; i <= T; ++i) {
       // ================= MFMA(i) =================
+      const int j = MULTI ? i % n_kb : i;  // tile of the current query block
+      const int blk = MULTI ? i / n_kb : 0;  // query block of the workgroup
+      if constexpr (MULTI) {
+        // the loading group stores the finished block here, ahead of this
+        // phase's tile loads (its counted waits then never cover stores)
+        if (LOADS && i >= 2 && (i - 1) % n_kb == 0 && i - 1 < T)
+          store_out(q - BLOCK_M, l_done);
+        if (j == 0 && i > 0 && i < T) {
+          read_q(blk);
+          m_run = -__builtin_inff();
+          q_block0 += BLOCK_M;
+          q_wave0 += BLOCK_M;
+          q += BLOCK_M;
+        }
+      }
       if (!LOADS) __builtin_amdgcn_s_setprio(1);  // the MFMA phase issues first on its SIMD
       // Tile j is issued by group 0 during MFMA(j-1), after workgroup barrier
       // 2j-2, and waited for at the end of SOFTMAX(j-1), before barrier 2j
       // (the prologue's barrier is number 0).  Every MFMA phase runs both
       // products: in the first one P is zero and V^T stage 2 holds zeros
       // (cleared in the prologue), in the last one the S^T result is unused.
-      const int kv0 = kv_begin + i * kBlockN;
+      const int kv0 = kv_begin + j * kBlockN;
       const bool tail = kv0 + kBlockN > a.Skv;
       // operand base addresses of this phase's K and V^T stages; opaque to
       // the compiler, so every read is one register plus an immediate
@@ -567,7 +689,7 @@ void attn_fwd_kernel(AttnArgs a) {
       asm("" : "+v"(kl), "+v"(vl));
       // group 0 issues tile i+1; past the last tile it re-reads the last one
       // into the stages tile i+1 would use, which are free (see above)
-      const TileDst nxt = tile_dst(min(i + 1, n_kb - 1), i + 1);
+      const TileDst nxt = tile_dst(min(i + 1, T - 1) % n_kb, i + 1);
       // Without a window mask the row max is taken between the PV MFMAs, over
       // the raw scores: rows past Skv duplicate key Skv-1, and the keys a
       // shifted last tile repeats were in the tile before, so the raw max is
@@ -577,7 +699,13 @@ void attn_fwd_kernel(AttnArgs a) {
       // the masked scores.
       float mh[8];
       mfma_phase<DK, DV, LOADS, !WINDOW>(kl, vl, qop, pop, s, acc, alpha, mh, tl, nxt);
-      if (i < n_kb) {
+      // the next block's Q, after the tile loads (so a counted wait can leave
+      // it in flight)
+      const bool q_issued = MULTI && LOADS && j == 0 && blk + 1 < nblk;
+      if constexpr (MULTI && LOADS) {
+        if (q_issued) issue_q(blk + 1);
+      }
+      if (i < T) {
         bool masked = tail;
         if (a.mask == RP_MASK_CAUSAL) masked |= kv0 + kBlockN - 1 > q_wave0;
         if (a.mask == RP_MASK_SHARED_PREFIX) masked |= kv0 + kBlockN > a.prefix;
@@ -593,7 +721,7 @@ void attn_fwd_kernel(AttnArgs a) {
           }
           const int pre_end = a.mask == RP_MASK_SHARED_PREFIX ? min(a.prefix, a.Skv) : 0;
           // keys before kv0 are the shifted last tile's repeats
-          const int kvl = tile_begin(i) + 32 * lg;
+          const int kvl = tile_begin(j) + 32 * lg;
           const int lo_t = lo - kvl, hi_t = hi - kvl, pe_t = pre_end - kvl, new_t = kv0 - kvl;
   #pragma unroll
           for (int hh = 0; hh < 4; ++hh)
@@ -605,7 +733,7 @@ void attn_fwd_kernel(AttnArgs a) {
             }
         }
         float mx;
-        if (!WINDOW && !(i == 0 && tile_begin(0) != kv0)) {
+        if (!WINDOW && !(j == 0 && tile_begin(0) != kv0)) {
           constexpr int NP = 2 * G::ETILES;   // partial maxima mh[0 .. NP)
           if constexpr (NP == 2) {
             mx = max3f(mh[0], mh[1], mh[1]);
@@ -637,7 +765,13 @@ void attn_fwd_kernel(AttnArgs a) {
       __syncthreads();
 
       // ================= SOFTMAX(i) =================
-      if (i < n_kb) {
+      if constexpr (MULTI) {
+        if (j == 0 && i > 0 && i < T) {
+          l_done = l_run;   // the finished block's row sum, before this tile's update
+          if (!LOADS) store_out(q - BLOCK_M, l_done);
+        }
+      }
+      if (i < T) {
         float ps[4] = {-0.0f, -0.0f, -0.0f, -0.0f};  // x + -0 == x: no first add
   #pragma unroll
         for (int m = 0; m < 2; ++m) {
@@ -657,7 +791,12 @@ void attn_fwd_kernel(AttnArgs a) {
         }
         l_run = l_run * alpha + ((ps[0] + ps[1]) + (ps[2] + ps[3]));
       }
-      if (LOADS) wait_vmem_all();
+      if constexpr (LOADS) {
+        // tile i+1 must have landed; Q loads issued in this phase may stay
+        // in flight unless the next tile opens the block that reads them
+        if (MULTI && q_issued && j + 1 < n_kb) wait_vmem_n<Q_LOADS>();
+        else wait_vmem_all();
+      }
       __syncthreads();
     }
   };
@@ -668,9 +807,9 @@ void attn_fwd_kernel(AttnArgs a) {
     run(std::false_type{});
   }
 
-  // ---- epilogue: out = acc * v_scale / l  (acc carries P*448, l sums P*448)
-  const float l = xhalf_sum(l_run);
+  // ---- epilogue: the (last) query block's output, or a split's partials
   if constexpr (OUT == kOutSplit) {
+    const float l = xhalf_sum(l_run);
     // partial result of this key split, relative to its own running max
     if (q < a.Sq) {
       const int64_t row = ((int64_t)split * a.B * a.H + bh) * a.Sq + q;
@@ -686,32 +825,7 @@ void attn_fwd_kernel(AttnArgs a) {
     }
     return;
   }
-  const float inv = v_scale / l;
-  if (q < a.Sq) {
-    const int64_t obase = (int64_t)b * a.osb + (int64_t)h * a.osh + (int64_t)q * a.oss + dv_off;
-#pragma unroll
-    for (int e = 0; e < G::ETILES; ++e)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int d = 32 * e + 8 * i + 4 * lg;
-        const float o0 = acc[e][4 * i + 0] * inv, o1 = acc[e][4 * i + 1] * inv;
-        const float o2 = acc[e][4 * i + 2] * inv, o3 = acc[e][4 * i + 3] * inv;
-        if constexpr (OUT == kOutF32) {
-          *reinterpret_cast<float4*>(static_cast<float*>(a.out) + obase + d) =
-              make_float4(o0, o1, o2, o3);
-        } else {
-          uint2 pk;
-          if constexpr (OUT == kOutF16) {
-            pk.x = pack_f16x2(o0, o1);
-            pk.y = pack_f16x2(o2, o3);
-          } else {
-            pk.x = pack_bf16x2(o0, o1);
-            pk.y = pack_bf16x2(o2, o3);
-          }
-          *reinterpret_cast<uint2*>(static_cast<uint16_t*>(a.out) + obase + d) = pk;
-        }
-      }
-  }
+  store_out(q, l_run);
 }
 
 // Merge the key splits of one query row: with m_j, l_j, O_j the running
@@ -775,10 +889,48 @@ template <int D, int OUT>
 void launch_fwd(const AttnArgs& a, hipStream_t st) {
   constexpr int DV = kPVWidth<D>;
   const dim3 grid(a.n_work), block(512);
+  if constexpr (OUT != kOutSplit && DV == D) {
+    if (a.qb_per_wg > 1) {
+      hipLaunchKernelGGL((attn_fwd_kernel<D, DV, OUT, false, true>), grid, block, 0, st, a);
+      return;
+    }
+  }
   if (a.mask != RP_MASK_NONE)
-    hipLaunchKernelGGL((attn_fwd_kernel<D, DV, OUT, true>), grid, block, 0, st, a);
+    hipLaunchKernelGGL((attn_fwd_kernel<D, DV, OUT, true, false>), grid, block, 0, st, a);
   else
-    hipLaunchKernelGGL((attn_fwd_kernel<D, DV, OUT, false>), grid, block, 0, st, a);
+    hipLaunchKernelGGL((attn_fwd_kernel<D, DV, OUT, false, false>), grid, block, 0, st, a);
+}
+
+// Multi-block launches pay off where a workgroup's fixed cost (Q load,
+// first-tile latency, pipeline fill and drain, output store, all serialised
+// with one workgroup per CU) is large against its key tiles: short,
+// unmasked key ranges.  Costs in units of one key tile's time: a workgroup's
+// fixed cost is ~7 tiles (measured: a Skv sweep at the Wan query shape
+// extrapolates to 0.51 ms at Skv = 0 against 0.074 ms per 128 keys over 46
+// rounds of workgroups), and a block switch inside a multi-block workgroup
+// costs about one to two tiles (measured on the same sweep; the plans do not
+// change between the two).  Returns the query blocks per workgroup (1: off)
+// that minimises rounds-of-256-workgroups x workgroup time.
+constexpr int kMultiMaxTiles = 32;  // key tiles per block up to which it applies
+constexpr int kCUs = 256;
+constexpr int64_t kFixedTiles = 7, kSwitchTiles = 1;
+inline int multi_block_plan(const AttnArgs& a, int D) {
+  const int n_kb = (a.Skv + kBlockN - 1) / kBlockN;
+  const int64_t heads = (int64_t)a.B * a.H;
+  if (a.mask != RP_MASK_NONE || a.kv_splits != 1 || D > 128 || n_kb > kMultiMaxTiles)
+    return 1;
+  auto rounds = [&](int64_t wgs) { return (wgs + kCUs - 1) / kCUs; };
+  int best = 1;
+  int64_t best_cost = rounds(heads * a.n_qblocks) * (n_kb + kFixedTiles);
+  for (int per = 2; per <= a.n_qblocks; ++per) {
+    const int64_t wgs = heads * ((a.n_qblocks + per - 1) / per);
+    const int64_t cost = rounds(wgs) * (per * (n_kb + kSwitchTiles) + kFixedTiles);
+    if (cost < best_cost) {
+      best = per;
+      best_cost = cost;
+    }
+  }
+  return best;
 }
 
 constexpr int kBlockM = 32 * 8;  // query rows per workgroup
@@ -804,7 +956,11 @@ int launch_attn(const AttnArgs& base, int out_dtype, hipStream_t st) {
   a.n_qblocks = (a.Sq + kBlockM - 1) / kBlockM;
   a.D = D;
   a.dv_halves = D / kPVWidth<D>;
-  const int64_t work = (int64_t)a.n_qblocks * a.B * a.H * a.kv_splits * a.dv_halves;
+  a.qb_per_wg = multi_block_plan(a, D);
+  a.wg_per_bh = (a.n_qblocks + a.qb_per_wg - 1) / a.qb_per_wg;
+  const int64_t work = a.qb_per_wg > 1
+                           ? (int64_t)a.wg_per_bh * a.B * a.H
+                           : (int64_t)a.n_qblocks * a.B * a.H * a.kv_splits * a.dv_halves;
   if (work > 0x7fffffff || (int64_t)a.B * a.H * a.Sq * (D / 4) > 0x7fffffffLL * 256) {
     rp_set_error("attn: grid too large");
     return RP_ERR_UNSUPPORTED;
@@ -934,6 +1090,18 @@ extern "C" int rp_fp8_attn_fwd(const uint8_t* q8, const uint8_t* k8, const uint8
                             sm_scale, out, out_dtype, osb, osh, oss, B, H, Sq, Skv, D, mask,
                             prefix_len, suffix_len);
   return rc != RP_OK ? rc : attn_run(a, D, out_dtype, stream);
+}
+
+extern "C" int rp_fp8_attn_blocks_per_workgroup(int B, int H, int Sq, int Skv, int D, int mask,
+                                               int kv_splits) {
+  if (B <= 0 || H <= 0 || Sq <= 0 || Skv <= 0 || kv_splits < 1) return 0;
+  AttnArgs a{};
+  a.B = B; a.H = H; a.Sq = Sq; a.Skv = Skv; a.mask = mask;
+  int split_tiles = 0, n_splits = 1;
+  split_plan(Skv, kv_splits, &split_tiles, &n_splits);
+  a.kv_splits = n_splits;
+  a.n_qblocks = (Sq + kBlockM - 1) / kBlockM;
+  return multi_block_plan(a, D);
 }
 
 extern "C" size_t rp_fp8_attn_workspace_bytes(int B, int H, int Sq, int D, int kv_splits) {

@@ -164,3 +164,22 @@ def test_rmsnorm_workspace_sizing() -> None:
     assert L.rp_fp8_rmsnorm_quant_workspace_bytes(1, 2, 64, 128, 1) == 1 * 4
     assert L.rp_fp8_rmsnorm_quant_workspace_bytes(1, 40, 75600, 128, 0) == 40 * 591 * 4
     assert L.rp_fp8_rmsnorm_quant_workspace_bytes(1, 2, 64, 96, 0) == 0
+
+
+def test_multi_block_launch_plan() -> None:
+    """Which shapes stream several query blocks per workgroup (short,
+    unmasked key ranges with many query blocks), and that the others keep
+    one block per workgroup."""
+    L = _capi.lib()
+    plan = L.rp_fp8_attn_blocks_per_workgroup
+    assert plan(1, 40, 75600, 512, 128, 0, 1) == 50          # Wan cross: 240 workgroups
+    assert plan(1, 40, 75600, 75600, 128, 0, 1) == 1         # Wan self: long key range
+    assert plan(1, 40, 75600, 512, 128, 1, 1) == 1           # causal mask
+    assert plan(1, 40, 75600, 512, 128, 2, 1) == 1           # shared-prefix mask
+    assert plan(1, 40, 75600, 512, 256, 0, 1) == 1           # head dim 256 (two halves)
+    assert plan(1, 40, 75600, 512, 128, 0, 4) == 1           # key splits
+    assert plan(1, 40, 75600, 100, 128, 0, 8) > 1            # one tile: no split happens
+    assert plan(1, 8, 1024, 1024, 64, 0, 1) == 1             # C1: 32 blocks in all
+    assert plan(1, 40, 75600, 4096, 128, 0, 1) > 1           # 32 tiles: still pays
+    assert plan(1, 40, 75600, 4097, 128, 0, 1) == 1          # 33 tiles: off
+    assert plan(0, 40, 75600, 512, 128, 0, 1) == 0           # invalid

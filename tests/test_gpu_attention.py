@@ -156,6 +156,53 @@ def test_fp16_and_bf16_outputs_are_one_rounding_of_fp32(gpu: torch.device) -> No
         assert torch.equal(ob, o32.to(torch.bfloat16))
 
 
+MULTI_CASES = [
+    # name, B, H, Sq, Skv, D, dtype, out_dtype: shapes on which a workgroup
+    # streams several query blocks (rp_fp8_attn_blocks_per_workgroup > 1);
+    # ragged Sq, a key range shorter than one tile, a shifted last tile
+    ("d64_one_partial_tile", 1, 64, 16384 + 77, 100, 64, torch.bfloat16, torch.float32),
+    ("d128_shifted_tail", 2, 20, 12000, 300, 128, torch.bfloat16, torch.bfloat16),
+    ("d32_fp16", 1, 48, 8192 + 5, 512, 32, torch.float16, torch.float16),
+    ("d128_wan_cross_like", 1, 40, 9000, 512, 128, torch.bfloat16, torch.float32),
+]
+
+
+@pytest.mark.parametrize("case", MULTI_CASES, ids=[c[0] for c in MULTI_CASES])
+def test_multi_block_launches_vs_oracle(gpu: torch.device, case: tuple) -> None:
+    """Rows at the start, at block boundaries and at the end of workgroups'
+    block streams, against the oracle; the launch takes the multi-block path."""
+    from oracle import quant
+    from repercep_runtime_amd import _capi
+
+    name, B, H, Sq, Skv, D, dtype, out_dtype = case
+    per = _capi.lib().rp_fp8_attn_blocks_per_workgroup(B, H, Sq, Skv, D, 0, 1)
+    assert per > 1, f"{name}: not a multi-block launch"
+    g = torch.Generator().manual_seed(sum(map(ord, name)))
+    q = torch.randn(B, H, Sq, D, generator=g).to(dtype)
+    k = torch.randn(B, H, Skv, D, generator=g).to(dtype)
+    v = torch.randn(B, H, Skv, D, generator=g).to(dtype)
+    out = ops.fp8_flash_attention(q.to(gpu), k.to(gpu), v.to(gpu), out_dtype=out_dtype)
+    out = out.float().cpu().numpy()
+    blk = 256 * per   # query rows of one workgroup
+    rows = set()
+    for w0 in range(0, Sq, blk):
+        for r in (w0, w0 + 1, w0 + 255, w0 + 256, w0 + 257, w0 + blk - 1, w0 + blk // 2):
+            rows.add(min(r, Sq - 1))
+    rows |= {Sq - 1, Sq - 2}
+    rows = np.array(sorted(rows))
+    for b in range(B):
+        sl = slice(b, b + 1)
+        qs, q8 = quant.quantize_codes(q[sl])
+        ks, k8 = quant.quantize_codes(k[sl])
+        vs, v8 = quant.quantize_codes(v[sl])
+        for h in (0, H // 2, H - 1):
+            ref = native.attn_rows(q8[0, h], k8[0, h], v8[0, h], qs[h], ks[h], vs[h],
+                                   D ** -0.5, rows, block_n=ops.BLOCK_N)
+            if out_dtype != torch.float32:
+                ref = torch.from_numpy(ref).to(out_dtype).float().numpy()
+            _check(out[b, h, rows], ref, f"{name} per={per} b={b} h={h}")
+
+
 def test_per_tensor_granularity(gpu: torch.device) -> None:
     g = torch.Generator().manual_seed(5)
     q, k, v = (torch.randn(1, 4, 600, 128, generator=g).mul(1 + i).to(torch.bfloat16)
