@@ -161,10 +161,9 @@ def bench_attention(args, cfg) -> dict:
         if fused_norm:
             qs, q8 = ops.rmsnorm_scale_quantize(q)
             ks, k8 = ops.rmsnorm_scale_quantize(k)
-        else:
-            qs, q8 = ops.scale_quantize(q, "bh", "bhsd")
-            ks, k8 = ops.scale_quantize(k, "bh", "bhsd")
-        vs, vt8 = ops.scale_quantize(v, "bh", "bhds")
+            vs, vt8 = ops.scale_quantize(v, "bh", "bhds")
+        else:   # what fp8_flash_attention runs: one library call for Q, K, V
+            qs, q8, ks, k8, vs, vt8 = ops.scale_quantize_qkv(q, k, v, "bh")
         if ev is not None:
             ev[1].record(st)
         ops.attention_fp8(q8.view(torch.uint8), k8.view(torch.uint8), vt8.view(torch.uint8),
@@ -198,6 +197,33 @@ def bench_attention(args, cfg) -> dict:
     quant_ms = sum(e[0].elapsed_time(e[1]) for e in evs) / len(evs)
     attn_ms = sum(e[1].elapsed_time(e[2]) for e in evs) / len(evs)
     log(f"[bench] split: quantize {quant_ms:.3f} ms, attention kernel {attn_ms:.3f} ms")
+
+    graph = None
+    if args.graph:
+        # the same step captured in a HIP graph and replayed: what a serving
+        # loop runs when host launch work bounds small calls
+        g = torch.cuda.CUDAGraph()
+        s2 = torch.cuda.Stream(dev)
+        s2.wait_stream(st)
+        with torch.cuda.stream(s2):
+            step()   # warm the capture stream's allocator pool
+        st.wait_stream(s2)
+        torch.cuda.synchronize()
+        with torch.cuda.graph(g):
+            step()
+        for _ in range(args.warmup):
+            g.replay()
+        torch.cuda.synchronize()
+        t0.record(st)
+        for _ in range(args.steps):
+            g.replay()
+        t1.record(st)
+        torch.cuda.synchronize()
+        g_ms = t0.elapsed_time(t1) / args.steps
+        graph = {"ms_per_step": round(g_ms, 4),
+                 "value": round(cfg.flops / (g_ms * 1e-3) / 1e12, 2),
+                 "note": "the step captured once with torch.cuda.graph, then replayed"}
+        log(f"[bench] graph replay: {g_ms:.4f} ms/step")
 
     tflops_step = cfg.flops / (ms_per_step * 1e-3) / 1e12
     tflops_attn = cfg.flops / (attn_ms * 1e-3) / 1e12
@@ -237,8 +263,10 @@ def bench_attention(args, cfg) -> dict:
             "bytes": qbytes,
             "note": ("Q, K: RMSNorm fused into amax pass + finalize + apply; V: amax pass + "
                      "finalize + apply (transposed); 5 B/element" if fused_norm else
-                     "Q, K, V: amax pass + finalize + apply (V transposed), 5 B/element"),
+                     "Q, K, V: one multi-tensor amax pass + finalize + apply (V "
+                     "transposed), 5 B/element"),
         },
+        **({"graph": graph} if graph else {}),
     }
     del q, k, v, out
     return res
@@ -339,6 +367,9 @@ def main() -> int:
                     help="run one device-to-device copy of this many MiB first, so a "
                          "rocprofv3 --pmc FETCH_SIZE/WRITE_SIZE run can scale the counters "
                          "against a plain copy of known size")
+    ap.add_argument("--graph", action="store_true",
+                    help="attention configs: also time the step captured in a HIP graph and "
+                         "replayed (small calls are bound by host launch work)")
     ap.add_argument("--library-gemm", action="store_true",
                     help="c4_wan_ffn_up only: also time the vendor library's FP8 GEMM "
                          "(torch._scaled_mm) on the same operands, for comparison")

@@ -111,6 +111,24 @@ int rp_fp8_scale_quantize(const void* x, int x_dtype, int64_t B, int64_t H, int6
                           float* dequant_out, uint8_t* codes, int layout, int64_t ld,
                           void* workspace, size_t workspace_bytes, void* stream);
 
+/* Q, K and V of one attention call in one call: the scales and codes of
+ * rp_fp8_scale_quantize for q and k ((B, H, S, D) codes) and for v (V^T,
+ * (B, H, D, ldv)), from four kernel launches (amax of all three, their
+ * scales, q and k codes, V^T codes) instead of nine -- launches bound small
+ * calls.  dequant_out: float[3 * G], G = B*H (RP_SCALE_PER_BH) or 1, in the
+ * order q, k, v.  workspace: rp_fp8_quant_qkv_workspace_bytes, 256-byte
+ * aligned.  Replaces the three _per_bh_scale + _quantize pairs at
+ * kernels/triton_kernels/fp8_flash_attn.py:522-528 with one host call. */
+size_t rp_fp8_quant_qkv_workspace_bytes(int64_t B, int64_t H, int64_t Sq, int64_t Skv,
+                                        int64_t D, int granularity);
+int rp_fp8_scale_quantize_qkv(const void* q, const void* k, const void* v, int x_dtype,
+                              int64_t B, int64_t H, int64_t Sq, int64_t Skv, int64_t D,
+                              int64_t qsb, int64_t qsh, int64_t qss, int64_t ksb, int64_t ksh,
+                              int64_t kss, int64_t vsb, int64_t vsh, int64_t vss,
+                              int granularity, float* dequant_out, uint8_t* q8, uint8_t* k8,
+                              uint8_t* vt8, int64_t ldv, void* workspace,
+                              size_t workspace_bytes, void* stream);
+
 /* --------------------------------------------------------- attention
  * FP8 flash-attention forward, FA-2 online softmax in fp32, both dot
  * products on gfx950 e4m3 MFMAs, P re-quantized as e4m3fn(p * 448).

@@ -35,7 +35,9 @@ RP_ROPE_INTERLEAVED = 2
 EXPORTS = (
     "rp_abi_version", "rp_status_string", "rp_last_error",
     "rp_fp8_quant_workspace_bytes", "rp_fp8_scale", "rp_fp8_quantize",
-    "rp_fp8_scale_quantize", "rp_fp8_attn_fwd", "rp_fp8_attn_workspace_bytes",
+    "rp_fp8_scale_quantize", "rp_fp8_quant_qkv_workspace_bytes", "rp_fp8_scale_quantize_qkv",
+    "rp_fp8_attn_fwd",
+    "rp_fp8_attn_workspace_bytes",
     "rp_fp8_attn_blocks_per_workgroup",
     "rp_fp8_attn_fwd_split", "rp_fp8_rmsnorm_quant_workspace_bytes",
     "rp_fp8_rmsnorm_scale_quantize", "rp_fp8_gemm", "rp_fp8_transpose",
@@ -75,6 +77,11 @@ def _declare(L: ctypes.CDLL) -> None:
     L.rp_fp8_scale_quantize.restype = _int
     L.rp_fp8_scale_quantize.argtypes = [_vp, _int, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
                                         _int, _vp, _vp, _int, _i64, _vp, _sz, _vp]
+    L.rp_fp8_quant_qkv_workspace_bytes.restype = _sz
+    L.rp_fp8_quant_qkv_workspace_bytes.argtypes = [_i64] * 5 + [_int]
+    L.rp_fp8_scale_quantize_qkv.restype = _int
+    L.rp_fp8_scale_quantize_qkv.argtypes = ([_vp, _vp, _vp, _int] + [_i64] * 14
+                                            + [_int, _vp, _vp, _vp, _vp, _i64, _vp, _sz, _vp])
     L.rp_fp8_attn_fwd.restype = _int
     L.rp_fp8_attn_fwd.argtypes = [_vp, _vp, _vp, _i64, _vp, _vp, _vp, _int, _f32, _vp, _int,
                                   _i64, _i64, _i64, _int, _int, _int, _int, _int, _int, _int,

@@ -75,8 +75,8 @@ __device__ __forceinline__ uint32_t pk_umax16(uint32_t a, uint32_t b) {
   return lo | (hi << 16);
 }
 
-__global__ __launch_bounds__(kQThreads) void amax_partial_kernel(QParams p, uint32_t* partial) {
-  const int64_t blk = blockIdx.x;
+__device__ __forceinline__ void amax_partial_body(int64_t blk_id, QParams p, uint32_t* partial) {
+  const int64_t blk = blk_id;
   const int64_t g = blk / p.nbg;
   const int64_t j = blk - g * p.nbg;
   const int64_t first = j * p.rpb;
@@ -113,10 +113,14 @@ __global__ __launch_bounds__(kQThreads) void amax_partial_kernel(QParams p, uint
   }
 }
 
+__global__ __launch_bounds__(kQThreads) void amax_partial_kernel(QParams p, uint32_t* partial) {
+  amax_partial_body(blockIdx.x, p, partial);
+}
+
 template <int DT>
-__global__ __launch_bounds__(kQThreads) void scale_finalize_kernel(const uint32_t* partial,
+__device__ __forceinline__ void scale_finalize_body(int64_t blk_id, const uint32_t* partial,
                                                                    int64_t nbg, float* dequant) {
-  const int64_t g = blockIdx.x;
+  const int64_t g = blk_id;
   uint32_t m = 0;
   for (int64_t i = threadIdx.x; i < nbg; i += kQThreads) m = umax32(m, partial[g * nbg + i]);
 #pragma unroll
@@ -130,6 +134,12 @@ __global__ __launch_bounds__(kQThreads) void scale_finalize_kernel(const uint32_
     for (int w = 1; w < kQThreads / kWave; ++w) r = umax32(r, wmax[w]);
     dequant[g] = dequant_from_amax<DT>(r);
   }
+}
+
+template <int DT>
+__global__ __launch_bounds__(kQThreads) void scale_finalize_kernel(const uint32_t* partial,
+                                                                   int64_t nbg, float* dequant) {
+  scale_finalize_body<DT>(blockIdx.x, partial, nbg, dequant);
 }
 
 template <int DT>
@@ -149,9 +159,9 @@ __device__ __forceinline__ uint32_t quant4(uint32_t lo_pair, uint32_t hi_pair, f
 constexpr int kFlatLoads = kElemsPerBlock / 8 / kQThreads;  // 16-byte loads per thread
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
-__global__ __launch_bounds__(kQThreads) void amax_flat_kernel(const uint16_t* x, int64_t gsize,
+__device__ __forceinline__ void amax_flat_body(int64_t blk_id, const uint16_t* x, int64_t gsize,
                                                               int64_t nbg, uint32_t* partial) {
-  const int64_t blk = blockIdx.x;
+  const int64_t blk = blk_id;
   const int64_t g = blk / nbg;
   const int64_t j = blk - g * nbg;
   const int64_t start = g * gsize + j * kElemsPerBlock;
@@ -185,11 +195,16 @@ __global__ __launch_bounds__(kQThreads) void amax_flat_kernel(const uint16_t* x,
   }
 }
 
+__global__ __launch_bounds__(kQThreads) void amax_flat_kernel(const uint16_t* x, int64_t gsize,
+                                                              int64_t nbg, uint32_t* partial) {
+  amax_flat_body(blockIdx.x, x, gsize, nbg, partial);
+}
+
 template <int DT>
-__global__ __launch_bounds__(kQThreads) void quant_flat_kernel(const uint16_t* x, int64_t gsize,
+__device__ __forceinline__ void quant_flat_body(int64_t blk_id, const uint16_t* x, int64_t gsize,
                                                                int64_t nbg, const float* dequant,
                                                                int per_bh, uint8_t* codes) {
-  const int64_t blk = blockIdx.x;
+  const int64_t blk = blk_id;
   const int64_t g = blk / nbg;
   const int64_t j = blk - g * nbg;
   const int64_t start = g * gsize + j * kElemsPerBlock;
@@ -215,11 +230,18 @@ __global__ __launch_bounds__(kQThreads) void quant_flat_kernel(const uint16_t* x
   }
 }
 
+template <int DT>
+__global__ __launch_bounds__(kQThreads) void quant_flat_kernel(const uint16_t* x, int64_t gsize,
+                                                               int64_t nbg, const float* dequant,
+                                                               int per_bh, uint8_t* codes) {
+  quant_flat_body<DT>(blockIdx.x, x, gsize, nbg, dequant, per_bh, codes);
+}
+
 // BHSD output: codes[r*D + d] for global row r = bh*S + s.
 template <int DT>
-__global__ __launch_bounds__(kQThreads) void quant_apply_kernel(QParams p, const float* dequant,
+__device__ __forceinline__ void quant_apply_body(int64_t blk_id, QParams p, const float* dequant,
                                                                 int per_bh, uint8_t* codes) {
-  const int64_t blk = blockIdx.x;
+  const int64_t blk = blk_id;
   const int64_t g = blk / p.nbg;
   const int64_t j = blk - g * p.nbg;
   const int64_t first = j * p.rpb;
@@ -245,6 +267,12 @@ __global__ __launch_bounds__(kQThreads) void quant_apply_kernel(QParams p, const
     cur.advance(step, p);
     r += step;
   }
+}
+
+template <int DT>
+__global__ __launch_bounds__(kQThreads) void quant_apply_kernel(QParams p, const float* dequant,
+                                                                int per_bh, uint8_t* codes) {
+  quant_apply_body<DT>(blockIdx.x, p, dequant, per_bh, codes);
 }
 
 // BHDS output: per head, codes[(bh*D + d)*ld + s]; columns [S, ld) zeroed.
@@ -306,6 +334,53 @@ __global__ __launch_bounds__(kQThreads) void quant_apply_t_kernel(QParams p, con
     const uint4 v = *reinterpret_cast<const uint4*>(&tile[dr * 128 + ch * 16]);
     *reinterpret_cast<uint4*>(codes + (bh * p.D + d0 + dr) * ld + s0 + ch * 16) = v;
   }
+}
+
+// Multi-tensor launches (the Q, K and V of one attention call): blockIdx.y
+// selects the job, blockIdx.x is the block inside it, and blocks past a
+// job's own count return at once.  One launch per pass instead of three.
+struct QJob {
+  QParams p;          // the tensor's plan
+  int flat;           // contiguous: the flat kernels
+  int per_bh;
+  int64_t gsize;      // elements per group (flat)
+  int64_t nblocks;    // ngroups * nbg
+  uint32_t* partial;  // this job's partial maxima
+  float* dequant;     // this job's scales
+  uint8_t* codes;     // BHSD codes (apply jobs)
+};
+struct QJobs3 {
+  QJob j0, j1, j2;
+};
+
+// the job of this block (a select, not a dynamic index into the kernel
+// arguments, which would copy them to scratch)
+__device__ __forceinline__ const QJob& job_of(const QJobs3& jobs) {
+  return blockIdx.y == 0 ? jobs.j0 : blockIdx.y == 1 ? jobs.j1 : jobs.j2;
+}
+
+__global__ __launch_bounds__(kQThreads) void amax_multi_kernel(QJobs3 jobs) {
+  const QJob& jb = job_of(jobs);
+  if ((int64_t)blockIdx.x >= jb.nblocks) return;
+  if (jb.flat) amax_flat_body(blockIdx.x, jb.p.x, jb.gsize, jb.p.nbg, jb.partial);
+  else amax_partial_body(blockIdx.x, jb.p, jb.partial);
+}
+
+template <int DT>
+__global__ __launch_bounds__(kQThreads) void finalize_multi_kernel(QJobs3 jobs) {
+  const QJob& jb = job_of(jobs);
+  if ((int64_t)blockIdx.x >= jb.p.ngroups) return;
+  scale_finalize_body<DT>(blockIdx.x, jb.partial, jb.p.nbg, jb.dequant);
+}
+
+template <int DT>
+__global__ __launch_bounds__(kQThreads) void apply_multi_kernel(QJobs3 jobs) {
+  const QJob& jb = job_of(jobs);
+  if ((int64_t)blockIdx.x >= jb.nblocks) return;
+  if (jb.flat)
+    quant_flat_body<DT>(blockIdx.x, jb.p.x, jb.gsize, jb.p.nbg, jb.dequant, jb.per_bh, jb.codes);
+  else
+    quant_apply_body<DT>(blockIdx.x, jb.p, jb.dequant, jb.per_bh, jb.codes);
 }
 
 __global__ void selftest_e4m3_kernel(const float* x, uint8_t* out, int64_t n) {
@@ -546,6 +621,95 @@ extern "C" int rp_fp8_scale_quantize(const void* x, int x_dtype, int64_t B, int6
   rc = launch_scale(pl, dequant_out, workspace, workspace_bytes, st);
   if (rc) return rc;
   return launch_apply(pl, x, B, H, S, D, sb, sh, ss, dequant_out, codes, layout, ld, st);
+}
+
+static size_t align256(size_t n) { return (n + 255) / 256 * 256; }
+
+extern "C" size_t rp_fp8_quant_qkv_workspace_bytes(int64_t B, int64_t H, int64_t Sq, int64_t Skv,
+                                                   int64_t D, int granularity) {
+  const size_t q = rp_fp8_quant_workspace_bytes(B, H, Sq, D, granularity);
+  const size_t kv = rp_fp8_quant_workspace_bytes(B, H, Skv, D, granularity);
+  if (q == 0 || kv == 0) return 0;
+  return align256(q) + align256(kv) + kv;
+}
+
+extern "C" int rp_fp8_scale_quantize_qkv(const void* q, const void* k, const void* v, int x_dtype,
+                                         int64_t B, int64_t H, int64_t Sq, int64_t Skv, int64_t D,
+                                         int64_t qsb, int64_t qsh, int64_t qss, int64_t ksb,
+                                         int64_t ksh, int64_t kss, int64_t vsb, int64_t vsh,
+                                         int64_t vss, int granularity, float* dequant_out,
+                                         uint8_t* q8, uint8_t* k8, uint8_t* vt8, int64_t ldv,
+                                         void* workspace, size_t workspace_bytes, void* stream) {
+  if (q == nullptr || k == nullptr || v == nullptr || dequant_out == nullptr || q8 == nullptr ||
+      k8 == nullptr || vt8 == nullptr) {
+    rp_set_error("scale_quantize_qkv: null pointer");
+    return RP_ERR_INVALID_ARGUMENT;
+  }
+  Plan pq, pk, pv;
+  int rc = make_plan(q, x_dtype, B, H, Sq, D, qsb, qsh, qss, granularity, &pq);
+  if (rc) return rc;
+  if ((rc = make_plan(k, x_dtype, B, H, Skv, D, ksb, ksh, kss, granularity, &pk))) return rc;
+  if ((rc = make_plan(v, x_dtype, B, H, Skv, D, vsb, vsh, vss, granularity, &pv))) return rc;
+  if (D % 32 != 0 || ldv < Skv || ldv % 128 != 0) {
+    rp_set_error("scale_quantize_qkv: V^T needs D %% 32 == 0 and ldv >= Skv with ldv %% 128 == 0");
+    return RP_ERR_UNSUPPORTED;
+  }
+  if (B * H > 65535) {
+    rp_set_error("scale_quantize_qkv: B*H=%lld exceeds the grid limit", (long long)(B * H));
+    return RP_ERR_UNSUPPORTED;
+  }
+  // partial maxima of the three tensors side by side in the workspace
+  const size_t off_k = align256(pq.ws_bytes), off_v = off_k + align256(pk.ws_bytes);
+  const size_t need = off_v + pv.ws_bytes;
+  if (workspace == nullptr || workspace_bytes < need ||
+      reinterpret_cast<uintptr_t>(workspace) % 256 != 0) {
+    rp_set_error("scale_quantize_qkv: workspace of %zu bytes (256-byte aligned) needed, got %zu",
+                 need, workspace_bytes);
+    return RP_ERR_WORKSPACE;
+  }
+  const int64_t ng = pq.p.ngroups;
+  uint8_t* ws = static_cast<uint8_t*>(workspace);
+  auto job = [&](const Plan& pl, size_t off, float* dq, uint8_t* codes) {
+    QJob jb{};
+    jb.p = pl.p;
+    jb.flat = pl.flat;
+    jb.per_bh = pl.per_bh;
+    jb.gsize = pl.gsize;
+    jb.nblocks = pl.p.ngroups * pl.p.nbg;
+    jb.partial = reinterpret_cast<uint32_t*>(ws + off);
+    jb.dequant = dq;
+    jb.codes = codes;
+    return jb;
+  };
+  QJobs3 jobs;
+  jobs.j0 = job(pq, 0, dequant_out, q8);
+  jobs.j1 = job(pk, off_k, dequant_out + ng, k8);
+  jobs.j2 = job(pv, off_v, dequant_out + 2 * ng, nullptr);
+  const int64_t amax_blocks = max(jobs.j0.nblocks, max(jobs.j1.nblocks, jobs.j2.nblocks));
+  const int64_t apply_blocks = max(jobs.j0.nblocks, jobs.j1.nblocks);
+  if (amax_blocks > 0x7fffffff) {
+    rp_set_error("scale_quantize_qkv: grid too large");
+    return RP_ERR_UNSUPPORTED;
+  }
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  hipLaunchKernelGGL(amax_multi_kernel, dim3((unsigned)amax_blocks, 3), dim3(kQThreads), 0, st,
+                     jobs);
+  if ((rc = check_launch("amax_multi"))) return rc;
+  if (x_dtype == RP_DTYPE_F16) {
+    hipLaunchKernelGGL(finalize_multi_kernel<kInF16>, dim3((unsigned)ng, 3), dim3(kQThreads), 0,
+                       st, jobs);
+    hipLaunchKernelGGL(apply_multi_kernel<kInF16>, dim3((unsigned)apply_blocks, 2),
+                       dim3(kQThreads), 0, st, jobs);
+  } else {
+    hipLaunchKernelGGL(finalize_multi_kernel<kInBf16>, dim3((unsigned)ng, 3), dim3(kQThreads), 0,
+                       st, jobs);
+    hipLaunchKernelGGL(apply_multi_kernel<kInBf16>, dim3((unsigned)apply_blocks, 2),
+                       dim3(kQThreads), 0, st, jobs);
+  }
+  if ((rc = check_launch("apply_multi"))) return rc;
+  // V^T: its own grid shape
+  return launch_apply(pv, v, B, H, Skv, D, vsb, vsh, vss, dequant_out + 2 * ng, vt8,
+                      RP_LAYOUT_BHDS, ldv, st);
 }
 
 extern "C" int rp_selftest_e4m3(const float* x, uint8_t* out, int64_t n, void* stream) {

@@ -20,6 +20,7 @@ Numerics (OCP e4m3fn, FP8_MAX = 448):
 
 from __future__ import annotations
 
+import functools
 import math
 from typing import Callable, Literal
 
@@ -162,6 +163,54 @@ def scale_quantize(x: torch.Tensor, granularity: Granularity = "bh",
     if x.dim() != 4 and layout == "bhsd":
         codes = codes.reshape(x.shape)
     return dq, codes
+
+
+@functools.lru_cache(maxsize=256)
+def _qkv_ws_bytes(B: int, H: int, Sq: int, Skv: int, D: int, g: int) -> int:
+    return int(C.lib().rp_fp8_quant_qkv_workspace_bytes(B, H, Sq, Skv, D, g))
+
+
+def _align(n: int, a: int = 256) -> int:
+    return (n + a - 1) // a * a
+
+
+def scale_quantize_qkv(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                       granularity: Granularity = "bh"
+                       ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor,
+                                  torch.Tensor, torch.Tensor]:
+    """(q_scale, q8, k_scale, k8, v_scale, vt8) of one attention call from one
+    library call (rp_fp8_scale_quantize_qkv: four kernel launches instead of
+    nine) into one device allocation: the same scales and codes as three
+    ``scale_quantize`` calls (V transposed, "bhds"), with a fraction of the
+    host work, which is what bounds small calls.  (B, H, S, D) inputs, bf16 or fp16, any strides with a contiguous
+    head dim; K and V share their shape."""
+    dt = _in_dtype("q", q)
+    for name, t in (("k", k), ("v", v)):
+        if _in_dtype(name, t) != dt:
+            raise TypeError(f"q, k, v dtypes differ ({q.dtype}, {k.dtype}, {v.dtype})")
+    B, H, Sq, D, qsb, qsh, qss = _bhsd_view(q)
+    _, _, Skv, _, ksb, ksh, kss = _bhsd_view(k)
+    _, _, _, _, vsb, vsh, vss = _bhsd_view(v)
+    g = _GRAN[granularity]
+    G = B * H if granularity == "bh" else 1
+    ldv = _round_up(Skv, V_PAD)
+    nq, nk, nv = B * H * Sq * D, B * H * Skv * D, B * H * D * ldv
+    ws = _qkv_ws_bytes(B, H, Sq, Skv, D, g)
+    o_k = _align(nq)
+    o_v = o_k + _align(nk)
+    o_s = o_v + _align(nv)
+    o_w = o_s + _align(3 * G * 4)
+    arena = torch.empty(o_w + max(ws, 16), dtype=torch.uint8, device=q.device)
+    base = arena.data_ptr()
+    C.check(C.lib().rp_fp8_scale_quantize_qkv(
+        q.data_ptr(), k.data_ptr(), v.data_ptr(), dt, B, H, Sq, Skv, D, qsb, qsh, qss,
+        ksb, ksh, kss, vsb, vsh, vss, g, base + o_s, base, base + o_k, base + o_v, ldv,
+        base + o_w, ws, _stream(q)), "rp_fp8_scale_quantize_qkv")
+    dq = arena[o_s:o_s + 3 * G * 4].view(torch.float32)
+    q8 = arena[:nq].view(B, H, Sq, D).view(torch.float8_e4m3fn)
+    k8 = arena[o_k:o_k + nk].view(B, H, Skv, D).view(torch.float8_e4m3fn)
+    vt8 = arena[o_v:o_v + nv].view(B, H, D, ldv).view(torch.float8_e4m3fn)
+    return dq[:G], q8, dq[G:2 * G], k8, dq[2 * G:], vt8
 
 
 _ROPE = {None: C.RP_ROPE_NONE, "half": C.RP_ROPE_HALF, "interleaved": C.RP_ROPE_INTERLEAVED}
@@ -347,9 +396,7 @@ def fp8_flash_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *,
         raise ValueError(f"head_dim {D} not in compiled tile shapes {sorted(SUPPORTED_HEAD_DIMS)}")
     if scale is None:
         scale = 1.0 / math.sqrt(D)
-    qs, q8 = scale_quantize(q, granularity, "bhsd")
-    ks, k8 = scale_quantize(k, granularity, "bhsd")
-    vs, vt8 = scale_quantize(v, granularity, "bhds")
+    qs, q8, ks, k8, vs, vt8 = scale_quantize_qkv(q, k, v, granularity)
 
     def run(splits: int) -> torch.Tensor:
         return attention_fp8(q8.view(torch.uint8), k8.view(torch.uint8), vt8.view(torch.uint8),

@@ -50,16 +50,31 @@ def cache_path() -> Path:
     return Path(override) if override else _DEFAULT_CACHE_PATH
 
 
+#: (path, mtime_ns, size) -> parsed cache; the file is re-read only when it
+#: changes, so a winner another process records is still picked up on the
+#: next call (the reference re-reads the file every call,
+#: fp8_flash_attn.py:459-468) without a JSON parse per attention call.
+_memo: tuple[tuple[str, int, int], dict] | None = None
+
+
 def cache_load() -> dict:
+    global _memo
     path = cache_path()
-    if not path.exists():
+    try:
+        st = path.stat()
+    except OSError:
         return {}
+    stamp = (str(path), st.st_mtime_ns, st.st_size)
+    if _memo is not None and _memo[0] == stamp:
+        return dict(_memo[1])
     try:
         with path.open("r") as fh:
             data = json.load(fh)
     except (OSError, ValueError):
         return {}
-    return data if isinstance(data, dict) else {}
+    data = data if isinstance(data, dict) else {}
+    _memo = (stamp, data)
+    return dict(data)
 
 
 def cache_save(cache: dict) -> None:

@@ -183,3 +183,16 @@ def test_multi_block_launch_plan() -> None:
     assert plan(1, 40, 75600, 4096, 128, 0, 1) > 1           # 32 tiles: still pays
     assert plan(1, 40, 75600, 4097, 128, 0, 1) == 1          # 33 tiles: off
     assert plan(0, 40, 75600, 512, 128, 0, 1) == 0           # invalid
+
+
+def test_qkv_quantizer_argument_checks() -> None:
+    L = _capi.lib()
+    args = [FAKE, FAKE, FAKE, _capi.RP_DTYPE_BF16, 1, 2, 64, 128, 64,
+            2 * 64 * 64, 64 * 64, 64, 2 * 128 * 64, 128 * 64, 64, 2 * 128 * 64, 128 * 64, 64,
+            0, FAKE, FAKE, FAKE, FAKE, 128, FAKE, 1 << 20, None]
+    bad = list(args); bad[1] = None
+    assert L.rp_fp8_scale_quantize_qkv(*bad) == 1 and "null" in L.rp_last_error().decode()
+    bad = list(args); bad[3] = 7
+    assert L.rp_fp8_scale_quantize_qkv(*bad) == 1 and "dtype" in L.rp_last_error().decode()
+    bad = list(args); bad[23] = 100                      # ldv < Skv
+    assert L.rp_fp8_scale_quantize_qkv(*bad) == 2 and "ldv" in L.rp_last_error().decode()

@@ -1,0 +1,37 @@
+"""The FP8 attention path under HIP graph capture (torch.cuda.graph): small
+calls are bound by host launch work, which a captured graph removes.  Every
+replay, with new inputs copied into the captured buffers and eager work and
+synchronisations between replays, equals an eager call bit for bit."""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from repercep_runtime_amd import ops
+from repercep_runtime_amd.workloads import C1, C5, attn_inputs
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("cfg", [C1, C5], ids=["c1", "c5_shared_prefix"])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_captured_attention_replays_match_eager(gpu: torch.device, cfg, dtype) -> None:
+    kw = dict(prefix_len=cfg.prefix, suffix_len=cfg.suffix) if cfg.prefix else {}
+    q, k, v = (t.to(dtype) for t in attn_inputs(cfg, device=gpu))
+    sq, sk, sv = q.clone(), k.clone(), v.clone()          # the captured inputs
+    ops.fp8_flash_attention(sq, sk, sv, kv_splits=1, **kw)   # warm up outside capture
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        sout = ops.fp8_flash_attention(sq, sk, sv, kv_splits=1, **kw)
+    g = torch.Generator(device=gpu).manual_seed(7)
+    for rep in range(4):
+        if rep:   # new inputs for every later replay
+            for src in (sq, sk, sv):
+                src.copy_(torch.randn(src.shape, generator=g, device=gpu).to(dtype))
+        graph.replay()
+        torch.cuda.synchronize()
+        want = ops.fp8_flash_attention(sq.clone(), sk.clone(), sv.clone(), kv_splits=1, **kw)
+        _ = torch.randn(1024, device=gpu).sum().item()      # unrelated eager work + sync
+        assert torch.equal(sout, want), f"replay {rep} differs from eager"

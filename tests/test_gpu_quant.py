@@ -268,3 +268,22 @@ def test_fp16_zero_scale_group_matches_torch_on_the_gpu(gpu: torch.device) -> No
     ref_c = quant.quantize(xg, ref_dq).view(torch.uint8).cpu().numpy()
     _assert_scales_equal(dq.cpu().numpy(), ref_dq.cpu().numpy())
     _assert_codes_equal(codes_np(codes), ref_c)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("granularity", ["bh", "tensor"])
+def test_scale_quantize_qkv_equals_three_calls(gpu: torch.device, dtype: torch.dtype,
+                                               granularity: str) -> None:
+    """One library call for Q, K and V (rp_fp8_scale_quantize_qkv) gives the
+    same scales and codes as three rp_fp8_scale_quantize calls; K/V longer
+    than Q, and strided (permuted BSHD) inputs."""
+    g = torch.Generator().manual_seed(31)
+    q = torch.randn(2, 300, 3, 128, generator=g).mul(2).to(dtype).to(gpu).permute(0, 2, 1, 3)
+    k = torch.randn(2, 3, 700, 128, generator=g).to(dtype).to(gpu)
+    v = torch.randn(2, 700, 3, 128, generator=g).mul(0.5).to(dtype).to(gpu).permute(0, 2, 1, 3)
+    qs, q8, ks, k8, vs, vt8 = ops.scale_quantize_qkv(q, k, v, granularity)
+    for (s, c), x, lay in (((qs, q8), q, "bhsd"), ((ks, k8), k, "bhsd"), ((vs, vt8), v, "bhds")):
+        s2, c2 = ops.scale_quantize(x, granularity, lay)
+        _assert_scales_equal(s.cpu().numpy(), s2.cpu().numpy())
+        assert c.shape == c2.shape
+        assert torch.equal(c.view(torch.uint8), c2.view(torch.uint8))

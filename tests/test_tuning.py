@@ -149,3 +149,21 @@ def test_split_entry_point_checks_and_sizing() -> None:
     assert _split_call(L, 8, 1 << 20, n8 - 1) == 1                # one byte short
     assert _split_call(L, 8, (1 << 20) + 64, n8) == 1             # misaligned
     assert "256-byte" in L.rp_last_error().decode()
+
+
+def test_cache_is_reread_when_the_file_changes(cache_file: Path) -> None:
+    """The parsed cache is kept between calls, but a file another process
+    rewrites is picked up on the next lookup (as the reference's per-call
+    read would)."""
+    import os
+
+    legacy = dict(tuning.FALLBACK_CONFIG)
+    tuning.record_config(1, 8, 8192, 8192, 128, False, legacy)
+    assert ops.tuned_kv_splits(1, 8, 8192, 8192, 128) == 1
+    key = tuning.cache_key(1, 8, 8192, 8192, 128, False)
+    cache_file.write_text(json.dumps({key: {**legacy, "KV_SPLITS": 4}}))
+    st = cache_file.stat()
+    os.utime(cache_file, ns=(st.st_atime_ns, st.st_mtime_ns + 1_000_000))
+    assert ops.tuned_kv_splits(1, 8, 8192, 8192, 128) == 4
+    cache_file.unlink()
+    assert ops.tuned_kv_splits(1, 8, 8192, 8192, 128) == 1        # gone: a miss
