@@ -223,6 +223,17 @@ int rp_fp8_gemm(const uint8_t* a8, const uint8_t* bt8, void* c,
                 float a_scale, float b_scale, const float* a_scale_dev,
                 const float* b_scale_dev, void* stream);
 
+/* rp_fp8_gemm with a bias: C = bf16(fp32(fp32(A8 . B8) * a_scale * b_scale)
+ * + bias[n]), bias bf16 [N] (8-byte aligned), the product and the sum each
+ * rounded to fp32 -- the epilogue of a bf16 nn.Linear.  A NULL bias makes
+ * it rp_fp8_gemm.  No counterpart in the reference GEMM
+ * (kernels/hip/fp8_attn/fp8_gemm.hip has no bias); it serves the FP8 linear
+ * layers that replace nn.Linear in the module-swap pattern of
+ * src/repercep/runtime/quantize.py:135-179. */
+int rp_fp8_linear(const uint8_t* a8, const uint8_t* bt8, const void* bias, void* c, int64_t M,
+                  int64_t N, int64_t K, int64_t lda, int64_t ldb, int64_t ldc, float a_scale,
+                  float b_scale, const float* a_scale_dev, const float* b_scale_dev, void* stream);
+
 /* FP8 byte transpose: dst (C, R) <- src (R, C); row strides lds, ldd.
  * Turns the reference GEMM's row-major B (K, N) into the (N, K) operand. */
 int rp_fp8_transpose(const uint8_t* src, uint8_t* dst, int64_t R, int64_t C,

@@ -40,7 +40,7 @@ EXPORTS = (
     "rp_fp8_attn_workspace_bytes",
     "rp_fp8_attn_blocks_per_workgroup",
     "rp_fp8_attn_fwd_split", "rp_fp8_rmsnorm_quant_workspace_bytes",
-    "rp_fp8_rmsnorm_scale_quantize", "rp_fp8_gemm", "rp_fp8_transpose",
+    "rp_fp8_rmsnorm_scale_quantize", "rp_fp8_gemm", "rp_fp8_linear", "rp_fp8_transpose",
     "rp_selftest_e4m3", "rp_selftest_scale",
 )
 
@@ -102,6 +102,9 @@ def _declare(L: ctypes.CDLL) -> None:
     L.rp_fp8_gemm.restype = _int
     L.rp_fp8_gemm.argtypes = [_vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _f32, _f32,
                               _vp, _vp, _vp]
+    L.rp_fp8_linear.restype = _int
+    L.rp_fp8_linear.argtypes = [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _f32,
+                                _f32, _vp, _vp, _vp]
     L.rp_fp8_transpose.restype = _int
     L.rp_fp8_transpose.argtypes = [_vp, _vp, _i64, _i64, _i64, _i64, _vp]
     L.rp_selftest_e4m3.restype = _int

@@ -35,12 +35,35 @@ struct GemmArgs {
   const uint8_t* a;
   const uint8_t* bt;
   uint16_t* c;
+  const uint16_t* bias;   // bf16 [N] added in the epilogue, or null
   int64_t M, N, K, lda, ldb, ldc;
   float a_scale, b_scale;
   const float* a_dev;
   const float* b_dev;
   int tiles_m, tiles_n;
 };
+
+// Bias values of the 4 columns n..n+3 (bf16 pairs), or zeros past N.  Every
+// thread loads its columns before the first output store: the bias and C are
+// both bf16 pointers, so a load after a store would have to wait for it.
+__device__ __forceinline__ uint2 bias4(const GemmArgs& g, int64_t n) {
+  return n < g.N ? *reinterpret_cast<const uint2*>(g.bias + n) : make_uint2(0u, 0u);
+}
+
+// Epilogue value: t = fp32(acc * scale), then fp32(t + bias[n]) when there
+// is a bias -- two roundings (the empty asm keeps the compiler from fusing
+// them into one FMA), the fp32 result a bf16 nn.Linear rounds once.
+__device__ __forceinline__ void epi4(bool has_bias, uint2 bb, float scale, float v0, float v1,
+                                     float v2, float v3, float (&o)[4]) {
+  o[0] = v0 * scale; o[1] = v1 * scale; o[2] = v2 * scale; o[3] = v3 * scale;
+  if (has_bias) {
+    asm("" : "+v"(o[0]), "+v"(o[1]), "+v"(o[2]), "+v"(o[3]));
+    o[0] += bf16_to_f32(bb.x & 0xffffu);
+    o[1] += bf16_to_f32(bb.x >> 16);
+    o[2] += bf16_to_f32(bb.y & 0xffffu);
+    o[3] += bf16_to_f32(bb.y >> 16);
+  }
+}
 
 __device__ __forceinline__ f32x4 mfma_16x16x128(const i32x8& a, const i32x8& b, const f32x4& c) {
   return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, 0, 0, 0);
@@ -175,6 +198,11 @@ void gemm_kernel(GemmArgs g) {
   }
 
   const float scale = (g.a_dev ? *g.a_dev : g.a_scale) * (g.b_dev ? *g.b_dev : g.b_scale);
+  const bool has_bias = g.bias != nullptr;
+  uint2 bb[G::TN];
+#pragma unroll
+  for (int j = 0; j < G::TN; ++j)
+    bb[j] = has_bias ? bias4(g, n0 + wn * G::WN + 16 * j + 4 * lg) : make_uint2(0u, 0u);
 #pragma unroll
   for (int i = 0; i < G::TM; ++i) {
     const int64_t m = m0 + wm * G::WM + 16 * i + li;
@@ -184,9 +212,11 @@ void gemm_kernel(GemmArgs g) {
       const int64_t n = n0 + wn * G::WN + 16 * j + 4 * lg;
       if (n >= g.N) continue;
       const f32x4 v = acc[j][i];
+      float o[4];
+      epi4(has_bias, bb[j], scale, v[0], v[1], v[2], v[3], o);
       uint2 pk;
-      pk.x = f32_to_bf16_bits(v[0] * scale) | (f32_to_bf16_bits(v[1] * scale) << 16);
-      pk.y = f32_to_bf16_bits(v[2] * scale) | (f32_to_bf16_bits(v[3] * scale) << 16);
+      pk.x = f32_to_bf16_bits(o[0]) | (f32_to_bf16_bits(o[1]) << 16);
+      pk.y = f32_to_bf16_bits(o[2]) | (f32_to_bf16_bits(o[3]) << 16);
       *reinterpret_cast<uint2*>(g.c + m * g.ldc + n) = pk;
     }
   }
@@ -413,6 +443,14 @@ void gemm256_kernel(GemmArgs g) {
 
   // epilogue: C[m][n] = bf16(acc * a_scale * b_scale)
   const float scale = (g.a_dev ? *g.a_dev : g.a_scale) * (g.b_dev ? *g.b_dev : g.b_scale);
+  const bool has_bias = g.bias != nullptr;
+  uint2 bb[4][4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      bb[j][q] = has_bias ? bias4(g, n0 + wn * 128 + 32 * j + 8 * q + 4 * lg)
+                          : make_uint2(0u, 0u);
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int64_t m = m0 + wm * 128 + 32 * i + lq;
@@ -424,9 +462,12 @@ void gemm256_kernel(GemmArgs g) {
         const int64_t n = n0 + wn * 128 + 32 * j + 8 * q + 4 * lg;
         if (n >= g.N) continue;
         const f32x16& v = acc[i][j];
+        float o[4];
+        epi4(has_bias, bb[j][q], scale, v[4 * q + 0], v[4 * q + 1], v[4 * q + 2],
+             v[4 * q + 3], o);
         uint2 pk;
-        pk.x = g2_pack_bf16(v[4 * q + 0] * scale, v[4 * q + 1] * scale);
-        pk.y = g2_pack_bf16(v[4 * q + 2] * scale, v[4 * q + 3] * scale);
+        pk.x = g2_pack_bf16(o[0], o[1]);
+        pk.y = g2_pack_bf16(o[2], o[3]);
         *reinterpret_cast<uint2*>(g.c + m * g.ldc + n) = pk;
       }
   }
@@ -489,10 +530,10 @@ int launch_gemm(GemmArgs g, hipStream_t st) {
 
 using namespace rp;
 
-extern "C" int rp_fp8_gemm(const uint8_t* a8, const uint8_t* bt8, void* c, int64_t M, int64_t N,
-                           int64_t K, int64_t lda, int64_t ldb, int64_t ldc, float a_scale,
-                           float b_scale, const float* a_scale_dev, const float* b_scale_dev,
-                           void* stream) {
+static int gemm_run(const uint8_t* a8, const uint8_t* bt8, const void* bias, void* c, int64_t M,
+                    int64_t N, int64_t K, int64_t lda, int64_t ldb, int64_t ldc, float a_scale,
+                    float b_scale, const float* a_scale_dev, const float* b_scale_dev,
+                    void* stream) {
   if (!a8 || !bt8 || !c) {
     rp_set_error("gemm: null pointer");
     return RP_ERR_INVALID_ARGUMENT;
@@ -512,8 +553,13 @@ extern "C" int rp_fp8_gemm(const uint8_t* a8, const uint8_t* bt8, void* c, int64
     rp_set_error("gemm: operands must be 16-byte aligned and C 8-byte aligned");
     return RP_ERR_UNSUPPORTED;
   }
+  if (bias != nullptr && reinterpret_cast<uintptr_t>(bias) % 8 != 0) {
+    rp_set_error("gemm: bias must be 8-byte aligned");
+    return RP_ERR_UNSUPPORTED;
+  }
   GemmArgs g{};
   g.a = a8; g.bt = bt8; g.c = static_cast<uint16_t*>(c);
+  g.bias = static_cast<const uint16_t*>(bias);
   g.M = M; g.N = N; g.K = K; g.lda = lda; g.ldb = ldb; g.ldc = ldc;
   g.a_scale = a_scale; g.b_scale = b_scale; g.a_dev = a_scale_dev; g.b_dev = b_scale_dev;
   // the large-tile kernel reads whole 64-byte K sub-slices and keeps tile
@@ -522,6 +568,22 @@ extern "C" int rp_fp8_gemm(const uint8_t* a8, const uint8_t* bt8, void* c, int64
       ldb * (int64_t)kG2Tile < (int64_t)1 << 32)
     return launch_gemm256(g, static_cast<hipStream_t>(stream));
   return launch_gemm<256, 128>(g, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int rp_fp8_gemm(const uint8_t* a8, const uint8_t* bt8, void* c, int64_t M, int64_t N,
+                           int64_t K, int64_t lda, int64_t ldb, int64_t ldc, float a_scale,
+                           float b_scale, const float* a_scale_dev, const float* b_scale_dev,
+                           void* stream) {
+  return gemm_run(a8, bt8, nullptr, c, M, N, K, lda, ldb, ldc, a_scale, b_scale, a_scale_dev,
+                  b_scale_dev, stream);
+}
+
+extern "C" int rp_fp8_linear(const uint8_t* a8, const uint8_t* bt8, const void* bias, void* c,
+                             int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldb,
+                             int64_t ldc, float a_scale, float b_scale, const float* a_scale_dev,
+                             const float* b_scale_dev, void* stream) {
+  return gemm_run(a8, bt8, bias, c, M, N, K, lda, ldb, ldc, a_scale, b_scale, a_scale_dev,
+                  b_scale_dev, stream);
 }
 
 extern "C" int rp_fp8_transpose(const uint8_t* src, uint8_t* dst, int64_t R, int64_t C,

@@ -12,8 +12,9 @@ weight as OCP e4m3fn codes with one per-tensor scale and runs the FP8 GEMM:
              e4m3fn(W / sw) -- K-contiguous rows, the GEMM's B^T operand as is
     forward  x (..., K) bf16 -> per-call per-tensor scale sa and codes (the
              attention quantizer's arithmetic), then
-             y = bf16(fp32(x8 . W8^T) * sa * sw)   [rp_fp8_gemm]
-             y = y + bias                           [bf16, when present]
+             y = bf16(fp32(x8 . W8^T) * sa * sw + bias)   [rp_fp8_linear: the
+             product and the bias sum each rounded to fp32, as a bf16
+             nn.Linear's fp32 epilogue; rp_fp8_gemm without a bias]
 
 Same members as the reference's module: ``qweight``, ``scale`` (buffers, so
 ``.to()`` and state dicts work), ``bias`` (a Parameter or None),
@@ -88,9 +89,8 @@ class FP8Linear(torch.nn.Module):
         if not x2.is_contiguous():
             x2 = x2.contiguous()
         sa, a8 = ops.scale_quantize(x2, "tensor", "bhsd")
-        y = ops.fp8_gemm(a8.view(torch.uint8), self.qweight, sa, self.scale, b_transposed=True)
-        if self.bias is not None:
-            y = y + self.bias
+        y = ops.fp8_gemm(a8.view(torch.uint8), self.qweight, sa, self.scale, b_transposed=True,
+                         bias=self.bias)
         return y.reshape(*lead, self.out_features)
 
     def extra_repr(self) -> str:

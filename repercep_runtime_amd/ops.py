@@ -467,7 +467,7 @@ def transpose_fp8(x8: torch.Tensor) -> torch.Tensor:
 
 def fp8_gemm(a8: torch.Tensor, b8: torch.Tensor, a_scale: float | torch.Tensor,
              b_scale: float | torch.Tensor, *, b_transposed: bool = False,
-             out: torch.Tensor | None = None) -> torch.Tensor:
+             out: torch.Tensor | None = None, bias: torch.Tensor | None = None) -> torch.Tensor:
     """C (M, N) bf16 = bf16(fp32(A8 . B8) * a_scale * b_scale).
 
     Same contract as the reference's ``fp8_gemm(A, B, a_scale, b_scale)``
@@ -475,7 +475,9 @@ def fp8_gemm(a8: torch.Tensor, b8: torch.Tensor, a_scale: float | torch.Tensor,
     (M, K) row-major, B8 is (K, N) row-major -- or, with ``b_transposed``,
     already (N, K) (the K-contiguous operand the kernel reads; the reference
     layout costs one extra transpose pass).  Scales may be Python floats or
-    one-element device tensors (read on the device, no host sync).
+    one-element device tensors (read on the device, no host sync).  ``bias``
+    (bf16 [N]) is added to the fp32 product before the bf16 rounding
+    (``rp_fp8_linear``, an nn.Linear epilogue; the reference GEMM has none).
     """
     _check_cuda("a8", a8)
     _check_cuda("b8", b8)
@@ -495,12 +497,22 @@ def fp8_gemm(a8: torch.Tensor, b8: torch.Tensor, a_scale: float | torch.Tensor,
         out = torch.empty((M, N), dtype=torch.bfloat16, device=a8.device)
     a_dev = a_scale.to(torch.float32).contiguous() if isinstance(a_scale, torch.Tensor) else None
     b_dev = b_scale.to(torch.float32).contiguous() if isinstance(b_scale, torch.Tensor) else None
-    C.check(C.lib().rp_fp8_gemm(
-        a8.data_ptr(), bt.data_ptr(), out.data_ptr(), M, N, K, a8.stride(0), bt.stride(0),
-        out.stride(0), 0.0 if a_dev is not None else float(a_scale),
-        0.0 if b_dev is not None else float(b_scale),
-        a_dev.data_ptr() if a_dev is not None else None,
-        b_dev.data_ptr() if b_dev is not None else None, _stream(a8)), "rp_fp8_gemm")
+    args = (M, N, K, a8.stride(0), bt.stride(0), out.stride(0),
+            0.0 if a_dev is not None else float(a_scale),
+            0.0 if b_dev is not None else float(b_scale),
+            a_dev.data_ptr() if a_dev is not None else None,
+            b_dev.data_ptr() if b_dev is not None else None, _stream(a8))
+    if bias is None:
+        C.check(C.lib().rp_fp8_gemm(a8.data_ptr(), bt.data_ptr(), out.data_ptr(), *args),
+                "rp_fp8_gemm")
+    else:
+        _check_bf16("bias", bias)
+        if bias.shape != (N,) or not bias.is_contiguous():
+            raise ValueError(f"bias must be a contiguous ({N},) tensor, got {tuple(bias.shape)}")
+        if bias.data_ptr() % 8 != 0:          # the epilogue reads 4 bias values at a time
+            bias = bias.clone()
+        C.check(C.lib().rp_fp8_linear(a8.data_ptr(), bt.data_ptr(), bias.data_ptr(),
+                                      out.data_ptr(), *args), "rp_fp8_linear")
     return out
 
 

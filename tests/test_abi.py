@@ -114,6 +114,19 @@ def test_gemm_argument_checks(args: tuple, status: int, msg: str) -> None:
     assert msg in L.rp_last_error().decode()
 
 
+def test_linear_argument_checks() -> None:
+    """rp_fp8_linear runs the GEMM's checks, then needs an 8-byte aligned bias
+    (the epilogue reads four bf16 values at once); a null bias is rp_fp8_gemm."""
+    L = _capi.lib()
+    ok = (FAKE, FAKE, FAKE, FAKE, 64, 64, 64, 64, 64, 64, 1.0, 1.0, None, None, None)
+    bad = list(ok); bad[2] = FAKE + 2
+    assert L.rp_fp8_linear(*bad) == 2 and "bias" in L.rp_last_error().decode()
+    bad = list(ok); bad[0] = None
+    assert L.rp_fp8_linear(*bad) == 1 and "null" in L.rp_last_error().decode()
+    bad = list(ok); bad[5] = 6
+    assert L.rp_fp8_linear(*bad) == 2 and "multiples" in L.rp_last_error().decode()
+
+
 def test_quantizer_argument_checks() -> None:
     L = _capi.lib()
     bf16, f16 = _capi.RP_DTYPE_BF16, _capi.RP_DTYPE_F16

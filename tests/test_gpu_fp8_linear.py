@@ -41,17 +41,16 @@ def test_fp8_linear_matches_oracle(gpu: torch.device, shape: tuple[int, ...], bi
     sa, a8 = quant.quantize_codes(x2.reshape(1, 1, -1, K), "tensor")
     a8 = a8.reshape(-1, K)
     y2 = y.reshape(-1, N)
-    if bias:   # undo the bf16 bias add exactly where it is exact: compare y - bias loosely,
-        # and check the add itself against torch on the GEMM's own output
-        gemm = ops.fp8_gemm(torch.from_numpy(a8).to(gpu), m.qweight, float(sa[0]),
-                            float(sw[0]), b_transposed=True)
-        assert torch.equal(y2, gemm + m.bias)
-        y2 = gemm
     got = bf16_to_f32(bf16_bits(y2))
     bt8 = np.ascontiguousarray(w8.reshape(N, K))
-    ref = native.gemm_rows(a8, bt8, float(sa[0]), float(sw[0]), np.arange(a8.shape[0]))
-    _assert_one_rounding_apart(got, bf16_to_f32(ref), a8, bt8,
-                               float(np.float32(sa[0]) * np.float32(sw[0])))
+    scale = float(np.float32(sa[0]) * np.float32(sw[0]))
+    if not bias:
+        ref = native.gemm_rows(a8, bt8, float(sa[0]), float(sw[0]), np.arange(a8.shape[0]))
+        _assert_one_rounding_apart(got, bf16_to_f32(ref), a8, bt8, scale)
+    else:
+        # rp_fp8_linear: bf16(fp32(fp32(acc * s) + bias)), one bf16 rounding
+        bvec = m.bias.float().cpu().numpy().astype(np.float64)
+        _assert_one_rounding_apart(got, None, a8, bt8, scale, bvec)
     # against the bf16 layer: FP8 noise only
     ref = lin(x.to(gpu)).float()
     rel = (y.float() - ref).abs().mean() / ref.abs().mean()

@@ -31,19 +31,26 @@ def _bf16_rne(x: np.ndarray) -> np.ndarray:
                                   .numpy().view(np.uint16))).astype(np.float64)
 
 
-def _assert_one_rounding_apart(got: np.ndarray, ref: np.ndarray, a8: np.ndarray,
-                               bt8: np.ndarray, scale: float) -> None:
+def _assert_one_rounding_apart(got: np.ndarray, ref: np.ndarray | None, a8: np.ndarray,
+                               bt8: np.ndarray, scale: float,
+                               bias: np.ndarray | None = None) -> None:
     """Every kernel output is the bf16 rounding of some value within eps of the exact
     scaled dot product, eps = 2^-14 * sum |a||b| * scale.  The f8f6f4 MFMA's dot
     product is not an exactly rounded fp32 sum (measured: up to 2^-15.5 of
     sum |a||b| away from it, identically for the 16x16x128 and 32x32x64 forms),
-    so a result may round to the bf16 neighbour of the oracle's.  Also reports
-    BASELINE's error metrics against the oracle (exact sum rounded once)."""
-    st = err_stats(got, ref)
+    so a result may round to the bf16 neighbour of the oracle's.  With a
+    ``bias`` (float64 [N]) the value is exact * scale + bias, and eps widens by
+    the two fp32 roundings of the epilogue (product, then sum).  Also reports
+    BASELINE's error metrics against ``ref``, the oracle (exact sum rounded
+    once); ``ref=None`` takes that rounding of the float64 sum here."""
     A = DECODE[a8].astype(np.float64)
     Bt = DECODE[bt8].astype(np.float64)
     exact = (A @ Bt.T) * float(np.float32(scale))
     eps = 2.0 ** -14 * (np.abs(A) @ np.abs(Bt).T) * abs(scale)
+    if bias is not None:
+        eps = eps + 2.0 ** -23 * (2 * np.abs(exact) + np.abs(bias))
+        exact = exact + bias
+    st = err_stats(got, _bf16_rne(exact) if ref is None else ref)
     lo = _bf16_rne(exact - eps)
     hi = _bf16_rne(exact + eps)
     g = got.astype(np.float64)
@@ -88,6 +95,49 @@ def test_random_vs_oracle(gpu: torch.device, mnk: tuple[int, int, int]) -> None:
     got2 = ops.fp8_gemm(a8.to(gpu), bt8.to(gpu).t().contiguous(),
                         torch.tensor([sa], device=gpu), torch.tensor([sb], device=gpu))
     assert torch.equal(got2, got)
+
+
+@pytest.mark.parametrize("mnk", [(64, 64, 256), (300, 200, 512), (5, 4, 16)])
+def test_bias_epilogue_small_integers_exact(gpu: torch.device, mnk: tuple[int, int, int]) -> None:
+    """rp_fp8_linear on integer operands (exact fp32 sums) with scale fp32(1/3):
+    the output is bf16(fp32(fp32(acc * s) + bias)) bit for bit, which differs
+    from rounding the product to bf16 before the bias is added."""
+    M, N, K = mnk
+    g = torch.Generator().manual_seed(M * N + K)
+    a_i = torch.randint(-2, 3, (M, K), generator=g, dtype=torch.float32)
+    b_i = torch.randint(-2, 3, (K, N), generator=g, dtype=torch.float32)
+    bias = torch.randn(N, generator=g).mul(20).to(torch.bfloat16)
+    s = np.float32(1.0 / 3.0)
+    t = (a_i @ b_i) * torch.tensor(s)
+    ref = (t + bias.float()).to(torch.bfloat16)
+    got = ops.fp8_gemm(a_i.to(gpu).to(torch.float8_e4m3fn), b_i.to(gpu).to(torch.float8_e4m3fn),
+                       float(s), 1.0, bias=bias.to(gpu)).cpu()
+    assert torch.equal(got, ref), f"max abs diff {(got.float() - ref.float()).abs().max().item()}"
+    if M * N >= 4096:
+        twice = (t.to(torch.bfloat16).float() + bias.float()).to(torch.bfloat16)
+        assert not torch.equal(twice, ref), "case does not tell one rounding from two"
+
+
+@pytest.mark.parametrize("mnk", [(257, 520, 384), (1000, 64, 512), (600, 520, 192),
+                                 (513, 260, 48)])
+def test_bias_epilogue_vs_oracle(gpu: torch.device, mnk: tuple[int, int, int]) -> None:
+    """Both GEMM kernels (256x256 tiles when K % 64 == 0, the 256x128 fallback
+    otherwise) with a bias: every output within one rounding of
+    exact * scale + bias, and with a zero bias bit-identical to rp_fp8_gemm."""
+    M, N, K = mnk
+    g = torch.Generator().manual_seed(3 * M + N + K)
+    a8 = torch.randn(M, K, generator=g).mul(30).to(torch.float8_e4m3fn)
+    bt8 = torch.randn(N, K, generator=g).mul(30).to(torch.float8_e4m3fn)
+    bias = torch.randn(N, generator=g).mul(50).to(torch.bfloat16)
+    sa, sb = 0.013, 0.0071
+    got = ops.fp8_gemm(a8.to(gpu), bt8.to(gpu), sa, sb, b_transposed=True, bias=bias.to(gpu))
+    bias64 = bias.float().numpy().astype(np.float64)
+    _assert_one_rounding_apart(bf16_to_f32(bf16_bits(got)), None, codes_np(a8), codes_np(bt8),
+                               sa * sb, bias64)
+    plain = ops.fp8_gemm(a8.to(gpu), bt8.to(gpu), sa, sb, b_transposed=True)
+    zero = ops.fp8_gemm(a8.to(gpu), bt8.to(gpu), sa, sb, b_transposed=True,
+                        bias=torch.zeros(N, dtype=torch.bfloat16, device=gpu))
+    assert torch.equal(zero, plain)
 
 
 def test_wan_ffn_gemm_full_shape_sampled_rows(gpu: torch.device) -> None:
