@@ -104,7 +104,7 @@ def test_quantize_bhsd_bit_exact(gpu: torch.device, shape: tuple[int, ...],
 
 
 @pytest.mark.parametrize("shape", [(1, 8, 1024, 64), (2, 3, 257, 128), (1, 2, 1, 128),
-                                   (1, 1, 300, 256)])
+                                   (1, 1, 300, 256), (1, 3, 200, 32), (2, 2, 130, 96)])
 def test_quantize_bhds_transposed_bit_exact(gpu: torch.device, shape: tuple[int, ...]) -> None:
     g = torch.Generator().manual_seed(7 + sum(shape))
     x = torch.randn(shape, generator=g).to(torch.bfloat16)
