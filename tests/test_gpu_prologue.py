@@ -41,6 +41,10 @@ CASES = [
     ("rope_interleaved", (2, 2, 300, 64), 1.0, False, "interleaved", "bh"),
     ("per_tensor", (2, 3, 400, 128), 0.01, True, "half", "tensor"),
     ("tiny_rows", (1, 1, 5, 64), 1.0, True, "half", "bh"),
+    # rows of one block step across many heads (S below the 32/16-row step)
+    ("per_tensor_short_heads", (2, 5, 3, 64), 1.0, False, "interleaved", "tensor"),
+    ("short_heads_d128", (1, 7, 2, 128), 1.0, True, "half", "bh"),
+    ("per_tensor_ragged", (3, 3, 37, 128), 1.0, True, None, "tensor"),
 ]
 
 
