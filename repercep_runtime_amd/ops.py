@@ -191,6 +191,11 @@ def scale_quantize_qkv(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     B, H, Sq, D, qsb, qsh, qss = _bhsd_view(q)
     _, _, Skv, _, ksb, ksh, kss = _bhsd_view(k)
     _, _, _, _, vsb, vsh, vss = _bhsd_view(v)
+    if k.shape[:2] != q.shape[:2] or k.shape[3] != D or v.shape != k.shape:
+        raise ValueError(f"k and v must share one (B, H, Skv, D) shape with q's B, H and D "
+                         f"(q {tuple(q.shape)}, k {tuple(k.shape)}, v {tuple(v.shape)})")
+    if k.device != q.device or v.device != q.device:
+        raise ValueError("q, k and v must be on one device")
     g = _GRAN[granularity]
     G = B * H if granularity == "bh" else 1
     ldv = _round_up(Skv, V_PAD)
@@ -495,6 +500,11 @@ def fp8_gemm(a8: torch.Tensor, b8: torch.Tensor, a_scale: float | torch.Tensor,
         raise ValueError(f"K mismatch: A {tuple(a8.shape)}, B {tuple(b8.shape)}")
     if out is None:
         out = torch.empty((M, N), dtype=torch.bfloat16, device=a8.device)
+    else:
+        _check_bf16("out", out)
+        if out.shape != (M, N) or out.stride(1) != 1:
+            raise ValueError(f"out must be a ({M}, {N}) bf16 tensor with unit column stride, "
+                             f"got {tuple(out.shape)} strides {out.stride()}")
     a_dev = a_scale.to(torch.float32).contiguous() if isinstance(a_scale, torch.Tensor) else None
     b_dev = b_scale.to(torch.float32).contiguous() if isinstance(b_scale, torch.Tensor) else None
     args = (M, N, K, a8.stride(0), bt.stride(0), out.stride(0),

@@ -163,3 +163,17 @@ def test_wan_ffn_gemm_full_shape_sampled_rows(gpu: torch.device) -> None:
                                sa_h * float(sw.item()))
     del a, w, a8, wt8, c
     torch.cuda.empty_cache()
+
+
+def test_out_argument_is_checked(gpu: torch.device) -> None:
+    a = torch.zeros(64, 32, device=gpu).to(torch.float8_e4m3fn)
+    bt = torch.zeros(16, 32, device=gpu).to(torch.float8_e4m3fn)
+    for bad in (torch.empty(64, 8, dtype=torch.bfloat16, device=gpu),      # too narrow
+                torch.empty(64, 16, dtype=torch.float32, device=gpu),      # dtype
+                torch.empty(16, 64, dtype=torch.bfloat16, device=gpu).t()):  # column stride
+        with pytest.raises((ValueError, TypeError)):
+            ops.fp8_gemm(a, bt, 1.0, 1.0, b_transposed=True, out=bad)
+    wide = torch.full((64, 24), 7.0, dtype=torch.bfloat16, device=gpu)
+    c = ops.fp8_gemm(a, bt, 1.0, 1.0, b_transposed=True, out=wide[:, :16])
+    assert torch.equal(c, torch.zeros(64, 16, dtype=torch.bfloat16, device=gpu))
+    assert torch.equal(wide[:, 16:], torch.full((64, 8), 7.0, dtype=torch.bfloat16, device=gpu))

@@ -287,3 +287,16 @@ def test_scale_quantize_qkv_equals_three_calls(gpu: torch.device, dtype: torch.d
         _assert_scales_equal(s.cpu().numpy(), s2.cpu().numpy())
         assert c.shape == c2.shape
         assert torch.equal(c.view(torch.uint8), c2.view(torch.uint8))
+
+
+def test_scale_quantize_qkv_refuses_mismatched_shapes(gpu: torch.device) -> None:
+    """One B, H and D go to the library for all three tensors, so any
+    disagreement is refused on the host, before a launch could read past K or V."""
+    q = torch.zeros(1, 2, 64, 64, dtype=torch.bfloat16, device=gpu)
+    kv = torch.zeros(1, 2, 128, 64, dtype=torch.bfloat16, device=gpu)
+    for k, v in ((kv[:, :1], kv[:, :1]),                                  # H differs
+                 (torch.zeros(1, 2, 128, 32, dtype=torch.bfloat16, device=gpu),) * 2,  # D
+                 (kv, kv[:, :, :100]),                                    # Skv differs
+                 (torch.zeros(2, 2, 128, 64, dtype=torch.bfloat16, device=gpu),) * 2):  # B
+        with pytest.raises(ValueError, match="share one"):
+            ops.scale_quantize_qkv(q, k, v)
