@@ -54,6 +54,17 @@ def _check_cuda(name: str, t: torch.Tensor) -> None:
         raise ValueError(f"{name} must be a GPU tensor (got device {t.device})")
 
 
+def _on_device_of(ref: torch.Tensor, **tensors: torch.Tensor | None) -> None:
+    """Every given tensor (None skipped) lives on ``ref``'s GPU: the kernels
+    launch on that device and dereference each pointer there."""
+    for name, t in tensors.items():
+        if t is None:
+            continue
+        _check_cuda(name, t)
+        if t.device != ref.device:
+            raise ValueError(f"{name} is on {t.device}, the other operands on {ref.device}")
+
+
 def _bhsd_view(x: torch.Tensor) -> tuple[int, int, int, int, int, int, int]:
     """(B, H, S, D, sb, sh, ss) for a 4-D (B, H, S, D) tensor with unit stride on D."""
     if x.dim() != 4:
@@ -118,7 +129,7 @@ def quantize(x: torch.Tensor, dequant: torch.Tensor, granularity: Granularity = 
     operand layout of the attention kernel.
     """
     dt = _in_dtype("x", x)
-    _check_cuda("dequant", dequant)
+    _on_device_of(x, dequant=dequant)
     x4 = _as4d(x)
     B, H, S, D, sb, sh, ss = _bhsd_view(x4)
     dq = dequant.to(torch.float32).contiguous()
@@ -194,8 +205,7 @@ def scale_quantize_qkv(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     if k.shape[:2] != q.shape[:2] or k.shape[3] != D or v.shape != k.shape:
         raise ValueError(f"k and v must share one (B, H, Skv, D) shape with q's B, H and D "
                          f"(q {tuple(q.shape)}, k {tuple(k.shape)}, v {tuple(v.shape)})")
-    if k.device != q.device or v.device != q.device:
-        raise ValueError("q, k and v must be on one device")
+    _on_device_of(q, k=k, v=v)
     g = _GRAN[granularity]
     G = B * H if granularity == "bh" else 1
     ldv = _round_up(Skv, V_PAD)
@@ -243,6 +253,7 @@ def rmsnorm_scale_quantize(x: torch.Tensor, weight: torch.Tensor | None = None,
     w_ptr = None
     if weight is not None:
         _check_bf16("weight", weight)
+        _on_device_of(x, weight=weight)
         if weight.shape != (D,) or not weight.is_contiguous():
             raise ValueError(f"weight must be a contiguous ({D},) bf16 vector")
         w_ptr = weight.data_ptr()
@@ -250,8 +261,8 @@ def rmsnorm_scale_quantize(x: torch.Tensor, weight: torch.Tensor | None = None,
     cos_ptr = sin_ptr = None
     if rope is not None:
         cos, sin = rope
+        _on_device_of(x, cos=cos, sin=sin)
         for name, t in (("cos", cos), ("sin", sin)):
-            _check_cuda(name, t)
             if t.dtype != torch.float32 or t.shape != (S, D) or not t.is_contiguous():
                 raise ValueError(f"{name} must be a contiguous float32 ({S}, {D}) table")
         cos_ptr, sin_ptr = cos.data_ptr(), sin.data_ptr()
@@ -323,8 +334,12 @@ def attention_fp8(q8: torch.Tensor, k8: torch.Tensor, vt8: torch.Tensor, q_scale
     select the shared-prefix candidate mask.  ``kv_splits`` > 1 runs the key
     range in that many parts and merges them (``rp_fp8_attn_fwd_split``).
     """
+    _check_cuda("q8", q8)
+    _on_device_of(q8, k8=k8, vt8=vt8, q_scale=q_scale, k_scale=k_scale, v_scale=v_scale,
+                  out=out)
     for name, t in (("q8", q8), ("k8", k8), ("vt8", vt8)):
-        _check_cuda(name, t)
+        if t.dtype not in (torch.float8_e4m3fn, torch.uint8):
+            raise TypeError(f"{name} must hold e4m3fn codes (float8_e4m3fn or uint8), got {t.dtype}")
         if not t.is_contiguous():
             raise ValueError(f"{name} must be contiguous")
     B, H, Sq, D = q8.shape
@@ -485,7 +500,9 @@ def fp8_gemm(a8: torch.Tensor, b8: torch.Tensor, a_scale: float | torch.Tensor,
     (``rp_fp8_linear``, an nn.Linear epilogue; the reference GEMM has none).
     """
     _check_cuda("a8", a8)
-    _check_cuda("b8", b8)
+    _on_device_of(a8, b8=b8, out=out, bias=bias,
+                  a_scale=a_scale if isinstance(a_scale, torch.Tensor) else None,
+                  b_scale=b_scale if isinstance(b_scale, torch.Tensor) else None)
     if a8.dim() != 2 or b8.dim() != 2:
         raise ValueError("A and B must be 2-D")
     for name, t in (("A", a8), ("B", b8)):

@@ -440,3 +440,23 @@ def test_diffusers_bridge_runs_fp8_kernel_on_bshd(gpu: torch.device) -> None:
         q.permute(0, 2, 1, 3).float(), k.permute(0, 2, 1, 3).float(),
         v.permute(0, 2, 1, 3).float()).permute(0, 2, 1, 3)
     assert _rel_vs_sdpa(out, ref) < 0.10
+
+
+def test_operands_off_the_gpu_are_refused(gpu: torch.device) -> None:
+    """Scales or an output buffer in host memory would be dereferenced by the
+    kernel: refused on the host before any launch, like codes of a wrong dtype."""
+    q8 = torch.zeros(1, 1, 128, 64, dtype=torch.uint8, device=gpu)
+    vt8 = torch.zeros(1, 1, 64, 128, dtype=torch.uint8, device=gpu)
+    one = torch.ones(1, device=gpu)
+    with pytest.raises(ValueError, match="GPU tensor"):
+        ops.attention_fp8(q8, q8, vt8, one.cpu(), one, one, 0.125)
+    with pytest.raises(ValueError, match="GPU tensor"):
+        ops.attention_fp8(q8, q8, vt8, one, one, one, 0.125,
+                          out=torch.empty(1, 1, 128, 64, dtype=torch.bfloat16))
+    with pytest.raises(TypeError, match="codes"):
+        ops.attention_fp8(q8.to(torch.bfloat16), q8, vt8, one, one, one, 0.125)
+    a = torch.zeros(32, 32, dtype=torch.uint8, device=gpu)
+    with pytest.raises(ValueError, match="GPU tensor"):
+        ops.fp8_gemm(a, a, torch.ones(1), 1.0, b_transposed=True)
+    out = ops.attention_fp8(q8, q8, vt8, one, one, one, 0.125)
+    assert torch.equal(out, torch.zeros_like(out))      # all-zero codes: mean of zero V
