@@ -198,7 +198,9 @@ int rp_fp8_attn_fwd_split(const uint8_t* q8, const uint8_t* k8, const uint8_t* v
  * 114-123), the rank-4 item of the path's next steps.  codes are BHSD
  * contiguous; D in {64, 128}; x, strides*2, weight, tables and codes
  * 16-byte aligned; the sum of squares runs in the order the header of
- * rp_prologue.hip states. */
+ * rp_prologue.hip states.  The workspace holds the amax pass's partial
+ * maxima and each row's fp32 inverse norm, which the apply pass reads back
+ * (4 bytes per row); it must not be shared by calls that may overlap. */
 size_t rp_fp8_rmsnorm_quant_workspace_bytes(int64_t B, int64_t H, int64_t S, int64_t D,
                                             int granularity);
 int rp_fp8_rmsnorm_scale_quantize(const void* x, int64_t B, int64_t H, int64_t S, int64_t D,

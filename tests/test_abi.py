@@ -172,10 +172,12 @@ def test_rmsnorm_quantize_argument_checks(kw: dict, status: int, msg: str) -> No
 
 def test_rmsnorm_workspace_sizing() -> None:
     L = _capi.lib()
-    # one partial per 16384 elements of a group: 64 rows x 128 per (b, h) -> 1 block each
-    assert L.rp_fp8_rmsnorm_quant_workspace_bytes(1, 2, 64, 128, 0) == 2 * 4
-    assert L.rp_fp8_rmsnorm_quant_workspace_bytes(1, 2, 64, 128, 1) == 1 * 4
-    assert L.rp_fp8_rmsnorm_quant_workspace_bytes(1, 40, 75600, 128, 0) == 40 * 591 * 4
+    # one partial per 16384 elements of a group (64 rows x 128 per (b, h) -> 1 block
+    # each), padded to 256 bytes, then one fp32 inverse norm per row
+    assert L.rp_fp8_rmsnorm_quant_workspace_bytes(1, 2, 64, 128, 0) == 256 + 2 * 64 * 4
+    assert L.rp_fp8_rmsnorm_quant_workspace_bytes(1, 2, 64, 128, 1) == 256 + 2 * 64 * 4
+    assert L.rp_fp8_rmsnorm_quant_workspace_bytes(1, 40, 75600, 128, 0) == \
+        (40 * 591 * 4 + 255) // 256 * 256 + 40 * 75600 * 4
     assert L.rp_fp8_rmsnorm_quant_workspace_bytes(1, 2, 64, 96, 0) == 0
 
 
