@@ -381,7 +381,7 @@ def main() -> int:
     if args.gpus != 1 or world != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}, "
               f"WORLD_SIZE={world}); the FP8 attention path shards over heads with no "
-              f"collective -- see DESIGN.md", file=sys.stderr)
+              f"collective, so one GPU's throughput is the per-GPU figure", file=sys.stderr)
         return 2
 
     # a run's own launch-configuration cache, unless the caller names one
