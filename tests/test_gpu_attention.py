@@ -460,3 +460,45 @@ def test_operands_off_the_gpu_are_refused(gpu: torch.device) -> None:
         ops.fp8_gemm(a, a, torch.ones(1), 1.0, b_transposed=True)
     out = ops.attention_fp8(q8, q8, vt8, one, one, one, 0.125)
     assert torch.equal(out, torch.zeros_like(out))      # all-zero codes: mean of zero V
+
+
+def test_diffusers_bridge_recomputes_non_finite_output_with_sdpa(gpu: torch.device,
+                                                                 monkeypatch: pytest.MonkeyPatch,
+                                                                 caplog) -> None:
+    """The bridge's guard (reference diffusers_backend.py, non-finite check
+    after the FP8 call): a non-finite FP8 result is replaced by native SDPA's
+    output for the same call, with a warning.  First forced (the FP8 call
+    writes NaN), then real: an infinite V entry makes its head's FP8 output
+    NaN, and the call returns exactly what SDPA returns for it."""
+    import logging
+
+    from repercep_runtime_amd.attention import diffusers_backend as db
+
+    g = torch.Generator(device=gpu).manual_seed(6)
+    q, k, v = (torch.randn(1, 4096, 2, 64, device=gpu, generator=g).to(torch.bfloat16)
+               for _ in range(3))
+    assert db._route_should_use_fp8(q, k, v)       # past the bridge's length crossover
+    sdpa = torch.nn.functional.scaled_dot_product_attention(
+        q.permute(0, 2, 1, 3), k.permute(0, 2, 1, 3), v.permute(0, 2, 1, 3)).permute(0, 2, 1, 3)
+
+    def nan_fp8(*_a, out, **_k):
+        out.fill_(float("nan"))
+        return out
+
+    with monkeypatch.context() as m:
+        m.setattr(ops, "fp8_flash_attention", nan_fp8)
+        with caplog.at_level(logging.WARNING):
+            out = db._repercep_fp8_attention(q, k, v)
+    assert torch.equal(out, sdpa)
+    assert "non-finite" in caplog.text
+
+    v_inf = v.clone()
+    v_inf[0, 7, 1, 3] = float("inf")
+    fp8 = ops.fp8_flash_attention(q.permute(0, 2, 1, 3), k.permute(0, 2, 1, 3),
+                                  v_inf.permute(0, 2, 1, 3))
+    assert not torch.isfinite(fp8[0, 1]).all() and torch.isfinite(fp8[0, 0]).all()
+    out = db._repercep_fp8_attention(q, k, v_inf)
+    ref = torch.nn.functional.scaled_dot_product_attention(
+        q.permute(0, 2, 1, 3), k.permute(0, 2, 1, 3),
+        v_inf.permute(0, 2, 1, 3)).permute(0, 2, 1, 3)
+    torch.testing.assert_close(out, ref, rtol=0, atol=0, equal_nan=True)
