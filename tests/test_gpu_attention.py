@@ -502,3 +502,24 @@ def test_diffusers_bridge_recomputes_non_finite_output_with_sdpa(gpu: torch.devi
         q.permute(0, 2, 1, 3), k.permute(0, 2, 1, 3),
         v_inf.permute(0, 2, 1, 3)).permute(0, 2, 1, 3)
     torch.testing.assert_close(out, ref, rtol=0, atol=0, equal_nan=True)
+
+
+@pytest.mark.parametrize("kind", ["sharp", "rising_max"])
+def test_softmax_extremes_vs_oracle(gpu: torch.device, kind: str) -> None:
+    """Rows whose scores are dominated by one key (Q and K scaled by 6), and
+    keys whose scale rises along the sequence so that the running max moves at
+    almost every tile (the O^T rescale and alpha path run constantly)."""
+    g = torch.Generator().manual_seed(31 if kind == "sharp" else 32)
+    B, H, S, D = (1, 2, 700, 128) if kind == "sharp" else (1, 2, 900, 64)
+    q = torch.randn(B, H, S, D, generator=g)
+    k = torch.randn(B, H, S, D, generator=g)
+    v = torch.randn(B, H, S, D, generator=g)
+    if kind == "sharp":
+        q, k = q * 6.0, k * 6.0
+    else:
+        k = k * torch.linspace(0.2, 4.0, S).reshape(1, 1, S, 1)
+    q, k, v = (t.to(torch.bfloat16) for t in (q, k, v))
+    out = ops.fp8_flash_attention(q.to(gpu), k.to(gpu), v.to(gpu),
+                                  out_dtype=torch.float32).cpu().numpy()[0]
+    ref, _ = _oracle_rows(q, k, v, list(range(H)), np.arange(S), sm_scale=D ** -0.5)
+    _check(out, ref, f"{kind} (1, {H}, {S}, {D})")
