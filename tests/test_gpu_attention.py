@@ -93,6 +93,10 @@ CASES = [
     ("cross_d256", 1, 1, 300, 450, 256, False),
     ("causal_d256", 1, 2, 513, 513, 256, True),
     ("tiny_d256", 1, 1, 5, 7, 256, False),
+    # causal with unequal lengths: the reference's top-left mask kv <= q
+    # (fp8_flash_attn.py:350-352); rows past Skv see every key
+    ("causal_q_longer", 1, 2, 700, 300, 128, True),
+    ("causal_kv_longer", 1, 2, 300, 700, 64, True),
 ]
 
 
@@ -245,6 +249,9 @@ SPLIT_CASES = [
     ("d256", 1, 2, 300, 1000, 256, False, None, None, (2, 8)),
     ("d256_causal", 1, 1, 600, 600, 256, True, None, None, (3,)),
     ("d32", 1, 2, 300, 1000, 32, False, None, None, (3,)),
+    # causal, 256 queries against 1000 keys: splits past every query hold
+    # nothing (their running max stays -inf) and the merge ignores them
+    ("causal_kv_longer", 1, 2, 256, 1000, 128, True, None, None, (2, 4)),
 ]
 
 
