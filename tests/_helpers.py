@@ -51,3 +51,14 @@ def bf16_to_f32(bits: np.ndarray) -> np.ndarray:
 def vt_to_bhsd(vt: np.ndarray, S: int) -> np.ndarray:
     """(B, H, D, ldv) transposed V codes -> (B, H, S, D)."""
     return np.ascontiguousarray(np.swapaxes(vt[..., :S], -1, -2))
+
+
+def golden_quant_cases() -> list[tuple[str, np.ndarray, np.ndarray, np.ndarray]]:
+    """(name, bf16 input bits (B, H, S, D), dequant scales, codes) from
+    tests/golden/quant_bf16.npz (written by tests/golden/make_quant_vectors.py:
+    torch's CPU ops in the reference quantizer's order)."""
+    from pathlib import Path
+
+    data = np.load(Path(__file__).with_name("golden") / "quant_bf16.npz")
+    names = sorted({k.rsplit("_x_bits", 1)[0] for k in data.files if k.endswith("_x_bits")})
+    return [(n, data[f"{n}_x_bits"], data[f"{n}_dequant"], data[f"{n}_codes"]) for n in names]

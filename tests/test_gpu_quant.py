@@ -300,3 +300,17 @@ def test_scale_quantize_qkv_refuses_mismatched_shapes(gpu: torch.device) -> None
                  (torch.zeros(2, 2, 128, 64, dtype=torch.bfloat16, device=gpu),) * 2):  # B
         with pytest.raises(ValueError, match="share one"):
             ops.scale_quantize_qkv(q, k, v)
+
+
+def test_device_reproduces_golden_vectors(gpu: torch.device) -> None:
+    """The device quantizer on the committed vectors of the reference
+    quantizer's torch ops: every scale and code bit for bit, both layouts."""
+    from tests._helpers import golden_quant_cases, vt_to_bhsd
+
+    for name, bits, dq_ref, codes_ref in golden_quant_cases():
+        x = torch.from_numpy(bits.view(np.int16).copy()).view(torch.bfloat16).to(gpu)
+        dq, codes = ops.scale_quantize(x, "bh", "bhsd")
+        assert np.array_equal(dq.cpu().numpy().view(np.uint32), dq_ref.view(np.uint32)), name
+        assert np.array_equal(codes_np(codes), codes_ref), name
+        _, vt = ops.scale_quantize(x, "bh", "bhds")
+        assert np.array_equal(vt_to_bhsd(codes_np(vt), x.shape[2]), codes_ref), name
