@@ -62,3 +62,14 @@ def golden_quant_cases() -> list[tuple[str, np.ndarray, np.ndarray, np.ndarray]]
     data = np.load(Path(__file__).with_name("golden") / "quant_bf16.npz")
     names = sorted({k.rsplit("_x_bits", 1)[0] for k in data.files if k.endswith("_x_bits")})
     return [(n, data[f"{n}_x_bits"], data[f"{n}_dequant"], data[f"{n}_codes"]) for n in names]
+
+
+def golden_gemm_cases() -> list[tuple[str, np.ndarray, np.ndarray, float, float, np.ndarray]]:
+    """(name, A8 (M, K), B8 (K, N) codes, a_scale, b_scale, C bf16 bits) from
+    tests/golden/gemm_small_int.npz (tests/golden/make_gemm_vectors.py)."""
+    from pathlib import Path
+
+    data = np.load(Path(__file__).with_name("golden") / "gemm_small_int.npz")
+    names = sorted({k.rsplit("_a8", 1)[0] for k in data.files if k.endswith("_a8")})
+    return [(n, data[f"{n}_a8"], data[f"{n}_b8"], float(data[f"{n}_scales"][0]),
+             float(data[f"{n}_scales"][1]), data[f"{n}_c_bits"]) for n in names]

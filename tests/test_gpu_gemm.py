@@ -177,3 +177,19 @@ def test_out_argument_is_checked(gpu: torch.device) -> None:
     c = ops.fp8_gemm(a, bt, 1.0, 1.0, b_transposed=True, out=wide[:, :16])
     assert torch.equal(c, torch.zeros(64, 16, dtype=torch.bfloat16, device=gpu))
     assert torch.equal(wide[:, 16:], torch.full((64, 8), 7.0, dtype=torch.bfloat16, device=gpu))
+
+
+def test_device_reproduces_golden_vectors(gpu: torch.device) -> None:
+    """The committed known-answer vectors through the reference's (K, N)
+    row-major B (the transposing path) and through the K-contiguous operand,
+    scales as host floats and as device tensors: every output bit for bit."""
+    from tests._helpers import golden_gemm_cases
+
+    for name, a8, b8, sa, sb, c_bits in golden_gemm_cases():
+        a = torch.from_numpy(a8).to(gpu).view(torch.float8_e4m3fn)
+        b = torch.from_numpy(b8).to(gpu).view(torch.float8_e4m3fn)
+        c1 = ops.fp8_gemm(a, b, sa, sb)
+        c2 = ops.fp8_gemm(a, b.t().contiguous(), torch.tensor([sa], device=gpu),
+                          torch.tensor([sb], device=gpu), b_transposed=True)
+        for c in (c1, c2):
+            assert np.array_equal(bf16_bits(c), c_bits), name
