@@ -113,3 +113,27 @@ def test_qknorm_attention_matches_unfused(gpu: torch.device) -> None:
                                   out_dtype=torch.float32, kv_splits=1)
     assert torch.equal(out, ref)
     assert math.isfinite(float(out.abs().max()))
+
+
+@pytest.mark.parametrize("gran", ["bh", "tensor"])
+def test_unit_weight_is_the_identity_on_extremes(gpu: torch.device, gran: str) -> None:
+    """bf16(bf16(x * r) * 1) = bf16(x * r): the weighted and unweighted
+    prologues agree bit for bit -- scales, codes and NaN payloads -- on rows
+    with NaN, Inf, values whose squares overflow (r = 0), values whose squares
+    underflow, and zeros, with and without eps."""
+    g = torch.Generator().manual_seed(77)
+    x = torch.randn(2, 3, 40, 128, generator=g)
+    x[0, 0, 1, 5] = float("nan")
+    x[0, 1, 2, 9] = float("inf")
+    x[0, 2, 3, 0] = -float("inf")
+    x[1, 0, 4] = 1e30                                  # squares overflow: r = 0
+    x[1, 0, 5] *= 1e-25                                # squares underflow to 0
+    x[1, 1, 6] = 0.0
+    x[1, 2, 7, 3] = 3e38
+    x = x.to(torch.bfloat16).to(gpu)
+    ones = torch.ones(128, dtype=torch.bfloat16, device=gpu)
+    for eps in (1e-6, 0.0):
+        dq_a, c_a = ops.rmsnorm_scale_quantize(x, None, eps, None, "half", gran)
+        dq_b, c_b = ops.rmsnorm_scale_quantize(x, ones, eps, None, "half", gran)
+        assert torch.equal(dq_a.view(torch.int32), dq_b.view(torch.int32)), eps
+        assert torch.equal(c_a.view(torch.uint8), c_b.view(torch.uint8)), eps
