@@ -2,19 +2,23 @@
 
 Default workload: BASELINE config 3, Wan-2.2 self-attention
 (B=1, H=40, S=75600, D=128, non-causal), bf16 inputs resident in HBM.
-One step = the whole hot path on one batch: per-(B,H) amax scale + e4m3fn
-quantization of Q, K and V (V written transposed) followed by the FP8
-flash-attention forward writing bf16 output -- the work of the reference's
-``fp8_flash_attention`` call.
+One step = the whole hot path on one batch: amax scale + e4m3fn quantization
+of Q, K and V (V written transposed) followed by the FP8 flash-attention
+forward writing bf16 output -- the work of the reference's
+``fp8_flash_attention`` call.  Scales are per tensor by default, as BASELINE
+configs 2-5 state them (``--granularity bh`` runs the reference's per-(B,H)
+scales; the attention kernel's work is the same either way).
 
 ``value`` is whole-step throughput in TFLOP/s (algorithmic FLOPs
 4*B*H*S^2*D per step / step time).  ``roofline`` is the attention kernel's
 own MFMA roofline, its average launch time measured with HIP events on the
-stream the kernel runs on.  ``quantize`` reports the quantizer's HBM rate
-(5 bytes per element).  ``cpu_baseline`` times the CPU oracle (the C
-restatement of the reference's FP8 attention) on a bounded sample, and
-``cpu_reference_sdpa`` the reference's own CPU attention path (one torch
-SDPA call in bf16).
+stream the kernel runs on; its ``traffic`` (HBM bytes per launch) is read from
+profiles/traffic.json, which the rocprofv3 counter runs wrote, and says so in
+``traffic_source``.  ``quantize`` reports the quantizer's HBM rate (5 bytes
+per element).  ``cpu_baseline`` times the reference's own CPU attention path
+(AMXSDPAAttention: one torch SDPA call in bf16 on all host cores) on a
+bounded sample, and ``cpu_oracle`` the C restatement of the reference's FP8
+attention (the test oracle) on another.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config NAME]
 """
@@ -34,6 +38,9 @@ sys.path.insert(0, str(ROOT))
 
 FP8_PEAK_TFLOPS = 5000.0  # MI355X dense FP8 MFMA, published
 HBM_PEAK_GBPS = 8000.0    # MI355X HBM3E, published
+TRAFFIC_SOURCE = ("profiles/traffic.json: FETCH_SIZE + WRITE_SIZE per launch from two "
+                  "rocprofv3 --pmc runs of this bench, scaled by a plain copy's readings; "
+                  "not measured in this run")
 
 
 def log(*a: object) -> None:
@@ -63,10 +70,11 @@ def _grow(run, start: int, limit: int, budget_s: float) -> tuple[int, float]:
     return rows, t
 
 
-def cpu_baseline(cfg, budget_s: float) -> dict:
+def cpu_oracle_timing(cfg, budget_s: float) -> dict:
     """The CPU oracle (C restatement of the reference's FP8 attention, OpenMP
     over query rows) on one head of the workload: a row slice of the queries
-    against all keys, scaled to the workload's FLOPs."""
+    against all keys, scaled to the workload's FLOPs.  Reported beside the
+    baseline, not as it."""
     import numpy as np
     import torch
 
@@ -104,11 +112,14 @@ def cpu_baseline(cfg, budget_s: float) -> dict:
 
 
 def cpu_sdpa_baseline(cfg, budget_s: float) -> dict:
-    """The reference's CPU attention path (one torch SDPA call in bf16, all
-    host cores) on one head, a row slice of the queries against all keys."""
+    """The reference's CPU attention path -- the registry's CPU floor
+    AMXSDPAAttention, whose call is one torch SDPA in bf16
+    (src/repercep/attention/amx_sdpa.py:76-94, registry.py:126) -- on all host
+    cores, on one head: a row slice of the queries against all keys, scaled
+    to the workload's FLOPs."""
     import torch
 
-    from oracle.cpu_sdpa import cpu_threads, sdpa_cpu
+    from oracle.cpu_sdpa import cpu_model, cpu_threads, sdpa_cpu
 
     threads = cpu_threads()
     gen = torch.Generator().manual_seed(cfg.seed)
@@ -123,8 +134,11 @@ def cpu_sdpa_baseline(cfg, budget_s: float) -> dict:
 
     rows, t = _grow(run, 256, cfg.Sq, budget_s)
     tflops = 4.0 * rows * cfg.Skv * cfg.D / t / 1e12
-    return {"value": round(tflops, 4), "unit": "TFLOP/s", "cores": threads,
-            "sample": f"torch SDPA bf16 on CPU, 1 head, {rows} query rows in {t:.2f} s"}
+    return {"value": round(tflops, 4), "unit": "TFLOP/s", "cores": threads, "kind": "port",
+            "sample": (f"the reference's CPU attention path (AMXSDPAAttention = torch SDPA "
+                       f"bf16, {threads} threads, {cpu_model()}): 1 head, {rows} query rows x "
+                       f"{cfg.Skv} keys x D={cfg.D} in {t:.2f} s; full {cfg.name} "
+                       f"extrapolates to {cfg.flops / (tflops * 1e12):.0f} s")}
 
 
 def bench_attention(args, cfg) -> dict:
@@ -139,6 +153,7 @@ def bench_attention(args, cfg) -> dict:
     # configs with QK RMSNorm take pre-norm Q/K: the norm runs fused into
     # their quantizers inside the step (rmsnorm_scale_quantize)
     fused_norm = cfg.rmsnorm_qk
+    gran = args.granularity
     q, k, v = attn_inputs(cfg, device=dev, normalize=not fused_norm)
     sm = cfg.D ** -0.5
     prefix = cfg.prefix
@@ -147,10 +162,10 @@ def bench_attention(args, cfg) -> dict:
     # launch configuration as the op resolves it (a timed search on a cache
     # miss for shapes too small to fill the GPU unsplit; see tuning.py)
     if fused_norm:
-        ops.fp8_flash_attention_qknorm(q, k, v, causal=cfg.causal, out=out)
+        ops.fp8_flash_attention_qknorm(q, k, v, causal=cfg.causal, out=out, granularity=gran)
     else:
         ops.fp8_flash_attention(q, k, v, causal=cfg.causal, prefix_len=prefix,
-                                suffix_len=cfg.suffix, out=out)
+                                suffix_len=cfg.suffix, out=out, granularity=gran)
     splits = ops.tuned_kv_splits(cfg.B, cfg.H, cfg.Sq, cfg.Skv, cfg.D, cfg.causal, prefix,
                                  cfg.suffix)
     log(f"[bench] kv_splits {splits}")
@@ -159,11 +174,11 @@ def bench_attention(args, cfg) -> dict:
         if ev is not None:
             ev[0].record(st)
         if fused_norm:
-            qs, q8 = ops.rmsnorm_scale_quantize(q)
-            ks, k8 = ops.rmsnorm_scale_quantize(k)
-            vs, vt8 = ops.scale_quantize(v, "bh", "bhds")
+            qs, q8 = ops.rmsnorm_scale_quantize(q, granularity=gran)
+            ks, k8 = ops.rmsnorm_scale_quantize(k, granularity=gran)
+            vs, vt8 = ops.scale_quantize(v, gran, "bhds")
         else:   # what fp8_flash_attention runs: one library call for Q, K, V
-            qs, q8, ks, k8, vs, vt8 = ops.scale_quantize_qkv(q, k, v, "bh")
+            qs, q8, ks, k8, vs, vt8 = ops.scale_quantize_qkv(q, k, v, gran)
         if ev is not None:
             ev[1].record(st)
         ops.attention_fp8(q8.view(torch.uint8), k8.view(torch.uint8), vt8.view(torch.uint8),
@@ -243,7 +258,8 @@ def bench_attention(args, cfg) -> dict:
         "dtype": "fp8_e4m3fn (fp32 accumulate, bf16 out)",
         "data": "synthetic: seeded N(0,1) bf16 Q/K/V generated on the GPU",
         "config": {"workload": cfg.name, "B": cfg.B, "H": cfg.H, "Sq": cfg.Sq, "Skv": cfg.Skv,
-                   "D": cfg.D, "causal": cfg.causal, "scale_granularity": "per (b,h)",
+                   "D": cfg.D, "causal": cfg.causal,
+                   "scale_granularity": "per tensor" if gran == "tensor" else "per (b,h)",
                    "kv_splits": splits, "flops_per_step": cfg.flops},
         "roofline": {
             "bound": "mfma",
@@ -252,6 +268,7 @@ def bench_attention(args, cfg) -> dict:
             "unit": "TFLOP/s",
             "frac": round(tflops_attn / FP8_PEAK_TFLOPS, 4),
             "traffic": _traffic_from_profiles("attn_fwd_kernel", cfg.name),
+            "traffic_source": TRAFFIC_SOURCE,
             "kernel": "attn_fwd_kernel",
             "kernel_ms": round(attn_ms, 4),
         },
@@ -317,6 +334,7 @@ def bench_gemm(args, cfg) -> dict:
         "roofline": {"bound": "mfma", "achieved": round(tf, 2), "peak": FP8_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(tf / FP8_PEAK_TFLOPS, 4),
                      "traffic": _traffic_from_profiles("gemm256_kernel", cfg.name),
+                     "traffic_source": TRAFFIC_SOURCE,
                      "kernel": "gemm256_kernel", "kernel_ms": round(gemm_ms, 4)},
         "quantize": {"ms": round(quant_ms, 4),
                      "achieved_GBps": round(5 * cfg.M * cfg.K / (quant_ms * 1e-3) / 1e9, 1)},
@@ -373,6 +391,9 @@ def main() -> int:
     ap.add_argument("--library-gemm", action="store_true",
                     help="c4_wan_ffn_up only: also time the vendor library's FP8 GEMM "
                          "(torch._scaled_mm) on the same operands, for comparison")
+    ap.add_argument("--granularity", choices=("tensor", "bh"), default="tensor",
+                    help="attention configs: scale groups -- per tensor (BASELINE's configs) "
+                         "or per (b, h) (the reference wrapper's)")
     ap.add_argument("--cpu-budget", type=float, default=12.0,
                     help="seconds of CPU work for the cpu_baseline sample (0 disables)")
     args = ap.parse_args()
@@ -411,8 +432,8 @@ def main() -> int:
         res = bench_attention(args, cfg)
         if args.cpu_budget > 0:
             log("[bench] timing the CPU baseline")
-            res["cpu_baseline"] = cpu_baseline(cfg, args.cpu_budget)
-            res["cpu_reference_sdpa"] = cpu_sdpa_baseline(cfg, args.cpu_budget / 3)
+            res["cpu_baseline"] = cpu_sdpa_baseline(cfg, args.cpu_budget)
+            res["cpu_oracle"] = cpu_oracle_timing(cfg, args.cpu_budget / 3)
     print(json.dumps(res), flush=True)
     return 0
 

@@ -170,6 +170,43 @@ void or_quantize_bf16_rows(const uint16_t* x, int64_t nrows, int64_t cols, int64
             codes[r * cols + c] = quant_one(x[r * row_stride + c], qmul);
 }
 
+/* -------------------------------------------------------- QK-norm prologue */
+
+/* RMSNorm over D of bf16 rows, unit weight, no rotation: the C form of
+ * oracle/prologue.py rmsnorm_rope(weight=None, rope=NONE), which restates the
+ * processors' norm_q / norm_k (reference docs/walkthroughs/02-architecture.md:
+ * 114-123) in the summation order the gfx950 prologue commits to:
+ *   ss_c = x_8c^2 + ... + x_8c+7^2 in order, per 8-element chunk c;
+ *   ss_c = ss_c + ss_(c^o) for o = D/16, ..., 1 (every chunk at once);
+ *   r = 1 / sqrt(ss_0 * fp32(1/D) + eps);  y = bf16(x * r).
+ * Every step is one correctly rounded fp32 operation (built without
+ * contraction).  D is a multiple of 16, at most 512.  x and y: nrows x D. */
+void or_rmsnorm_bf16_rows(const uint16_t* x, int64_t nrows, int D, float eps, uint16_t* y) {
+    const float inv_d = (float)(1.0 / (double)D);
+#pragma omp parallel for schedule(static)
+    for (int64_t r = 0; r < nrows; ++r) {
+        const uint16_t* xr = x + r * D;
+        float ss[64], nxt[64];
+        const int nc = D / 8;
+        for (int c = 0; c < nc; ++c) {
+            float acc = 0.0f;
+            for (int i = 0; i < 8; ++i) {
+                const float v = or_bf16_to_f32(xr[8 * c + i]);
+                const float sq = v * v;
+                acc = i == 0 ? sq : acc + sq;
+            }
+            ss[c] = acc;
+        }
+        for (int o = nc / 2; o >= 1; o /= 2) {
+            for (int c = 0; c < nc; ++c) nxt[c] = ss[c] + ss[c ^ o];
+            for (int c = 0; c < nc; ++c) ss[c] = nxt[c];
+        }
+        const float mean = ss[0] * inv_d;
+        const float rn = 1.0f / sqrtf(mean + eps);
+        for (int d = 0; d < D; ++d) y[r * D + d] = or_bf16_bits(or_bf16_to_f32(xr[d]) * rn);
+    }
+}
+
 /* --------------------------------------------------------------- attention */
 
 /* Mask modes: 0 none, 1 causal (kv <= q, fp8_flash_attn.py:350-352),

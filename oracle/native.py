@@ -56,6 +56,7 @@ def lib() -> ctypes.CDLL:
         _u8p, _u8p, ctypes.c_int, ctypes.c_int, ctypes.c_int,
         ctypes.c_float, ctypes.c_float, _i32p, ctypes.c_int, _u16p,
     ]
+    L.or_rmsnorm_bf16_rows.argtypes = [_u16p, _i64, ctypes.c_int, ctypes.c_float, _u16p]
     L.or_num_threads.restype = ctypes.c_int
     _lib = L
     return L
@@ -101,6 +102,18 @@ def quantize_groups(bits: np.ndarray, n_groups: int) -> tuple[np.ndarray, np.nda
         scales[g] = dequant_from_amax(amax_bf16(flat[g]))
         codes[g] = quantize_bf16(flat[g], float(scales[g]))
     return scales, codes.reshape(bits.shape)
+
+
+def rmsnorm_bf16(bits: np.ndarray, eps: float) -> np.ndarray:
+    """RMSNorm over the last axis (unit weight, no rotation) of bf16 bit
+    patterns, as bf16 bit patterns: ``oracle.prologue.rmsnorm_rope`` in C."""
+    bits = np.ascontiguousarray(bits, dtype=np.uint16)
+    D = bits.shape[-1]
+    assert D % 16 == 0 and D <= 512
+    out = np.empty(bits.shape, dtype=np.uint16)
+    lib().or_rmsnorm_bf16_rows(_ptr(bits, _u16p), bits.size // D, D, ctypes.c_float(eps),
+                               _ptr(out, _u16p))
+    return out
 
 
 def attn_rows(

@@ -1,17 +1,17 @@
 """Install the FP8 backend on a Wan pipeline's attention processors.
 
-Mirrors the reference's Wan bridge (src/repercep/attention/wan_processor.py:
-26-116).  Wan's diffusers transformer owns its attention processors, so
-selecting an ``AttentionOp`` does not reach it.  Recent diffusers releases
-route ``WanAttnProcessor`` through ``dispatch_attention_fn(...,
-backend=processor._attention_backend)``; setting that attribute to the
-registered ``"repercep_fp8"`` backend sends Wan's attention calls to
+Reference counterpart: src/repercep/attention/wan_processor.py:26-116.
+Wan's diffusers transformer owns its attention processors, so selecting an
+``AttentionOp`` does not reach it.  Recent diffusers releases route
+``WanAttnProcessor`` through ``dispatch_attention_fn(...,
+backend=processor._attention_backend)``; a processor whose attribute names
+the registered ``"repercep_fp8"`` backend sends Wan's attention calls to
 ``diffusers_backend._repercep_fp8_attention`` and from there to the gfx950
 kernel, while the processor itself (projections, QK-norm, rotary embedding)
 stays diffusers' own.
 
-The same opt-in as the reference: ``REPERCEP_FP8_ATTENTION`` set to one of
-its accepted values.  Without diffusers, or with a release that lacks the
+The opt-in is the reference's: ``REPERCEP_FP8_ATTENTION`` set to one of its
+accepted values.  Without diffusers, or with a release that lacks the
 processor class, nothing is installed and the pipeline keeps its path.
 """
 
@@ -19,15 +19,16 @@ from __future__ import annotations
 
 import logging
 import os
-from typing import Any
+from typing import Any, Iterator
 
 logger = logging.getLogger(__name__)
 
 #: Values of REPERCEP_FP8_ATTENTION that opt in (the reference's set).
 FP8_ENV_VALUES = frozenset({"1", "true", "on", "triton", "scaled_mm", "fa", "flash"})
 
-#: Pipeline attributes that hold Wan transformers (A14B has two experts).
-TRANSFORMER_ATTRS = ("transformer", "transformer_2")
+#: Pipeline attributes that may hold a Wan transformer: Wan-2.2 A14B runs a
+#: high-noise and a low-noise expert.
+EXPERT_ATTRS = ("transformer", "transformer_2")
 
 
 def maybe_install_repercep_wan_attention(pipe: Any) -> bool:
@@ -39,52 +40,56 @@ def maybe_install_repercep_wan_attention(pipe: Any) -> bool:
 
 
 def install_repercep_wan_attention(pipe: Any) -> int:
-    """Give every Wan transformer of ``pipe`` a ``WanAttnProcessor`` bound to
-    the FP8 backend; returns how many accepted it."""
-    processor_cls = _wan_attn_processor_class()
-    if processor_cls is None:
+    """Give every Wan transformer of ``pipe`` one shared ``WanAttnProcessor``
+    bound to the FP8 backend; returns how many transformers accepted it."""
+    processor = _fp8_bound_processor()
+    if processor is None:
         return 0
+    return sum(_hand_over(expert, processor) for expert in _experts(pipe))
+
+
+def _fp8_bound_processor() -> Any | None:
+    """A fresh diffusers ``WanAttnProcessor`` whose dispatch backend is the
+    registered FP8 backend, or None when diffusers cannot provide one."""
+    try:
+        from diffusers.models.transformers.transformer_wan import WanAttnProcessor
+    except Exception as exc:  # diffusers absent, or a release without the class
+        logger.debug("wan attention: no WanAttnProcessor (%s: %s)", type(exc).__name__, exc)
+        return None
     from repercep_runtime_amd.attention import diffusers_backend
 
     try:
         backend = diffusers_backend.register_repercep_fp8_backend()
-        processor = processor_cls()
-    except Exception as exc:  # diffusers-version dependent
-        logger.debug("wan attention: backend or processor unavailable (%s: %s)",
-                     type(exc).__name__, exc)
-        return 0
-    processor._attention_backend = backend
-    processor._repercep_attention_backend = diffusers_backend.REPERCEP_FP8_BACKEND_NAME
-
-    installed = 0
-    for transformer in wan_transformers(pipe):
-        setter = getattr(transformer, "set_attn_processor", None)
-        if not callable(setter):
-            logger.debug("wan attention: %s has no set_attn_processor",
-                         type(transformer).__name__)
-            continue
-        try:
-            setter(processor)
-        except Exception as exc:  # model-version dependent
-            logger.warning("wan attention: %s refused the processor (%s: %s)",
-                           type(transformer).__name__, type(exc).__name__, exc)
-            continue
-        installed += 1
-    return installed
-
-
-def wan_transformers(pipe: Any) -> tuple[Any, ...]:
-    return tuple(t for t in (getattr(pipe, a, None) for a in TRANSFORMER_ATTRS) if t is not None)
-
-
-def _wan_attn_processor_class() -> type | None:
-    try:
-        from diffusers.models.transformers.transformer_wan import WanAttnProcessor
-    except Exception as exc:  # diffusers absent or too old
-        logger.debug("wan attention: WanAttnProcessor unavailable (%s: %s)",
+        processor = WanAttnProcessor()
+    except Exception as exc:  # the dispatcher's internals differ in this release
+        logger.debug("wan attention: cannot bind the FP8 backend (%s: %s)",
                      type(exc).__name__, exc)
         return None
-    return WanAttnProcessor
+    processor._attention_backend = backend
+    return processor
+
+
+def _experts(pipe: Any) -> Iterator[Any]:
+    for attr in EXPERT_ATTRS:
+        expert = getattr(pipe, attr, None)
+        if expert is not None:
+            yield expert
+
+
+def _hand_over(expert: Any, processor: Any) -> bool:
+    """``expert.set_attn_processor(processor)``; False when the transformer
+    has no such method or refuses."""
+    set_processor = getattr(expert, "set_attn_processor", None)
+    if not callable(set_processor):
+        logger.debug("wan attention: %s takes no attention processor", type(expert).__name__)
+        return False
+    try:
+        set_processor(processor)
+    except Exception as exc:  # model-version dependent
+        logger.warning("wan attention: %s refused the FP8 processor (%s: %s)",
+                       type(expert).__name__, type(exc).__name__, exc)
+        return False
+    return True
 
 
 __all__ = ["install_repercep_wan_attention", "maybe_install_repercep_wan_attention"]

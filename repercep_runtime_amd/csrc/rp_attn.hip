@@ -477,8 +477,15 @@ void attn_fwd_kernel(AttnArgs a) {
   const float q_scale = a.qs[bh * a.scale_stride];
   const float k_scale = a.ks[bh * a.scale_stride];
   const float v_scale = a.vs[bh * a.scale_stride];
-  // exp2 domain: s2 = dot * c2 with c2 = sm_scale*q_scale*k_scale*log2(e)
-  const float c2 = ((a.sm_scale * q_scale) * k_scale) * kLog2e;
+  // exp2 domain: s2 = dot * c2 with c2 = sm_scale*q_scale*k_scale*log2(e).
+  // A zero product (sm_scale = 0) becomes the smallest normal float: the
+  // reference scales the scores before masking them (fp8_flash_attn.py:
+  // 341-356), so every visible score is 0 and every masked one -inf, while
+  // here the masked raw score -inf times 0 would be NaN.  With c2 = FLT_MIN a
+  // visible score lands within 1e-30 of 0, which exp2 and the running max
+  // cannot tell from 0 (p = 448, alpha = 1 exactly), and -inf stays -inf.
+  const float c2_raw = ((a.sm_scale * q_scale) * k_scale) * kLog2e;
+  const float c2 = c2_raw == 0.0f ? 1.17549435e-38f : c2_raw;
 
   // ---- key range [kv_begin, kv_end): this workgroup's split; causal blocks
   // past the block's last query are skipped

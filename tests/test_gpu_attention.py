@@ -362,31 +362,129 @@ def test_codes_seen_by_kernel_match_oracle_codes(gpu: torch.device) -> None:
     assert np.array_equal(vt_to_bhsd(codes_np(vt8), C1.Skv), v8_ref)
 
 
-def _wan_sample(gpu: torch.device, cfg: AttnConfig, heads: list[int], nrows: int) -> None:
+def _group_scales_codes(x: torch.Tensor, heads: list[int], granularity: str
+                        ) -> tuple[dict, dict, float | None]:
+    """Oracle dequant scale and codes of the listed heads of a (1, H, S, D) bf16
+    CPU tensor: per (b, h) from the head alone, per tensor from the amax of
+    the whole tensor (third value; None per head)."""
+    bits = bf16_bits(x)
+    whole = None
+    if granularity == "tensor":
+        whole = float(native.dequant_from_amax(native.amax_bf16(bits)))
+    scales, codes = {}, {}
+    for h in heads:
+        s = whole if whole is not None else float(native.dequant_from_amax(
+            native.amax_bf16(bits[0, h])))
+        scales[h] = s
+        codes[h] = native.quantize_bf16(bits[0, h], s)
+    return scales, codes, whole
+
+
+def _wan_sample(gpu: torch.device, cfg: AttnConfig, heads: list[int], nrows: int,
+                granularity: str) -> None:
     q, k, v = attn_inputs(cfg, device=gpu)
-    out = ops.fp8_flash_attention(q, k, v, out_dtype=torch.float32)
+    out = ops.fp8_flash_attention(q, k, v, out_dtype=torch.float32, granularity=granularity)
+    gq = ops.scale_quantize_qkv(q, k, v, granularity)
     torch.cuda.synchronize()
     rng = np.random.default_rng(0)
     rows = np.sort(rng.choice(cfg.Sq, size=nrows, replace=False))
-    qc, kc, vc = q[:, heads].cpu(), k[:, heads].cpu(), v[:, heads].cpu()
-    # per-(b,h) scales depend only on the head's own data, so slicing heads is exact
-    ref, _ = _oracle_rows(qc, kc, vc, list(range(len(heads))), rows,
-                          sm_scale=cfg.D ** -0.5)
+    # per-tensor scales need every head; per-(b,h) scales only the sampled ones
+    src = (q, k, v) if granularity == "tensor" else (q[:, heads], k[:, heads], v[:, heads])
+    idx = heads if granularity == "tensor" else list(range(len(heads)))
+    ora = [_group_scales_codes(t.cpu(), idx, granularity) for t in src]
+    # the device scales are the oracle's, bit for bit
+    for (dev_s, (sc, _, whole)) in zip((gq[0], gq[2], gq[4]), ora):
+        dev_s = dev_s.cpu().numpy()
+        if granularity == "tensor":
+            assert dev_s.shape == (1,) and dev_s[0] == np.float32(whole)
+        else:
+            assert all(dev_s[h] == np.float32(sc[i]) for h, i in zip(heads, idx))
     got = out[0, heads][:, torch.from_numpy(rows).to(gpu)].cpu().numpy()
-    _check(got, ref, f"{cfg.name} heads {heads} rows {nrows}")
+    ref = np.stack([native.attn_rows(ora[0][1][i], ora[1][1][i], ora[2][1][i], ora[0][0][i],
+                                     ora[1][0][i], ora[2][0][i], cfg.D ** -0.5, rows,
+                                     block_n=ops.BLOCK_N) for i in idx])
+    _check(got, ref, f"{cfg.name} {granularity} heads {heads} rows {nrows}")
     assert torch.isfinite(out).all()
-    del q, k, v, out
+    del q, k, v, out, gq
     torch.cuda.empty_cache()
 
 
-def test_wan_self_attention_full_shape_sampled_rows(gpu: torch.device) -> None:
-    """C3 self (1, 40, 75600, 128): full kernel run, 128 rows x 3 heads vs oracle."""
-    _wan_sample(gpu, C3_SELF, [0, 17, 39], 128)
+@pytest.mark.parametrize("granularity", ["bh", "tensor"])
+def test_wan_self_attention_full_shape_sampled_rows(gpu: torch.device, granularity: str) -> None:
+    """C3 self (1, 40, 75600, 128): full kernel run, 128 rows x 3 heads vs oracle,
+    per-(b,h) scales (the reference's) and per-tensor scales (BASELINE's wording)."""
+    _wan_sample(gpu, C3_SELF, [0, 17, 39], 128, granularity)
 
 
-def test_wan_cross_attention_full_shape_sampled_rows(gpu: torch.device) -> None:
-    """C3 cross (Skv = 512): 512 rows x 4 heads vs oracle."""
-    _wan_sample(gpu, C3_CROSS, [0, 5, 20, 39], 512)
+@pytest.mark.parametrize("granularity", ["bh", "tensor"])
+def test_wan_cross_attention_full_shape_sampled_rows(gpu: torch.device, granularity: str) -> None:
+    """C3 cross (Skv = 512): 512 rows x 4 heads vs oracle, both granularities."""
+    _wan_sample(gpu, C3_CROSS, [0, 5, 20, 39], 512, granularity)
+
+
+def test_cosmos_full_shape_per_tensor_through_fused_qknorm(gpu: torch.device) -> None:
+    """BASELINE config 2, Cosmos (1, 32, 56320, 128): pre-norm Q/K through the
+    fused RMSNorm prologue, per-tensor scales, the full attention kernel run
+    (56320 is a whole number of 128-key tiles: no shifted last tile).  The
+    oracle normalises every row of Q and K on the CPU (oracle/c
+    or_rmsnorm_bf16_rows, the prologue's summation order) for the
+    whole-tensor amax; scales and the sampled heads' codes are bit-exact, and
+    128 rows x 3 heads of the output are within tolerance."""
+    from repercep_runtime_amd.workloads import C2
+
+    assert C2.Skv % 128 == 0
+    q, k, v = attn_inputs(C2, device=gpu, normalize=False)
+    out = ops.fp8_flash_attention_qknorm(q, k, v, granularity="tensor", out_dtype=torch.float32)
+    dqq, q8 = ops.rmsnorm_scale_quantize(q, granularity="tensor")
+    dqk, k8 = ops.rmsnorm_scale_quantize(k, granularity="tensor")
+    torch.cuda.synchronize()
+    heads = [0, 13, 31]
+    rows = np.sort(np.random.default_rng(2).choice(C2.Sq, size=128, replace=False))
+    ora = []
+    for x, dq_dev, c_dev in ((q, dqq, q8), (k, dqk, k8), (v, None, None)):
+        bits = bf16_bits(x.cpu())
+        if dq_dev is not None:
+            bits = native.rmsnorm_bf16(bits, 1e-6)
+        s = float(native.dequant_from_amax(native.amax_bf16(bits)))
+        codes = {h: native.quantize_bf16(bits[0, h], s) for h in heads}
+        if dq_dev is not None:
+            assert dq_dev.cpu().numpy()[0] == np.float32(s)
+            for h in heads:
+                assert np.array_equal(codes_np(c_dev[0, h]), codes[h]), h
+        ora.append((s, codes))
+        del bits
+    got = out[0, heads][:, torch.from_numpy(rows).to(gpu)].cpu().numpy()
+    ref = np.stack([native.attn_rows(ora[0][1][h], ora[1][1][h], ora[2][1][h], ora[0][0],
+                                     ora[1][0], ora[2][0], C2.D ** -0.5, rows,
+                                     block_n=ops.BLOCK_N) for h in heads])
+    _check(got, ref, f"c2 per-tensor heads {heads} rows 128")
+    assert torch.isfinite(out).all()
+    del q, k, v, out, q8, k8
+    torch.cuda.empty_cache()
+
+
+def test_zero_softmax_scale_gives_mean_of_visible_values(gpu: torch.device) -> None:
+    """scale = 0: the reference scales the scores before masking them, so each
+    row averages the values it may see (SDPA does the same).  Causal and a
+    ragged key range exercise the masked paths."""
+    g = torch.Generator().manual_seed(41)
+    S, D = 300, 64
+    q, k, v = (torch.randn(1, 2, S, D, generator=g).to(torch.bfloat16) for _ in range(3))
+    from oracle import quant
+
+    for causal in (False, True):
+        out = ops.fp8_flash_attention(q.to(gpu), k.to(gpu), v.to(gpu), causal=causal, scale=0.0,
+                                      out_dtype=torch.float32).cpu().numpy()[0]
+        assert np.isfinite(out).all(), causal
+        ref, _ = _oracle_rows(q, k, v, [0, 1], np.arange(S), sm_scale=0.0,
+                              mask=1 if causal else 0)
+        _check(out, ref, f"scale=0 causal={causal}")
+        # closed form: the running mean of the dequantized values
+        vs, v8 = native.quantize_groups(bf16_bits(v), 2)
+        vd = np.stack([quant.decode_e4m3fn(v8[0, h]) * vs[h] for h in range(2)])
+        mean = (np.cumsum(vd, axis=1) / np.arange(1, S + 1)[None, :, None] if causal
+                else np.broadcast_to(vd.mean(axis=1, keepdims=True), vd.shape))
+        assert np.abs(out - mean).max() < 2e-2, causal
 
 
 # ----------------------------------------------------------------------------
@@ -430,7 +528,7 @@ def test_op_matches_sdpa_like_the_reference(gpu: torch.device, shape: tuple, cau
 
 def test_diffusers_bridge_runs_fp8_kernel_on_bshd(gpu: torch.device) -> None:
     """(B, S, H, D) through the dispatcher bridge: FP8 branch taken, equal to
-    the op on permuted copies, close to SDPA."""
+    the op on permuted copies, within tolerance of the oracle, close to SDPA."""
     from repercep_runtime_amd.attention import diffusers_backend as db
 
     g = torch.Generator(device=gpu).manual_seed(4)
@@ -443,6 +541,12 @@ def test_diffusers_bridge_runs_fp8_kernel_on_bshd(gpu: torch.device) -> None:
                                      k.permute(0, 2, 1, 3).contiguous(),
                                      v.permute(0, 2, 1, 3).contiguous())
     assert torch.equal(out, via_op.permute(0, 2, 1, 3))
+    # the (B, S, H, D) result itself against the oracle on the same inputs
+    rows = np.sort(np.random.default_rng(4).choice(4096, size=384, replace=False))
+    bhsd = [t.permute(0, 2, 1, 3).contiguous().cpu() for t in (q, k, v)]
+    oref, _ = _oracle_rows(*bhsd, list(range(4)), rows, sm_scale=128 ** -0.5)
+    got = out[0, torch.from_numpy(rows).to(gpu)].permute(1, 0, 2).float().cpu().numpy()
+    _check(got, torch.from_numpy(oref).to(torch.bfloat16).float().numpy(), "bridge (B,S,H,D)")
     ref = torch.nn.functional.scaled_dot_product_attention(
         q.permute(0, 2, 1, 3).float(), k.permute(0, 2, 1, 3).float(),
         v.permute(0, 2, 1, 3).float()).permute(0, 2, 1, 3)

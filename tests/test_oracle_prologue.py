@@ -142,3 +142,44 @@ def test_quantize_prologue_is_the_quantizer_of_y() -> None:
     assert np.array_equal(dq, dq2) and np.array_equal(codes, codes2)
     # RMS-normalised rows have |y| <= sqrt(D): amax = 8 at most for D = 64
     assert float(np.max(np.abs(y))) <= 8.0
+
+
+@pytest.mark.parametrize("D", [64, 128, 256])
+def test_c_rmsnorm_equals_numpy_restatement(D: int) -> None:
+    """oracle/c or_rmsnorm_bf16_rows (used for full-size per-tensor scales) is
+    the numpy restatement bit for bit, on rows that stress the summation
+    order: mixed magnitudes inside a row, zero rows (r = 1/sqrt(eps)), rows
+    whose squares overflow (r = 0) or underflow, and a single large entry."""
+    from oracle import native
+
+    x = _x(D + 11, (3, 5, 130, D)).float()
+    x[0, 0, :, : D // 2] *= 1e3                      # order-sensitive sums
+    x[0, 1, 3] = 0.0
+    x[0, 2, 4] = 1e30
+    x[1, 0, 5] *= 1e-25
+    x[1, 1, 6] = 0.0
+    x[1, 1, 6, 7] = 5.0
+    bits = quant.bf16_bits(x.to(torch.bfloat16))
+    for eps in (1e-6, 0.0, 1e-2):
+        ref = P.f32_to_bits(P.rmsnorm_rope(bits, eps))
+        got = native.rmsnorm_bf16(bits, eps)
+        assert np.array_equal(got, ref), (D, eps, int((got != ref).sum()))
+
+
+def test_c_rmsnorm_planted_order_change_is_caught() -> None:
+    """A different summation order (plain left-to-right over the row) changes
+    some bf16 results on order-sensitive rows, so the pin above can tell."""
+    from oracle import native
+
+    x = _x(5, (1, 1, 4096, 128)).float()
+    x[..., ::3] *= 1e3
+    bits = quant.bf16_bits(x.to(torch.bfloat16))
+    got = P.bits_to_f32(native.rmsnorm_bf16(bits, 1e-6))
+    xf = P.bits_to_f32(bits)
+    ss = np.zeros(xf.shape[:-1], dtype=np.float32)
+    for d in range(128):
+        ss = (ss + xf[..., d] * xf[..., d]).astype(np.float32)
+    r = (np.float32(1.0) / np.sqrt((ss * np.float32(1 / 128) + np.float32(1e-6))
+                                   .astype(np.float32))).astype(np.float32)
+    naive = P.bf16_round(xf * r[..., None])
+    assert not np.array_equal(got, naive)
