@@ -129,6 +129,28 @@ int rp_fp8_scale_quantize_qkv(const void* q, const void* k, const void* v, int x
                               uint8_t* vt8, int64_t ldv, void* workspace,
                               size_t workspace_bytes, void* stream);
 
+/* Allocation-free variant of rp_fp8_scale_quantize_qkv.  No counterpart in
+ * the reference: it is for callers that cannot allocate device memory --
+ * code under HIP graph capture, serving loops and harnesses that forbid
+ * hipMalloc.  Same arguments, scales and codes as rp_fp8_scale_quantize_qkv,
+ * without the workspace: the partial maxima go to a static device array of
+ * RP_QKV_NOALLOC_SCRATCH_BYTES that each GPU holds until the process ends
+ * (the library allocates nothing, here or on any later call).  Shapes whose
+ * rp_fp8_quant_qkv_workspace_bytes exceeds that size are refused with
+ * RP_ERR_WORKSPACE (at 16384 elements per partial, 1 MiB covers e.g. three
+ * 1.4e9-element tensors per tensor-scale, fewer with many small heads).
+ * Every call on one GPU shares that GPU's array: calls that may overlap on
+ * one GPU (two streams, two host threads) race and must be serialised by
+ * the caller; calls in one stream are ordered. */
+#define RP_QKV_NOALLOC_SCRATCH_BYTES (1u << 20)
+int rp_fp8_scale_quantize_qkv_noalloc(const void* q, const void* k, const void* v, int x_dtype,
+                                      int64_t B, int64_t H, int64_t Sq, int64_t Skv, int64_t D,
+                                      int64_t qsb, int64_t qsh, int64_t qss, int64_t ksb,
+                                      int64_t ksh, int64_t kss, int64_t vsb, int64_t vsh,
+                                      int64_t vss, int granularity, float* dequant_out,
+                                      uint8_t* q8, uint8_t* k8, uint8_t* vt8, int64_t ldv,
+                                      void* stream);
+
 /* --------------------------------------------------------- attention
  * FP8 flash-attention forward, FA-2 online softmax in fp32, both dot
  * products on gfx950 e4m3 MFMAs, P re-quantized as e4m3fn(p * 448).

@@ -30,12 +30,14 @@ RP_MASK_SHARED_PREFIX = 2
 RP_ROPE_NONE = 0
 RP_ROPE_HALF = 1
 RP_ROPE_INTERLEAVED = 2
+RP_QKV_NOALLOC_SCRATCH_BYTES = 1 << 20
 
 #: Every function include/repercep_fp8.h declares.
 EXPORTS = (
     "rp_abi_version", "rp_status_string", "rp_last_error",
     "rp_fp8_quant_workspace_bytes", "rp_fp8_scale", "rp_fp8_quantize",
     "rp_fp8_scale_quantize", "rp_fp8_quant_qkv_workspace_bytes", "rp_fp8_scale_quantize_qkv",
+    "rp_fp8_scale_quantize_qkv_noalloc",
     "rp_fp8_attn_fwd",
     "rp_fp8_attn_workspace_bytes",
     "rp_fp8_attn_blocks_per_workgroup",
@@ -82,6 +84,9 @@ def _declare(L: ctypes.CDLL) -> None:
     L.rp_fp8_scale_quantize_qkv.restype = _int
     L.rp_fp8_scale_quantize_qkv.argtypes = ([_vp, _vp, _vp, _int] + [_i64] * 14
                                             + [_int, _vp, _vp, _vp, _vp, _i64, _vp, _sz, _vp])
+    L.rp_fp8_scale_quantize_qkv_noalloc.restype = _int
+    L.rp_fp8_scale_quantize_qkv_noalloc.argtypes = ([_vp, _vp, _vp, _int] + [_i64] * 14
+                                                    + [_int, _vp, _vp, _vp, _vp, _i64, _vp])
     L.rp_fp8_attn_fwd.restype = _int
     L.rp_fp8_attn_fwd.argtypes = [_vp, _vp, _vp, _i64, _vp, _vp, _vp, _int, _f32, _vp, _int,
                                   _i64, _i64, _i64, _int, _int, _int, _int, _int, _int, _int,

@@ -33,6 +33,8 @@
 #include <stdarg.h>
 #include <stdio.h>
 
+#include <mutex>
+
 namespace rp {
 namespace {
 
@@ -633,23 +635,23 @@ extern "C" size_t rp_fp8_quant_qkv_workspace_bytes(int64_t B, int64_t H, int64_t
   return align256(q) + align256(kv) + kv;
 }
 
-extern "C" int rp_fp8_scale_quantize_qkv(const void* q, const void* k, const void* v, int x_dtype,
-                                         int64_t B, int64_t H, int64_t Sq, int64_t Skv, int64_t D,
-                                         int64_t qsb, int64_t qsh, int64_t qss, int64_t ksb,
-                                         int64_t ksh, int64_t kss, int64_t vsb, int64_t vsh,
-                                         int64_t vss, int granularity, float* dequant_out,
-                                         uint8_t* q8, uint8_t* k8, uint8_t* vt8, int64_t ldv,
-                                         void* workspace, size_t workspace_bytes, void* stream) {
+// Validates one Q/K/V quantizer call and returns the scratch bytes it needs
+// (the three tensors' partial maxima side by side, each run 256-byte aligned).
+static int qkv_plan(const void* q, const void* k, const void* v, int x_dtype, int64_t B,
+                    int64_t H, int64_t Sq, int64_t Skv, int64_t D, int64_t qsb, int64_t qsh,
+                    int64_t qss, int64_t ksb, int64_t ksh, int64_t kss, int64_t vsb, int64_t vsh,
+                    int64_t vss, int granularity, const float* dequant_out, const uint8_t* q8,
+                    const uint8_t* k8, const uint8_t* vt8, int64_t ldv, Plan* pq, Plan* pk,
+                    Plan* pv, size_t* off_k, size_t* off_v, size_t* need) {
   if (q == nullptr || k == nullptr || v == nullptr || dequant_out == nullptr || q8 == nullptr ||
       k8 == nullptr || vt8 == nullptr) {
     rp_set_error("scale_quantize_qkv: null pointer");
     return RP_ERR_INVALID_ARGUMENT;
   }
-  Plan pq, pk, pv;
-  int rc = make_plan(q, x_dtype, B, H, Sq, D, qsb, qsh, qss, granularity, &pq);
+  int rc = make_plan(q, x_dtype, B, H, Sq, D, qsb, qsh, qss, granularity, pq);
   if (rc) return rc;
-  if ((rc = make_plan(k, x_dtype, B, H, Skv, D, ksb, ksh, kss, granularity, &pk))) return rc;
-  if ((rc = make_plan(v, x_dtype, B, H, Skv, D, vsb, vsh, vss, granularity, &pv))) return rc;
+  if ((rc = make_plan(k, x_dtype, B, H, Skv, D, ksb, ksh, kss, granularity, pk))) return rc;
+  if ((rc = make_plan(v, x_dtype, B, H, Skv, D, vsb, vsh, vss, granularity, pv))) return rc;
   if (D % 32 != 0 || ldv < Skv || ldv % 128 != 0) {
     rp_set_error("scale_quantize_qkv: V^T needs D %% 32 == 0 and ldv >= Skv with ldv %% 128 == 0");
     return RP_ERR_UNSUPPORTED;
@@ -658,17 +660,20 @@ extern "C" int rp_fp8_scale_quantize_qkv(const void* q, const void* k, const voi
     rp_set_error("scale_quantize_qkv: B*H=%lld exceeds the grid limit", (long long)(B * H));
     return RP_ERR_UNSUPPORTED;
   }
-  // partial maxima of the three tensors side by side in the workspace
-  const size_t off_k = align256(pq.ws_bytes), off_v = off_k + align256(pk.ws_bytes);
-  const size_t need = off_v + pv.ws_bytes;
-  if (workspace == nullptr || workspace_bytes < need ||
-      reinterpret_cast<uintptr_t>(workspace) % 256 != 0) {
-    rp_set_error("scale_quantize_qkv: workspace of %zu bytes (256-byte aligned) needed, got %zu",
-                 need, workspace_bytes);
-    return RP_ERR_WORKSPACE;
-  }
+  *off_k = align256(pq->ws_bytes);
+  *off_v = *off_k + align256(pk->ws_bytes);
+  *need = *off_v + pv->ws_bytes;
+  return RP_OK;
+}
+
+// The four launches of one Q/K/V quantizer call, partial maxima in `ws`.
+static int qkv_launch(const Plan& pq, const Plan& pk, const Plan& pv, const void* v,
+                      int x_dtype, int64_t B, int64_t H, int64_t Skv, int64_t D, int64_t vsb,
+                      int64_t vsh, int64_t vss, float* dequant_out, uint8_t* q8, uint8_t* k8,
+                      uint8_t* vt8, int64_t ldv, uint8_t* ws, size_t off_k, size_t off_v,
+                      void* stream) {
+  int rc;
   const int64_t ng = pq.p.ngroups;
-  uint8_t* ws = static_cast<uint8_t*>(workspace);
   auto job = [&](const Plan& pl, size_t off, float* dq, uint8_t* codes) {
     QJob jb{};
     jb.p = pl.p;
@@ -710,6 +715,107 @@ extern "C" int rp_fp8_scale_quantize_qkv(const void* q, const void* k, const voi
   // V^T: its own grid shape
   return launch_apply(pv, v, B, H, Skv, D, vsb, vsh, vss, dequant_out + 2 * ng, vt8,
                       RP_LAYOUT_BHDS, ldv, st);
+}
+
+extern "C" int rp_fp8_scale_quantize_qkv(const void* q, const void* k, const void* v, int x_dtype,
+                                         int64_t B, int64_t H, int64_t Sq, int64_t Skv, int64_t D,
+                                         int64_t qsb, int64_t qsh, int64_t qss, int64_t ksb,
+                                         int64_t ksh, int64_t kss, int64_t vsb, int64_t vsh,
+                                         int64_t vss, int granularity, float* dequant_out,
+                                         uint8_t* q8, uint8_t* k8, uint8_t* vt8, int64_t ldv,
+                                         void* workspace, size_t workspace_bytes, void* stream) {
+  Plan pq, pk, pv;
+  size_t off_k, off_v, need;
+  int rc = qkv_plan(q, k, v, x_dtype, B, H, Sq, Skv, D, qsb, qsh, qss, ksb, ksh, kss, vsb, vsh,
+                    vss, granularity, dequant_out, q8, k8, vt8, ldv, &pq, &pk, &pv, &off_k,
+                    &off_v, &need);
+  if (rc) return rc;
+  if (workspace == nullptr || workspace_bytes < need ||
+      reinterpret_cast<uintptr_t>(workspace) % 256 != 0) {
+    rp_set_error("scale_quantize_qkv: workspace of %zu bytes (256-byte aligned) needed, got %zu",
+                 need, workspace_bytes);
+    return RP_ERR_WORKSPACE;
+  }
+  return qkv_launch(pq, pk, pv, v, x_dtype, B, H, Skv, D, vsb, vsh, vss, dequant_out, q8, k8,
+                    vt8, ldv, static_cast<uint8_t*>(workspace), off_k, off_v, stream);
+}
+
+// ------------------------------------------------ allocation-free variant
+// The partial maxima of rp_fp8_scale_quantize_qkv_noalloc live in this
+// file-scope device array: each GPU the library runs on holds its own copy
+// until the process ends.  Host code never passes the symbol itself to a
+// kernel (on the host it names a stand-in, not device memory); it passes the
+// device address hipGetSymbolAddress returns for the device in use, looked
+// up once per device.  Every partial is written by the amax pass before the
+// finalize pass reads it, so nothing needs clearing between calls.
+static __device__ __align__(256) uint8_t scratch[RP_QKV_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+uint8_t* g_scratch_ptr[kMaxDevices];  // device address of `scratch`, per device
+
+// Device address of `scratch` on the device that runs `stream`, looked up on
+// the first call for that device (with that device current).
+int scratch_for_stream(hipStream_t st, uint8_t** out) {
+  int dev = -1;
+  hipError_t e = st != nullptr ? hipStreamGetDevice(st, &dev) : hipGetDevice(&dev);
+  if (e != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    rp_set_error("scale_quantize_qkv_noalloc: cannot tell the stream's device (%s)",
+                 hipGetErrorString(e));
+    return RP_ERR_INVALID_ARGUMENT;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    int cur = -1;
+    if ((e = hipGetDevice(&cur)) != hipSuccess) {
+      rp_set_error("scale_quantize_qkv_noalloc: hipGetDevice: %s", hipGetErrorString(e));
+      return RP_ERR_LAUNCH;
+    }
+    if (cur != dev && (e = hipSetDevice(dev)) != hipSuccess) {
+      rp_set_error("scale_quantize_qkv_noalloc: hipSetDevice(%d): %s", dev, hipGetErrorString(e));
+      return RP_ERR_LAUNCH;
+    }
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (cur != dev) (void)hipSetDevice(cur);
+    if (e != hipSuccess || ptr == nullptr) {
+      rp_set_error("scale_quantize_qkv_noalloc: hipGetSymbolAddress(scratch) on device %d: %s",
+                   dev, hipGetErrorString(e));
+      return RP_ERR_LAUNCH;
+    }
+    g_scratch_ptr[dev] = static_cast<uint8_t*>(ptr);
+  }
+  *out = g_scratch_ptr[dev];
+  return RP_OK;
+}
+}  // namespace
+
+extern "C" int rp_fp8_scale_quantize_qkv_noalloc(const void* q, const void* k, const void* v,
+                                                 int x_dtype, int64_t B, int64_t H, int64_t Sq,
+                                                 int64_t Skv, int64_t D, int64_t qsb, int64_t qsh,
+                                                 int64_t qss, int64_t ksb, int64_t ksh,
+                                                 int64_t kss, int64_t vsb, int64_t vsh,
+                                                 int64_t vss, int granularity, float* dequant_out,
+                                                 uint8_t* q8, uint8_t* k8, uint8_t* vt8,
+                                                 int64_t ldv, void* stream) {
+  Plan pq, pk, pv;
+  size_t off_k, off_v, need;
+  int rc = qkv_plan(q, k, v, x_dtype, B, H, Sq, Skv, D, qsb, qsh, qss, ksb, ksh, kss, vsb, vsh,
+                    vss, granularity, dequant_out, q8, k8, vt8, ldv, &pq, &pk, &pv, &off_k,
+                    &off_v, &need);
+  if (rc) return rc;
+  if (need > RP_QKV_NOALLOC_SCRATCH_BYTES) {
+    rp_set_error("scale_quantize_qkv_noalloc: these shapes need %zu bytes of scratch, more than "
+                 "the %u this entry point holds; use rp_fp8_scale_quantize_qkv with a workspace",
+                 need, (unsigned)RP_QKV_NOALLOC_SCRATCH_BYTES);
+    return RP_ERR_WORKSPACE;
+  }
+  uint8_t* ws = nullptr;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if ((rc = scratch_for_stream(st, &ws))) return rc;
+  return qkv_launch(pq, pk, pv, v, x_dtype, B, H, Skv, D, vsb, vsh, vss, dequant_out, q8, k8,
+                    vt8, ldv, ws, off_k, off_v, stream);
 }
 
 extern "C" int rp_selftest_e4m3(const float* x, uint8_t* out, int64_t n, void* stream) {
