@@ -297,7 +297,12 @@ def bench_gemm(args, cfg) -> dict:
 
     dev = torch.device("cuda", 0)
     a, w = gemm_inputs(cfg, device=dev)
-    sw, wt8 = ops.fp8_linear_weight(w)   # weights quantized once, like a loaded layer
+    # weights quantized once, like a loaded layer, in both B layouts: (K, N) as
+    # the reference's fp8_gemm takes B, and (N, K) as nn.Linear stores it
+    sw, wt8 = ops.fp8_linear_weight(w, layout="nk")
+    _, w8 = ops.fp8_linear_weight(w, layout="kn")
+    kn = args.b_layout == "kn"
+    b_main, b_other = (w8, wt8) if kn else (wt8, w8)
     out = torch.empty((cfg.M, cfg.N), dtype=torch.bfloat16, device=dev)
     st = torch.cuda.current_stream(dev)
 
@@ -307,7 +312,7 @@ def bench_gemm(args, cfg) -> dict:
         sa, a8 = ops.scale_quantize(a, "tensor", "bhsd")
         if ev is not None:
             ev[1].record(st)
-        ops.fp8_gemm(a8.view(torch.uint8), wt8, sa, sw, b_transposed=True, out=out)
+        ops.fp8_gemm(a8.view(torch.uint8), b_main, sa, sw, b_transposed=not kn, out=out)
         if ev is not None:
             ev[2].record(st)
 
@@ -322,6 +327,23 @@ def bench_gemm(args, cfg) -> dict:
     gemm_ms = sum(e[1].elapsed_time(e[2]) for e in evs) / len(evs)
     quant_ms = sum(e[0].elapsed_time(e[1]) for e in evs) / len(evs)
     tf = cfg.flops / (gemm_ms * 1e-3) / 1e12
+    # the other B layout on the same codes: same kernel family, same output bits
+    sa, a8 = ops.scale_quantize(a, "tensor", "bhsd")
+    a8 = a8.view(torch.uint8)
+    other = torch.empty_like(out)
+    run_other = lambda: ops.fp8_gemm(a8, b_other, sa, sw, b_transposed=kn, out=other)
+    for _ in range(args.warmup):
+        run_other()
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0.record(st)
+    for _ in range(args.steps):
+        run_other()
+    t1.record(st)
+    torch.cuda.synchronize()
+    other_ms = t0.elapsed_time(t1) / args.steps
+    ops.fp8_gemm(a8, b_main, sa, sw, b_transposed=not kn, out=out)
+    same = bool(torch.equal(out, other))
     library = _library_gemm(args, cfg, a, wt8, sw, out) if args.library_gemm else None
     return {
         "metric": "FP8 scaled GEMM TFLOP/s (Wan FFN up-projection)",
@@ -330,7 +352,8 @@ def bench_gemm(args, cfg) -> dict:
         "ms_per_step": round(step_ms, 4), "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "fp8_e4m3fn (fp32 accumulate, bf16 out)",
         "data": "synthetic: seeded A ~ N(0,1), W ~ N(0,0.02) bf16",
-        "config": {"workload": cfg.name, "M": cfg.M, "K": cfg.K, "N": cfg.N},
+        "config": {"workload": cfg.name, "M": cfg.M, "K": cfg.K, "N": cfg.N,
+                   "b_layout": "(K, N) row-major" if kn else "(N, K)"},
         "roofline": {"bound": "mfma", "achieved": round(tf, 2), "peak": FP8_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(tf / FP8_PEAK_TFLOPS, 4),
                      "traffic": _traffic_from_profiles("gemm256_kernel", cfg.name),
@@ -338,6 +361,10 @@ def bench_gemm(args, cfg) -> dict:
                      "kernel": "gemm256_kernel", "kernel_ms": round(gemm_ms, 4)},
         "quantize": {"ms": round(quant_ms, 4),
                      "achieved_GBps": round(5 * cfg.M * cfg.K / (quant_ms * 1e-3) / 1e9, 1)},
+        "other_b_layout": {"b_layout": "(N, K)" if kn else "(K, N) row-major",
+                           "kernel_ms": round(other_ms, 4),
+                           "TFLOPs": round(cfg.flops / (other_ms * 1e-3) / 1e12, 2),
+                           "bit_identical_output": same},
         **({"library_gemm": library} if library else {}),
     }
 
@@ -394,6 +421,9 @@ def main() -> int:
     ap.add_argument("--granularity", choices=("tensor", "bh"), default="tensor",
                     help="attention configs: scale groups -- per tensor (BASELINE's configs) "
                          "or per (b, h) (the reference wrapper's)")
+    ap.add_argument("--b-layout", choices=("kn", "nk"), default="kn",
+                    help="c4_wan_ffn_up: the weight operand as the reference's fp8_gemm takes B, "
+                         "(K, N) row-major (kn), or transposed (nk); the other is timed beside it")
     ap.add_argument("--cpu-budget", type=float, default=12.0,
                     help="seconds of CPU work for the cpu_baseline sample (0 disables)")
     args = ap.parse_args()

@@ -65,7 +65,7 @@ extern "C" {
                                 /* q sees suffix key j = kv - prefix iff          */
                                 /* j / suffix == q / suffix and j <= q            */
 
-/* 2: the quantizer entry points take x_dtype; RP_OUT_F16. */
+/* 3: rp_fp8_gemm / rp_fp8_linear take b_layout (RP_B_KN or RP_B_NK). */
 int rp_abi_version(void);
 const char* rp_status_string(int status);
 const char* rp_last_error(void);
@@ -235,14 +235,23 @@ int rp_fp8_rmsnorm_scale_quantize(const void* x, int64_t B, int64_t H, int64_t S
 /* --------------------------------------------------------------- GEMM
  * C (M, N) bf16 = bf16( fp32(A8 . B8) * (a_scale * b_scale) ).
  * Replaces fp8_gemm_launch, kernels/hip/fp8_attn/fp8_gemm.hip:162-179
- * (kernel :79-156), with B supplied K-contiguous: bt8 is B transposed,
- * (N, K) with row stride ldb.  A8 (M, K) row stride lda; C row stride ldc.
+ * (kernel :79-156).  A8 (M, K) row-major, row stride lda; C row stride ldc.
+ * B8 in either layout (b_layout):
+ *   RP_B_KN  (K, N) row-major, row stride ldb >= N -- the reference's B
+ *            (binding.cpp:25-57 passes B as (K, N) contiguous), staged into
+ *            LDS as it lies and transposed by the LDS reads: no extra pass
+ *   RP_B_NK  B transposed, (N, K) rows of stride ldb >= K: the nn.Linear
+ *            weight layout
  * a_scale_dev / b_scale_dev: optional device pointers to the fp32 scales
  * (e.g. produced by rp_fp8_scale with RP_SCALE_PER_TENSOR); when non-NULL
  * they are used instead of the host values, avoiding a device->host read.
- * K, lda, ldb multiples of 16; N, ldc multiples of 4; a8 and bt8 16-byte
- * aligned, c 8-byte aligned. */
-int rp_fp8_gemm(const uint8_t* a8, const uint8_t* bt8, void* c,
+ * K, lda multiples of 16; N, ldc multiples of 4; a8 16-byte aligned, c
+ * 8-byte aligned; RP_B_NK also needs ldb % 16 == 0 and b8 16-byte aligned.
+ * Fastest path: K % 64 == 0 (and for RP_B_KN, N and ldb multiples of 16,
+ * b8 16-byte aligned); other shapes run a general kernel. */
+#define RP_B_NK 0
+#define RP_B_KN 1
+int rp_fp8_gemm(const uint8_t* a8, const uint8_t* b8, int b_layout, void* c,
                 int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldb, int64_t ldc,
                 float a_scale, float b_scale, const float* a_scale_dev,
                 const float* b_scale_dev, void* stream);
@@ -254,12 +263,14 @@ int rp_fp8_gemm(const uint8_t* a8, const uint8_t* bt8, void* c,
  * (kernels/hip/fp8_attn/fp8_gemm.hip has no bias); it serves the FP8 linear
  * layers that replace nn.Linear in the module-swap pattern of
  * src/repercep/runtime/quantize.py:135-179. */
-int rp_fp8_linear(const uint8_t* a8, const uint8_t* bt8, const void* bias, void* c, int64_t M,
-                  int64_t N, int64_t K, int64_t lda, int64_t ldb, int64_t ldc, float a_scale,
-                  float b_scale, const float* a_scale_dev, const float* b_scale_dev, void* stream);
+int rp_fp8_linear(const uint8_t* a8, const uint8_t* b8, int b_layout, const void* bias, void* c,
+                  int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldb, int64_t ldc,
+                  float a_scale, float b_scale, const float* a_scale_dev,
+                  const float* b_scale_dev, void* stream);
 
-/* FP8 byte transpose: dst (C, R) <- src (R, C); row strides lds, ldd.
- * Turns the reference GEMM's row-major B (K, N) into the (N, K) operand. */
+/* FP8 byte transpose: dst (C, R) <- src (R, C); row strides lds, ldd.  No
+ * counterpart in the reference; turns a (K, N) weight into the (N, K)
+ * nn.Linear layout once, for layers stored that way. */
 int rp_fp8_transpose(const uint8_t* src, uint8_t* dst, int64_t R, int64_t C,
                      int64_t lds, int64_t ldd, void* stream);
 

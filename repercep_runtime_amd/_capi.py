@@ -31,6 +31,8 @@ RP_ROPE_NONE = 0
 RP_ROPE_HALF = 1
 RP_ROPE_INTERLEAVED = 2
 RP_QKV_NOALLOC_SCRATCH_BYTES = 1 << 20
+RP_B_NK = 0
+RP_B_KN = 1
 
 #: Every function include/repercep_fp8.h declares.
 EXPORTS = (
@@ -105,11 +107,11 @@ def _declare(L: ctypes.CDLL) -> None:
                                                 _vp, _f32, _vp, _vp, _int, _int, _vp, _vp, _vp,
                                                 _sz, _vp]
     L.rp_fp8_gemm.restype = _int
-    L.rp_fp8_gemm.argtypes = [_vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _f32, _f32,
-                              _vp, _vp, _vp]
+    L.rp_fp8_gemm.argtypes = [_vp, _vp, _int, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _f32,
+                              _f32, _vp, _vp, _vp]
     L.rp_fp8_linear.restype = _int
-    L.rp_fp8_linear.argtypes = [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _f32,
-                                _f32, _vp, _vp, _vp]
+    L.rp_fp8_linear.argtypes = [_vp, _vp, _int, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64,
+                                _f32, _f32, _vp, _vp, _vp]
     L.rp_fp8_transpose.restype = _int
     L.rp_fp8_transpose.argtypes = [_vp, _vp, _i64, _i64, _i64, _i64, _vp]
     L.rp_selftest_e4m3.restype = _int

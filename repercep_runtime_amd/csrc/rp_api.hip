@@ -17,7 +17,7 @@ extern "C" void rp_set_error(const char* fmt, ...) {
 
 extern "C" const char* rp_last_error(void) { return g_last_error; }
 
-extern "C" int rp_abi_version(void) { return 2; }
+extern "C" int rp_abi_version(void) { return 3; }
 
 extern "C" const char* rp_status_string(int status) {
   switch (status) {

@@ -4,19 +4,25 @@
 // (fp32 accumulation, the product of the two scales applied once to the
 // accumulator, round-to-nearest-even bf16 output), on OCP e4m3fn operands.
 // The reference kernel is one wave per 16x16 tile with strided operand
-// gathers and no LDS.  Here both operands are K-contiguous rows (A8 (M, K),
-// B8 transposed (N, K)), so every MFMA operand is 32 contiguous bytes per
+// gathers and no LDS.  Here every MFMA operand is 32 K-contiguous bytes per
 // lane, and the MFMA computes C^T tiles (A operand = rows of B^T, B operand
 // = rows of A): the accumulator gives each lane 4 consecutive output columns
-// of one row, stored as one 8-byte write.  Two kernels:
+// of one row, stored as one 8-byte write.  B comes in either layout:
+// transposed, (N, K) rows (RP_B_NK: K-contiguous like A), or as the
+// reference takes it, (K, N) row-major (RP_B_KN).  A (K, N) slice is staged
+// in LDS as it lies in memory -- K rows of N bytes -- and the B^T operand is
+// read from it with ds_read_b64_tr_b8, the gfx950 LDS transpose read (see
+// kn_operand), so neither layout costs a transpose pass.  Two kernels:
 //
 // * gemm256_kernel (K a multiple of 64, the production shapes): 256 x 256
 //   block tiles on v_mfma_f32_32x32x64_f8f6f4, four waves of 128 x 128 with
 //   their accumulators in AGPRs, operands streamed into two LDS stages of
 //   128-byte K slices by direct-to-LDS loads one slice ahead.
-// * gemm_kernel (any K multiple of 16): 256 x 128 block tiles on
-//   v_mfma_f32_16x16x128_f8f6f4, operands staged through VGPRs into a
-//   double-buffered, XOR-swizzled LDS tile, K tail zero-filled.
+// * gemm_kernel (any K multiple of 16, any (K, N) B): 256 x 128 block tiles
+//   on v_mfma_f32_16x16x128_f8f6f4, operands staged through VGPRs into a
+//   double-buffered, XOR-swizzled LDS tile, K tail zero-filled; a (K, N) B
+//   is gathered byte by byte (the fallback for shapes the large-tile kernel
+//   does not take).
 //
 // Both remap workgroups so that those resident on one XCD cover a compact
 // patch of C and share operand rows in that XCD's L2.
@@ -41,6 +47,7 @@ struct GemmArgs {
   const float* a_dev;
   const float* b_dev;
   int tiles_m, tiles_n;
+  int b_kn;   // 1: B is (K, N) row-major, row stride ldb (RP_B_KN)
 };
 
 // Bias values of the 4 columns n..n+3 (bf16 pairs), or zeros past N.  Every
@@ -85,7 +92,21 @@ struct GGeo {
   static constexpr int B_LOADS = B_BYTES / 16 / kGThreads;
 };
 
-template <int BM, int BN>
+// Chunk ci of a B^T tile: row r (an N row of the tile), 16-byte K granule c.
+// For a (K, N) B the 128 rows of a chunk group are consecutive lanes, so the
+// byte gathers of one wave read consecutive N columns of each K row.
+template <int BN, bool KN>
+__device__ __forceinline__ void b_chunk(int ci, int& r, int& c) {
+  if constexpr (KN) {
+    r = ci % BN;
+    c = ci / BN;
+  } else {
+    r = ci >> 3;
+    c = ci & 7;
+  }
+}
+
+template <int BM, int BN, bool KN>
 __device__ __forceinline__ void gemm_load(const GemmArgs& g, int64_t m0, int64_t n0, int64_t k0,
                                           int tid, i32x4 (&sa)[GGeo<BM, BN>::A_LOADS],
                                           i32x4 (&sb)[GGeo<BM, BN>::B_LOADS]) {
@@ -102,15 +123,25 @@ __device__ __forceinline__ void gemm_load(const GemmArgs& g, int64_t m0, int64_t
 #pragma unroll
   for (int n = 0; n < G::B_LOADS; ++n) {
     const int ci = tid + kGThreads * n;
-    const int r = ci >> 3, c = ci & 7;
+    int r, c;
+    b_chunk<BN, KN>(ci, r, c);
     const int64_t row = min(n0 + r, g.N - 1);
     const int64_t k = k0 + c * 16;
-    sb[n] = k < g.K ? *reinterpret_cast<const i32x4*>(g.bt + row * g.ldb + k)
-                    : i32x4{0, 0, 0, 0};
+    if constexpr (KN) {
+      // column `row` of B, K rows k .. k+15 (zero past K), one byte each
+      uint32_t w[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+      for (int e = 0; e < 16; ++e)
+        if (k + e < g.K) w[e >> 2] |= (uint32_t)g.bt[(k + e) * g.ldb + row] << (8 * (e & 3));
+      sb[n] = i32x4{(int)w[0], (int)w[1], (int)w[2], (int)w[3]};
+    } else {
+      sb[n] = k < g.K ? *reinterpret_cast<const i32x4*>(g.bt + row * g.ldb + k)
+                      : i32x4{0, 0, 0, 0};
+    }
   }
 }
 
-template <int BM, int BN>
+template <int BM, int BN, bool KN>
 __device__ __forceinline__ void gemm_store(uint8_t* st, int tid,
                                            const i32x4 (&sa)[GGeo<BM, BN>::A_LOADS],
                                            const i32x4 (&sb)[GGeo<BM, BN>::B_LOADS]) {
@@ -125,7 +156,8 @@ __device__ __forceinline__ void gemm_store(uint8_t* st, int tid,
 #pragma unroll
   for (int n = 0; n < G::B_LOADS; ++n) {
     const int ci = tid + kGThreads * n;
-    const int r = ci >> 3, c = ci & 7;
+    int r, c;
+    b_chunk<BN, KN>(ci, r, c);
     *reinterpret_cast<i32x4*>(bl + r * kKStep + ((c ^ (r & 7)) << 4)) = sb[n];
   }
 }
@@ -137,7 +169,7 @@ __device__ __forceinline__ i32x8 lds_operand(const uint8_t* tile, int row, int l
               *reinterpret_cast<const i32x4*>(p + (((2 * lg + 1) ^ sw) << 4)));
 }
 
-template <int BM, int BN>
+template <int BM, int BN, bool KN>
 __global__ __launch_bounds__(kGThreads) __attribute__((amdgpu_waves_per_eu(1, 2)))
 void gemm_kernel(GemmArgs g) {
   using G = GGeo<BM, BN>;
@@ -174,14 +206,14 @@ void gemm_kernel(GemmArgs g) {
   i32x4 sa[G::A_LOADS];
   i32x4 sb[G::B_LOADS];
   const int nk = (int)((g.K + kKStep - 1) / kKStep);
-  gemm_load<BM, BN>(g, m0, n0, 0, tid, sa, sb);
-  gemm_store<BM, BN>(smem, tid, sa, sb);
+  gemm_load<BM, BN, KN>(g, m0, n0, 0, tid, sa, sb);
+  gemm_store<BM, BN, KN>(smem, tid, sa, sb);
   __syncthreads();
 
   for (int kk = 0; kk < nk; ++kk) {
     const int st = kk & 1;
     const bool more = kk + 1 < nk;
-    if (more) gemm_load<BM, BN>(g, m0, n0, (int64_t)(kk + 1) * kKStep, tid, sa, sb);
+    if (more) gemm_load<BM, BN, KN>(g, m0, n0, (int64_t)(kk + 1) * kKStep, tid, sa, sb);
     const uint8_t* al = smem + st * G::STAGE;
     const uint8_t* bl = al + G::A_BYTES;
     i32x8 bop[G::TN];
@@ -193,7 +225,7 @@ void gemm_kernel(GemmArgs g) {
 #pragma unroll
       for (int j = 0; j < G::TN; ++j) acc[j][i] = mfma_16x16x128(bop[j], aop, acc[j][i]);
     }
-    if (more) gemm_store<BM, BN>(smem + (st ^ 1) * G::STAGE, tid, sa, sb);
+    if (more) gemm_store<BM, BN, KN>(smem + (st ^ 1) * G::STAGE, tid, sa, sb);
     __syncthreads();
   }
 
@@ -301,6 +333,33 @@ struct G2Ops {
   i32x8 a[4], b[4];
 };
 
+typedef int i32x2 __attribute__((ext_vector_type(2)));
+
+// ds_read_b64_tr_b8: each group of 16 lanes reads an 8 x 16 byte block --
+// lane i supplies the address of bytes 8(i%2) .. 8(i%2)+7 of row i/2 -- and
+// lane i receives column i of it: byte j from row j.  (Measured on gfx950:
+// lane l, byte j <- lane 16(l/16) + 2j + (l%16)/8, byte l%8.)
+__device__ __forceinline__ i32x2 lds_tr8(uint32_t lds_addr) {
+  typedef __attribute__((address_space(3))) i32x2* lds_i32x2_p;
+  return __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_i32x2_p)(uintptr_t)lds_addr);
+}
+
+// B^T operand from a (K, N) slice in LDS (RP_B_KN).  Slice rows are K (256
+// bytes of N each); the 16 N granules of row r sit at slots g ^ 2(r & 7).
+// Lane l needs N column n = l % 32 of its 32-row block and K bytes
+// 32(l / 32) .. +31 of the sub-slice: four transpose reads of 8 K rows each.
+// Lane i of a 16-lane group points at row k8 + i/2 (k8 a multiple of 8, so
+// r & 7 = i/2), granule g of columns 16((l / 16) % 2) .. +15 of the block, byte
+// 8(i % 2): `base` carries the per-lane part, the rest is immediate.  The
+// slots g ^ {0, 2, .., 14} of one group's eight rows and g+1 ^ {...} of its
+// neighbour cover all sixteen 16-byte bank groups once: conflict-free.
+__device__ __forceinline__ i32x8 kn_operand(uint32_t base) {
+  const i32x2 r0 = lds_tr8(base), r1 = lds_tr8(base + 8 * kG2Tile);
+  const i32x2 r2 = lds_tr8(base + 16 * kG2Tile), r3 = lds_tr8(base + 24 * kG2Tile);
+  return i32x8{r0.x, r0.y, r1.x, r1.y, r2.x, r2.y, r3.x, r3.y};
+}
+
+template <bool KN>
 __global__ __launch_bounds__(kG2Threads) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void gemm256_kernel(GemmArgs g) {
   __shared__ __attribute__((aligned(1024))) uint8_t smem[kG2Stages * kG2Stage];
@@ -332,18 +391,29 @@ void gemm256_kernel(GemmArgs g) {
   const int wm = wave >> 1, wn = wave & 1;
 
   // This lane's direct-to-LDS loads: load n fills LDS KiB block n*4 + wave
-  // of a stage; blocks [0, kG2Half/1024) hold A rows, the rest B^T rows.
-  // Eight consecutive lanes read one row's 128-byte K slice (a whole cache
-  // line).  LDS granule `slot` of row r holds K granule slot ^ ((r >> 1) & 7).
-  // Rows past M or N re-read the last row (their results are not stored).
+  // of a stage; blocks [0, kG2Half/1024) hold A rows, the rest B.
+  // A and (N, K) B^T: eight consecutive lanes read one row's 128-byte K slice
+  // (a whole cache line); LDS granule `slot` of row r holds K granule
+  // slot ^ ((r >> 1) & 7).  Rows past M or N re-read the last row (their
+  // results are not stored).
+  // (K, N) B: sixteen consecutive lanes read one K row's 256 N bytes of the
+  // tile; LDS granule `slot` of row r holds N granule slot ^ 2(r & 7), and
+  // granules past N re-read the last one inside N (N % 16 == 0).
   const uint8_t* abase = g.a + m0 * g.lda;
-  const uint8_t* bbase = g.bt + n0 * g.ldb;
+  const uint8_t* bbase = KN ? g.bt + n0 : g.bt + n0 * g.ldb;
   uint32_t gofs[kG2Loads];
 #pragma unroll
   for (int n = 0; n < kG2Loads; ++n) {
     const int blk = n * 4 + wave;
     const bool is_a = n < kG2ALoads;
     const int p = (is_a ? blk : blk - kG2Half / 1024) * kWave + lane;
+    if (KN && !is_a) {
+      const int row = p >> 4, slot = p & 15;
+      const int last = (int)min((g.N - n0) >> 4, (int64_t)16) - 1;
+      const int gran = min(slot ^ (2 * (row & 7)), last);
+      gofs[n] = (uint32_t)((int64_t)row * g.ldb + gran * 16);
+      continue;
+    }
     const int row = p >> 3, slot = p & 7;
     const int s16 = (slot ^ ((row >> 1) & 7)) * 16;
     if (is_a) {
@@ -355,18 +425,26 @@ void gemm256_kernel(GemmArgs g) {
     }
   }
   // K in 64-byte sub-slices; slices are pairs of them.  With K % 128 == 64
-  // the last slice is a half: its lanes for K granules 4..7 re-read granules
-  // 0..3 (in bounds), and the sub-slice they fill is never used.
+  // the last slice is a half: the lanes that would fill its second sub-slice
+  // re-read in-bounds bytes of the first (K granules 0..3 of the row for A
+  // and B^T, K rows 0..63 for a (K, N) B), and that sub-slice is never used.
   const int nsub = (int)(g.K / kG2Sub);
   const int nslice = (nsub + 1) >> 1;
   const int half_tail = nsub & 1;
   // bit 2 of this lane's K granule is (slot bit 2) ^ (block parity), and a
   // block's parity is the wave's: the same for all of its loads
   const uint32_t tail_back = (uint32_t)(((lane >> 2) ^ wave) & 1) * 64;
+  // (K, N) B: loads n >= kG2ALoads + 4 fill K rows 64..127 of the slice
+  const uint32_t tail_back_kn = (uint32_t)(64 * g.ldb);
   auto issue = [&](int n, int kk) __attribute__((always_inline)) {
     uint32_t off = gofs[n];
-    if (half_tail && kk == nslice - 1) off -= tail_back;
-    const uint8_t* src = (n < kG2ALoads ? abase : bbase) + (int64_t)kk * kG2K;
+    const bool is_a = n < kG2ALoads;
+    if (half_tail && kk == nslice - 1) {
+      if (KN && !is_a) off -= n >= kG2ALoads + 4 ? tail_back_kn : 0u;
+      else off -= tail_back;
+    }
+    const uint8_t* src = is_a ? abase + (int64_t)kk * kG2K
+                              : bbase + (int64_t)kk * kG2K * (KN ? g.ldb : 1);
     g2_gload_lds16_s(src, off,
                      smem_lds + (uint32_t)((kk & 1) * kG2Stage + (n * 4 + wave) * 1024));
   };
@@ -381,6 +459,26 @@ void gemm256_kernel(GemmArgs g) {
   const int h10 = ((4 + 2 * lg) ^ swz) * 16, h11 = ((4 + 2 * lg + 1) ^ swz) * 16;
   const int a_off = (wm * 128 + lq) * kG2Pitch;
   const int b_off = kG2Half + (wn * 128 + lq) * kG2Pitch;
+  // (K, N) B: per-lane LDS offsets of the four B^T operands' transpose reads
+  // (see kn_operand); sub-slice h adds 64 K rows, an immediate
+  uint32_t kn_off[4];
+  {
+    const int i = lane & 15;
+    const int row = 32 * lg + (i >> 1);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int gr = 8 * wn + 2 * j + ((lane >> 4) & 1);
+      kn_off[j] = (uint32_t)(kG2Half + row * kG2Tile + ((gr ^ (i & 14)) << 4) + 8 * (i & 1));
+    }
+  }
+  auto b_op = [&](const uint8_t* st, int j, int h, int c0, int c1) __attribute__((always_inline)) {
+    if constexpr (KN) {
+      const uint32_t st_lds = smem_lds + (uint32_t)(st - smem);
+      return kn_operand(st_lds + kn_off[j] + (uint32_t)(64 * h * kG2Tile));
+    } else {
+      return g2_op(st + b_off + 32 * j * kG2Pitch, c0, c1);
+    }
+  };
 
   f32x16 acc[4][4];
 #pragma unroll
@@ -403,7 +501,7 @@ void gemm256_kernel(GemmArgs g) {
 #pragma unroll
   for (int i = 0; i < 4; ++i) o0.a[i] = g2_op(smem + a_off + 32 * i * kG2Pitch, h00, h01);
 #pragma unroll
-  for (int j = 0; j < 4; ++j) o0.b[j] = g2_op(smem + b_off + 32 * j * kG2Pitch, h00, h01);
+  for (int j = 0; j < 4; ++j) o0.b[j] = b_op(smem, j, 0, h00, h01);
 
   // Sub-step (kk, H): 16 MFMAs on `cur` (sub-slice 2kk + H) with the operand
   // reads of the next sub-slice into `nxt` spread between them.  Sub-step
@@ -430,7 +528,7 @@ void gemm256_kernel(GemmArgs g) {
       if ((t & 1) == 0 && more) {
         const int v = t >> 2;
         if ((t & 2) == 0) nxt.a[v] = g2_op(st + a_off + 32 * v * kG2Pitch, r0, r1);
-        else nxt.b[v] = g2_op(st + b_off + 32 * v * kG2Pitch, r0, r1);
+        else nxt.b[v] = b_op(st, v, H == 0 ? 1 : 0, r0, r1);
       }
     }
   };
@@ -481,7 +579,10 @@ int launch_gemm256(GemmArgs g, hipStream_t st) {
     rp_set_error("gemm: grid too large");
     return RP_ERR_UNSUPPORTED;
   }
-  hipLaunchKernelGGL(gemm256_kernel, dim3((unsigned)nwork), dim3(kG2Threads), 0, st, g);
+  if (g.b_kn)
+    hipLaunchKernelGGL(gemm256_kernel<true>, dim3((unsigned)nwork), dim3(kG2Threads), 0, st, g);
+  else
+    hipLaunchKernelGGL(gemm256_kernel<false>, dim3((unsigned)nwork), dim3(kG2Threads), 0, st, g);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) {
     rp_set_error("gemm: launch failed: %s", hipGetErrorString(e));
@@ -516,7 +617,12 @@ int launch_gemm(GemmArgs g, hipStream_t st) {
     rp_set_error("gemm: grid too large");
     return RP_ERR_UNSUPPORTED;
   }
-  hipLaunchKernelGGL((gemm_kernel<BM, BN>), dim3((unsigned)nwork), dim3(kGThreads), 0, st, g);
+  if (g.b_kn)
+    hipLaunchKernelGGL((gemm_kernel<BM, BN, true>), dim3((unsigned)nwork), dim3(kGThreads), 0, st,
+                       g);
+  else
+    hipLaunchKernelGGL((gemm_kernel<BM, BN, false>), dim3((unsigned)nwork), dim3(kGThreads), 0,
+                       st, g);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) {
     rp_set_error("gemm: launch failed: %s", hipGetErrorString(e));
@@ -530,27 +636,34 @@ int launch_gemm(GemmArgs g, hipStream_t st) {
 
 using namespace rp;
 
-static int gemm_run(const uint8_t* a8, const uint8_t* bt8, const void* bias, void* c, int64_t M,
-                    int64_t N, int64_t K, int64_t lda, int64_t ldb, int64_t ldc, float a_scale,
-                    float b_scale, const float* a_scale_dev, const float* b_scale_dev,
-                    void* stream) {
-  if (!a8 || !bt8 || !c) {
+static int gemm_run(const uint8_t* a8, const uint8_t* b8, int b_layout, const void* bias,
+                    void* c, int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldb,
+                    int64_t ldc, float a_scale, float b_scale, const float* a_scale_dev,
+                    const float* b_scale_dev, void* stream) {
+  if (!a8 || !b8 || !c) {
     rp_set_error("gemm: null pointer");
     return RP_ERR_INVALID_ARGUMENT;
   }
-  if (M <= 0 || N <= 0 || K <= 0 || lda < K || ldb < K || ldc < N) {
-    rp_set_error("gemm: bad sizes M=%lld N=%lld K=%lld lda=%lld ldb=%lld ldc=%lld",
-                 (long long)M, (long long)N, (long long)K, (long long)lda, (long long)ldb,
-                 (long long)ldc);
+  if (b_layout != RP_B_NK && b_layout != RP_B_KN) {
+    rp_set_error("gemm: unknown B layout %d", b_layout);
     return RP_ERR_INVALID_ARGUMENT;
   }
-  if (K % 16 != 0 || lda % 16 != 0 || ldb % 16 != 0 || N % 4 != 0 || ldc % 4 != 0) {
-    rp_set_error("gemm: needs K, lda, ldb multiples of 16 and N, ldc multiples of 4");
+  const bool kn = b_layout == RP_B_KN;
+  if (M <= 0 || N <= 0 || K <= 0 || lda < K || ldb < (kn ? N : K) || ldc < N) {
+    rp_set_error("gemm: bad sizes M=%lld N=%lld K=%lld lda=%lld ldb=%lld ldc=%lld (B %s)",
+                 (long long)M, (long long)N, (long long)K, (long long)lda, (long long)ldb,
+                 (long long)ldc, kn ? "(K, N)" : "(N, K)");
+    return RP_ERR_INVALID_ARGUMENT;
+  }
+  if (K % 16 != 0 || lda % 16 != 0 || N % 4 != 0 || ldc % 4 != 0 || (!kn && ldb % 16 != 0)) {
+    rp_set_error("gemm: needs K, lda multiples of 16, N, ldc multiples of 4, and for an (N, K) "
+                 "B, ldb a multiple of 16");
     return RP_ERR_UNSUPPORTED;
   }
-  if ((reinterpret_cast<uintptr_t>(a8) | reinterpret_cast<uintptr_t>(bt8)) % 16 != 0 ||
+  if (reinterpret_cast<uintptr_t>(a8) % 16 != 0 ||
+      (!kn && reinterpret_cast<uintptr_t>(b8) % 16 != 0) ||
       reinterpret_cast<uintptr_t>(c) % 8 != 0) {
-    rp_set_error("gemm: operands must be 16-byte aligned and C 8-byte aligned");
+    rp_set_error("gemm: A (and an (N, K) B) must be 16-byte aligned and C 8-byte aligned");
     return RP_ERR_UNSUPPORTED;
   }
   if (bias != nullptr && reinterpret_cast<uintptr_t>(bias) % 8 != 0) {
@@ -558,32 +671,35 @@ static int gemm_run(const uint8_t* a8, const uint8_t* bt8, const void* bias, voi
     return RP_ERR_UNSUPPORTED;
   }
   GemmArgs g{};
-  g.a = a8; g.bt = bt8; g.c = static_cast<uint16_t*>(c);
+  g.a = a8; g.bt = b8; g.c = static_cast<uint16_t*>(c);
   g.bias = static_cast<const uint16_t*>(bias);
   g.M = M; g.N = N; g.K = K; g.lda = lda; g.ldb = ldb; g.ldc = ldc;
   g.a_scale = a_scale; g.b_scale = b_scale; g.a_dev = a_scale_dev; g.b_dev = b_scale_dev;
-  // the large-tile kernel reads whole 64-byte K sub-slices and keeps tile
-  // offsets in 32 bits
-  if (K % kG2Sub == 0 && lda * (int64_t)kG2Tile < (int64_t)1 << 32 &&
-      ldb * (int64_t)kG2Tile < (int64_t)1 << 32)
-    return launch_gemm256(g, static_cast<hipStream_t>(stream));
+  g.b_kn = kn ? 1 : 0;
+  // The large-tile kernel reads whole 64-byte K sub-slices and keeps tile
+  // offsets in 32 bits; from a (K, N) B it loads whole 16-byte N granules.
+  const bool big = K % kG2Sub == 0 && lda * (int64_t)kG2Tile < (int64_t)1 << 32 &&
+                   (kn ? (N % 16 == 0 && ldb % 16 == 0 && reinterpret_cast<uintptr_t>(b8) % 16 == 0 &&
+                          ldb * (int64_t)kG2K < (int64_t)1 << 32)
+                       : ldb * (int64_t)kG2Tile < (int64_t)1 << 32);
+  if (big) return launch_gemm256(g, static_cast<hipStream_t>(stream));
   return launch_gemm<256, 128>(g, static_cast<hipStream_t>(stream));
 }
 
-extern "C" int rp_fp8_gemm(const uint8_t* a8, const uint8_t* bt8, void* c, int64_t M, int64_t N,
-                           int64_t K, int64_t lda, int64_t ldb, int64_t ldc, float a_scale,
-                           float b_scale, const float* a_scale_dev, const float* b_scale_dev,
-                           void* stream) {
-  return gemm_run(a8, bt8, nullptr, c, M, N, K, lda, ldb, ldc, a_scale, b_scale, a_scale_dev,
-                  b_scale_dev, stream);
+extern "C" int rp_fp8_gemm(const uint8_t* a8, const uint8_t* b8, int b_layout, void* c, int64_t M,
+                           int64_t N, int64_t K, int64_t lda, int64_t ldb, int64_t ldc,
+                           float a_scale, float b_scale, const float* a_scale_dev,
+                           const float* b_scale_dev, void* stream) {
+  return gemm_run(a8, b8, b_layout, nullptr, c, M, N, K, lda, ldb, ldc, a_scale, b_scale,
+                  a_scale_dev, b_scale_dev, stream);
 }
 
-extern "C" int rp_fp8_linear(const uint8_t* a8, const uint8_t* bt8, const void* bias, void* c,
-                             int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldb,
+extern "C" int rp_fp8_linear(const uint8_t* a8, const uint8_t* b8, int b_layout, const void* bias,
+                             void* c, int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldb,
                              int64_t ldc, float a_scale, float b_scale, const float* a_scale_dev,
                              const float* b_scale_dev, void* stream) {
-  return gemm_run(a8, bt8, bias, c, M, N, K, lda, ldb, ldc, a_scale, b_scale, a_scale_dev,
-                  b_scale_dev, stream);
+  return gemm_run(a8, b8, b_layout, bias, c, M, N, K, lda, ldb, ldc, a_scale, b_scale,
+                  a_scale_dev, b_scale_dev, stream);
 }
 
 extern "C" int rp_fp8_transpose(const uint8_t* src, uint8_t* dst, int64_t R, int64_t C,

@@ -14,7 +14,8 @@ Numerics (OCP e4m3fn, FP8_MAX = 448):
                  -- fp8_flash_attn_hopper.py:388-398
   fp8_flash_attention
                  FA-2 FP8 forward -- kernels/triton_kernels/fp8_flash_attn.py:480-645
-  fp8_gemm       bf16(fp32(A8 . B8) * a_scale * b_scale)
+  fp8_gemm       bf16(fp32(A8 . B8) * a_scale * b_scale), B (K, N) as the
+                 reference takes it or (N, K)
                  -- kernels/hip/fp8_attn/binding.cpp:25-57, fp8_gemm.hip:79-179
 """
 
@@ -492,12 +493,15 @@ def fp8_gemm(a8: torch.Tensor, b8: torch.Tensor, a_scale: float | torch.Tensor,
 
     Same contract as the reference's ``fp8_gemm(A, B, a_scale, b_scale)``
     (kernels/hip/fp8_attn/binding.cpp:25-57) with OCP e4m3fn operands: A8 is
-    (M, K) row-major, B8 is (K, N) row-major -- or, with ``b_transposed``,
-    already (N, K) (the K-contiguous operand the kernel reads; the reference
-    layout costs one extra transpose pass).  Scales may be Python floats or
-    one-element device tensors (read on the device, no host sync).  ``bias``
-    (bf16 [N]) is added to the fp32 product before the bf16 rounding
-    (``rp_fp8_linear``, an nn.Linear epilogue; the reference GEMM has none).
+    (M, K) row-major and B8 (K, N) row-major, which the kernel stages and
+    transposes in LDS itself (``RP_B_KN``: no transpose pass, no copy) -- or,
+    with ``b_transposed``, B^T (N, K), the nn.Linear weight layout
+    (``RP_B_NK``).  Either operand may be a row-strided view (unit stride
+    along its rows, row stride >= the row length; A's and B^T's row strides
+    multiples of 16).  Scales may be Python floats or one-element device
+    tensors (read on the device, no host sync).  ``bias`` (bf16 [N]) is added
+    to the fp32 product before the bf16 rounding (``rp_fp8_linear``, an
+    nn.Linear epilogue; the reference GEMM has none).
     """
     _check_cuda("a8", a8)
     _on_device_of(a8, b8=b8, out=out, bias=bias,
@@ -508,13 +512,19 @@ def fp8_gemm(a8: torch.Tensor, b8: torch.Tensor, a_scale: float | torch.Tensor,
     for name, t in (("A", a8), ("B", b8)):
         if t.dtype not in (torch.float8_e4m3fn, torch.uint8):
             raise TypeError(f"{name} must be float8_e4m3fn (got {t.dtype})")
-        if not t.is_contiguous():
-            raise ValueError(f"{name} must be contiguous")
+        if t.stride(1) != 1 or t.stride(0) < t.shape[1]:
+            raise ValueError(f"{name} must have unit column stride and a row stride of at "
+                             f"least its row length (got strides {t.stride()})")
     M, K = a8.shape
-    bt = b8 if b_transposed else transpose_fp8(b8)
-    N = bt.shape[0]
-    if bt.shape[1] != K:
-        raise ValueError(f"K mismatch: A {tuple(a8.shape)}, B {tuple(b8.shape)}")
+    if b_transposed:
+        N, Kb = b8.shape
+        layout = C.RP_B_NK
+    else:
+        Kb, N = b8.shape
+        layout = C.RP_B_KN
+    if Kb != K:
+        raise ValueError(f"K mismatch: A {tuple(a8.shape)}, B {tuple(b8.shape)}"
+                         f"{' (transposed)' if b_transposed else ''}")
     if out is None:
         out = torch.empty((M, N), dtype=torch.bfloat16, device=a8.device)
     else:
@@ -524,13 +534,13 @@ def fp8_gemm(a8: torch.Tensor, b8: torch.Tensor, a_scale: float | torch.Tensor,
                              f"got {tuple(out.shape)} strides {out.stride()}")
     a_dev = a_scale.to(torch.float32).contiguous() if isinstance(a_scale, torch.Tensor) else None
     b_dev = b_scale.to(torch.float32).contiguous() if isinstance(b_scale, torch.Tensor) else None
-    args = (M, N, K, a8.stride(0), bt.stride(0), out.stride(0),
+    args = (M, N, K, a8.stride(0), b8.stride(0), out.stride(0),
             0.0 if a_dev is not None else float(a_scale),
             0.0 if b_dev is not None else float(b_scale),
             a_dev.data_ptr() if a_dev is not None else None,
             b_dev.data_ptr() if b_dev is not None else None, _stream(a8))
     if bias is None:
-        C.check(C.lib().rp_fp8_gemm(a8.data_ptr(), bt.data_ptr(), out.data_ptr(), *args),
+        C.check(C.lib().rp_fp8_gemm(a8.data_ptr(), b8.data_ptr(), layout, out.data_ptr(), *args),
                 "rp_fp8_gemm")
     else:
         _check_bf16("bias", bias)
@@ -538,19 +548,34 @@ def fp8_gemm(a8: torch.Tensor, b8: torch.Tensor, a_scale: float | torch.Tensor,
             raise ValueError(f"bias must be a contiguous ({N},) tensor, got {tuple(bias.shape)}")
         if bias.data_ptr() % 8 != 0:          # the epilogue reads 4 bias values at a time
             bias = bias.clone()
-        C.check(C.lib().rp_fp8_linear(a8.data_ptr(), bt.data_ptr(), bias.data_ptr(),
+        C.check(C.lib().rp_fp8_linear(a8.data_ptr(), b8.data_ptr(), layout, bias.data_ptr(),
                                       out.data_ptr(), *args), "rp_fp8_linear")
     return out
 
 
-def fp8_linear_weight(w: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
-    """Quantize a bf16 weight W (K, N) once into the GEMM's (N, K) operand and its
-    per-tensor dequant scale (one transposing pass)."""
+def fp8_linear_weight(w: torch.Tensor, layout: Literal["nk", "kn"] = "nk"
+                      ) -> tuple[torch.Tensor, torch.Tensor]:
+    """Quantize a bf16 weight W (K, N) once, per tensor: (dequant scale (1,),
+    codes).  ``layout="nk"`` gives the (N, K) operand for
+    ``fp8_gemm(..., b_transposed=True)`` -- written transposed by the
+    quantizer itself when N % 32 == 0 (a row-strided (N, K) view of its
+    128-padded rows), else quantized as it lies and transposed once;
+    ``layout="kn"`` gives the (K, N) codes as they lie, for
+    ``fp8_gemm(..., b_transposed=False)``."""
     _check_bf16("w", w)
+    if w.dim() != 2:
+        raise ValueError(f"w must be 2-D (K, N), got {tuple(w.shape)}")
     K, N = w.shape
+    if layout == "kn" or N % 32 != 0:
+        # one group: the contiguous weight viewed as rows of 8 elements
+        if (K * N) % 8 != 0:
+            raise ValueError(f"K * N must be a multiple of 8 (got {K} x {N})")
+        dq, codes = scale_quantize(w.contiguous().reshape(1, 1, K * N // 8, 8), "tensor", "bhsd")
+        codes = codes.view(torch.uint8).reshape(K, N)
+        return (dq, codes) if layout == "kn" else (dq, transpose_fp8(codes))
     dq, codes = scale_quantize(w.reshape(1, 1, K, N), "tensor", "bhds")
-    # codes: (1, 1, N, ldk) with ldk = K rounded up to 128
-    return dq, codes.view(torch.uint8)[0, 0]
+    # codes: (1, 1, N, ldk) with ldk = K rounded up to 128; the (N, K) view
+    return dq, codes.view(torch.uint8)[0, 0, :, :K]
 
 
 def selftest_e4m3(x: torch.Tensor) -> torch.Tensor:

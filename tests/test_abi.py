@@ -56,7 +56,7 @@ def test_no_oracle_or_torch_symbols_in_library() -> None:
 
 def test_version_and_status_strings() -> None:
     L = _capi.lib()
-    assert L.rp_abi_version() == 2
+    assert L.rp_abi_version() == 3
     assert L.rp_status_string(0) == b"ok"
     assert L.rp_status_string(1) == b"invalid argument"
     assert L.rp_status_string(2) == b"unsupported shape or layout"
@@ -102,11 +102,22 @@ def test_attention_argument_checks(kw: dict, status: int, msg: str) -> None:
     assert msg in L.rp_last_error().decode()
 
 
+NK, KN = _capi.RP_B_NK, _capi.RP_B_KN
+
+
 @pytest.mark.parametrize("args,status,msg", [
-    ((None, FAKE, FAKE, 64, 64, 64, 64, 64, 64), 1, "null pointer"),
-    ((FAKE, FAKE, FAKE, 64, 64, 0, 64, 64, 64), 1, "bad sizes"),
-    ((FAKE, FAKE, FAKE, 64, 64, 40, 40, 40, 64), 2, "multiples of 16"),
-    ((FAKE, FAKE, FAKE + 4, 64, 64, 64, 64, 64, 64), 2, "aligned"),
+    # a8, b8, layout, c, M, N, K, lda, ldb, ldc
+    ((None, FAKE, NK, FAKE, 64, 64, 64, 64, 64, 64), 1, "null pointer"),
+    ((FAKE, FAKE, NK, FAKE, 64, 64, 0, 64, 64, 64), 1, "bad sizes"),
+    ((FAKE, FAKE, NK, FAKE, 64, 64, 40, 40, 40, 64), 2, "multiples of 16"),
+    ((FAKE, FAKE, NK, FAKE + 4, 64, 64, 64, 64, 64, 64), 2, "aligned"),
+    ((FAKE, FAKE, 7, FAKE, 64, 64, 64, 64, 64, 64), 1, "B layout"),
+    # (N, K) B: ldb >= K, a multiple of 16, B 16-byte aligned
+    ((FAKE, FAKE, NK, FAKE, 64, 128, 64, 64, 48, 128), 1, "bad sizes"),
+    ((FAKE, FAKE, NK, FAKE, 64, 64, 64, 64, 72, 64), 2, "multiples of 16"),
+    ((FAKE, FAKE + 8, NK, FAKE, 64, 64, 64, 64, 64, 64), 2, "aligned"),
+    # (K, N) B: ldb >= N (no alignment needed: the general kernel gathers bytes)
+    ((FAKE, FAKE, KN, FAKE, 64, 128, 64, 64, 100, 128), 1, "bad sizes"),
 ])
 def test_gemm_argument_checks(args: tuple, status: int, msg: str) -> None:
     L = _capi.lib()
@@ -118,12 +129,12 @@ def test_linear_argument_checks() -> None:
     """rp_fp8_linear runs the GEMM's checks, then needs an 8-byte aligned bias
     (the epilogue reads four bf16 values at once); a null bias is rp_fp8_gemm."""
     L = _capi.lib()
-    ok = (FAKE, FAKE, FAKE, FAKE, 64, 64, 64, 64, 64, 64, 1.0, 1.0, None, None, None)
-    bad = list(ok); bad[2] = FAKE + 2
+    ok = (FAKE, FAKE, NK, FAKE, FAKE, 64, 64, 64, 64, 64, 64, 1.0, 1.0, None, None, None)
+    bad = list(ok); bad[3] = FAKE + 2
     assert L.rp_fp8_linear(*bad) == 2 and "bias" in L.rp_last_error().decode()
     bad = list(ok); bad[0] = None
     assert L.rp_fp8_linear(*bad) == 1 and "null" in L.rp_last_error().decode()
-    bad = list(ok); bad[5] = 6
+    bad = list(ok); bad[6] = 6
     assert L.rp_fp8_linear(*bad) == 2 and "multiples" in L.rp_last_error().decode()
 
 

@@ -91,10 +91,68 @@ def test_random_vs_oracle(gpu: torch.device, mnk: tuple[int, int, int]) -> None:
     ref = native.gemm_rows(codes_np(a8), codes_np(bt8), sa, sb, np.arange(M))
     _assert_one_rounding_apart(bf16_to_f32(bf16_bits(got)), bf16_to_f32(ref), codes_np(a8),
                                codes_np(bt8), sa * sb)
-    # the reference's (K, N) row-major B through the transposing path, scales on device
+    # the reference's (K, N) row-major B, staged and transposed in LDS by the
+    # kernel (the MFMAs see the same bytes in the same order), scales on device
     got2 = ops.fp8_gemm(a8.to(gpu), bt8.to(gpu).t().contiguous(),
                         torch.tensor([sa], device=gpu), torch.tensor([sb], device=gpu))
     assert torch.equal(got2, got)
+
+
+@pytest.mark.parametrize("mnk,ldb_pad", [
+    ((300, 400, 320), 0),      # ragged N tile (256 + 144), K % 128 == 64: half last slice
+    ((257, 512, 1024), 48),    # row-strided (K, N) view, ldb = N + 48
+    ((64, 256, 64), 0),        # one 64-deep K slice
+    ((513, 272, 192), 16),     # N % 256 == 16: one granule in the last tile
+    ((100, 100, 4160), 0),     # N % 16 != 0: the general kernel's byte gathers
+    ((33, 12, 48), 4),         # K % 64 != 0, odd ldb: the general kernel
+])
+def test_row_major_b_vs_oracle(gpu: torch.device, mnk: tuple[int, int, int],
+                               ldb_pad: int, monkeypatch: pytest.MonkeyPatch) -> None:
+    """B given as the reference passes it, (K, N) row-major (rp_fp8_gemm with
+    RP_B_KN): no transpose pass runs, and the result is the (N, K) path's
+    bit for bit and within one rounding of the exact sum."""
+    M, N, K = mnk
+    g = torch.Generator().manual_seed(7 * M + N + K)
+    a8 = torch.randn(M, K, generator=g).mul(30).to(torch.float8_e4m3fn)
+    b8 = torch.randn(K, N, generator=g).mul(30).to(torch.float8_e4m3fn)
+    sa, sb = 0.011, 0.0093
+    store = torch.zeros(K, N + ldb_pad, dtype=torch.uint8)
+    store[:, :N] = b8.view(torch.uint8)
+    bview = store.to(gpu)[:, :N]
+    monkeypatch.setattr(ops, "transpose_fp8", lambda *_a, **_k: pytest.fail("transpose pass ran"))
+    got = ops.fp8_gemm(a8.to(gpu), bview, sa, sb)
+    nk = ops.fp8_gemm(a8.to(gpu), b8.t().contiguous().to(gpu), sa, sb, b_transposed=True)
+    assert torch.equal(got, nk), f"max diff {(got.float() - nk.float()).abs().max().item()}"
+    bt = np.ascontiguousarray(codes_np(b8).T)
+    ref = native.gemm_rows(codes_np(a8), bt, sa, sb, np.arange(M))
+    _assert_one_rounding_apart(bf16_to_f32(bf16_bits(got)), bf16_to_f32(ref), codes_np(a8),
+                               bt, sa * sb)
+
+
+def test_weight_with_unaligned_n_and_k(gpu: torch.device) -> None:
+    """fp8_linear_weight on a (K, N) weight with K % 128 != 0 and N % 32 != 0
+    (K = 4160, N = 100), both layouts, against the oracle: the (N, K) operand
+    is a valid B^T whatever its padding, and the (K, N) codes run as they lie."""
+    K, N, M = 4160, 100, 96
+    g = torch.Generator().manual_seed(4160)
+    w = torch.randn(K, N, generator=g).mul(0.02).to(torch.bfloat16)
+    a = torch.randn(M, K, generator=g).to(torch.bfloat16)
+    sa, a8 = ops.scale_quantize(a.to(gpu), "tensor", "bhsd")
+    a8 = a8.view(torch.uint8).reshape(M, K)
+    sw, wt8 = ops.fp8_linear_weight(w.to(gpu))
+    assert wt8.shape == (N, K)
+    sw2, w8 = ops.fp8_linear_weight(w.to(gpu), layout="kn")
+    assert w8.shape == (K, N) and float(sw2.item()) == float(sw.item())
+    ws_ref, w8_ref = native.quantize_groups(bf16_bits(w), 1)
+    assert float(ws_ref[0]) == float(sw.item())
+    assert np.array_equal(codes_np(w8), w8_ref) and np.array_equal(codes_np(wt8), w8_ref.T)
+    c_nk = ops.fp8_gemm(a8, wt8, sa, sw, b_transposed=True)
+    c_kn = ops.fp8_gemm(a8, w8, sa, sw)
+    assert torch.equal(c_nk, c_kn)
+    ref = native.gemm_rows(codes_np(a8), np.ascontiguousarray(w8_ref.T), float(sa.item()),
+                           float(sw.item()), np.arange(M))
+    _assert_one_rounding_apart(bf16_to_f32(bf16_bits(c_nk)), bf16_to_f32(ref), codes_np(a8),
+                               np.ascontiguousarray(w8_ref.T), float(sa.item()) * float(sw.item()))
 
 
 @pytest.mark.parametrize("mnk", [(64, 64, 256), (300, 200, 512), (5, 4, 16)])
@@ -161,7 +219,11 @@ def test_wan_ffn_gemm_full_shape_sampled_rows(gpu: torch.device) -> None:
     got = bf16_to_f32(bf16_bits(c[torch.from_numpy(rows).to(gpu)]))
     _assert_one_rounding_apart(got, bf16_to_f32(ref), a8_rows, codes_np(wt8)[:, :C4.K],
                                sa_h * float(sw.item()))
-    del a, w, a8, wt8, c
+    # the weight as the reference passes it, (K, N) row-major: the same output
+    sw2, w8 = ops.fp8_linear_weight(w, layout="kn")
+    c2 = ops.fp8_gemm(a8.view(torch.uint8), w8, sa, sw2)
+    assert torch.equal(c2, c)
+    del a, w, a8, wt8, c, c2, w8
     torch.cuda.empty_cache()
 
 
@@ -179,12 +241,15 @@ def test_out_argument_is_checked(gpu: torch.device) -> None:
     assert torch.equal(wide[:, 16:], torch.full((64, 8), 7.0, dtype=torch.bfloat16, device=gpu))
 
 
-def test_device_reproduces_golden_vectors(gpu: torch.device) -> None:
+def test_device_reproduces_golden_vectors(gpu: torch.device,
+                                         monkeypatch: pytest.MonkeyPatch) -> None:
     """The committed known-answer vectors through the reference's (K, N)
-    row-major B (the transposing path) and through the K-contiguous operand,
-    scales as host floats and as device tensors: every output bit for bit."""
+    row-major B (staged and transposed by the kernel, no transpose pass) and
+    through the K-contiguous operand, scales as host floats and as device
+    tensors: every output bit for bit."""
     from tests._helpers import golden_gemm_cases
 
+    monkeypatch.setattr(ops, "transpose_fp8", lambda *_a, **_k: pytest.fail("transpose pass ran"))
     for name, a8, b8, sa, sb, c_bits in golden_gemm_cases():
         a = torch.from_numpy(a8).to(gpu).view(torch.float8_e4m3fn)
         b = torch.from_numpy(b8).to(gpu).view(torch.float8_e4m3fn)
