@@ -151,6 +151,39 @@ int rp_fp8_scale_quantize_qkv_noalloc(const void* q, const void* k, const void* 
                                       uint8_t* q8, uint8_t* k8, uint8_t* vt8, int64_t ldv,
                                       void* stream);
 
+/* ------------------------------------------------------- row-wise FP8
+ * Per-row scales: each of `rows` rows of `cols` contiguous elements (bf16 or
+ * fp16, row stride ldx elements) gets its own amax over the row and
+ *   dequant_out[r] = dtype(max(amax, dtype(1e-6)) / 425.6)
+ *   codes[r, :]    = e4m3fn(clamp(x * dtype(dtype(1 / amax) * 425.6), -448, 448))
+ * (RNE; codes rows of stride ldq bytes).  Replaces _rowwise_quantize,
+ * src/repercep/attention/fp8_scaled_mm.py:107-133 (amax over the last axis;
+ * `target / amax` evaluates as amax.reciprocal() * target, two roundings to
+ * the input dtype), with the OCP e4m3fn constants (448, 0.95 * 448) as the
+ * OCP siblings of the per-(b,h) quantizer use them.  cols, ldx, ldq
+ * multiples of 8; x 16-byte and codes 8-byte aligned. */
+int rp_fp8_rowwise_quantize(const void* x, int x_dtype, int64_t rows, int64_t cols, int64_t ldx,
+                            float* dequant_out, uint8_t* codes, int64_t ldq, void* stream);
+
+/* 16-bit transpose of `batch` (R, C) matrices: dst_z (C, R) <- src_z (R, C),
+ * row strides lds / ldd and batch strides bs / bd in elements.  The
+ * reference's v.transpose(-1, -2).contiguous() ahead of V's row-wise
+ * quantization (src/repercep/attention/fp8_scaled_mm.py:167-168). */
+int rp_transpose16(const void* src, void* dst, int64_t batch, int64_t R, int64_t C, int64_t lds,
+                   int64_t ldd, int64_t bs, int64_t bd, void* stream);
+
+/* Softmax of raw bf16 scores and P's row-wise quantization in one pass per
+ * row: for row r (query q = r % sq) of `cols` raw scores (row stride lds),
+ *   s_j = bf16(raw_j * scale), -inf for j > q when causal
+ *   p_j = bf16(exp(s_j - max s) / sum_k exp(s_k - max s))   (fp32 math)
+ *   dequant_out[r], codes[r, :] = the row-wise quantization of p (as above)
+ * Replaces `scores_raw * scale`, the causal masked_fill, torch.softmax in
+ * bf16 and _rowwise_quantize(p) of src/repercep/attention/fp8_scaled_mm.py:
+ * 159-171.  cols, lds, ldq even; scores 4-byte aligned. */
+int rp_fp8_softmax_rowwise_quantize(const void* scores, int64_t rows, int64_t cols, int64_t lds,
+                                    int64_t sq, int causal, float scale, float* dequant_out,
+                                    uint8_t* codes, int64_t ldq, void* stream);
+
 /* --------------------------------------------------------- attention
  * FP8 flash-attention forward, FA-2 online softmax in fp32, both dot
  * products on gfx950 e4m3 MFMAs, P re-quantized as e4m3fn(p * 448).
@@ -267,6 +300,22 @@ int rp_fp8_linear(const uint8_t* a8, const uint8_t* b8, int b_layout, const void
                   int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldb, int64_t ldc,
                   float a_scale, float b_scale, const float* a_scale_dev,
                   const float* b_scale_dev, void* stream);
+
+/* rp_fp8_gemm with row-wise scales, batched: for each batch z < `batch`,
+ *   C_z (M, N) = bf16( fp32(fp32(A8_z . B8_z) * row_scale_z[m]) * col_scale_z[n] )
+ * with A8_z = a8 + z*bsa, B8_z = b8 + z*bsb (bytes), C_z = c + z*bsc,
+ * row_scale_z = row_scale + z*bs_row, col_scale_z = col_scale + z*bs_col
+ * (elements).  Replaces the two torch._scaled_grouped_mm calls of the
+ * reference's unfused FP8 attention (src/repercep/attention/
+ * fp8_scaled_mm.py:149-157 and :172-178: scale_a per row of A, scale_b per
+ * column of the product, a (BH, M, K) x (BH, N, K)^T batch).  Same size
+ * rules as rp_fp8_gemm; col_scale_z 16-byte aligned; batch <= 65535; batch
+ * strides of A and B multiples of 16, of C of 4. */
+int rp_fp8_gemm_rowwise(const uint8_t* a8, const uint8_t* b8, int b_layout, void* c, int64_t M,
+                        int64_t N, int64_t K, int64_t lda, int64_t ldb, int64_t ldc,
+                        const float* row_scale, const float* col_scale, int64_t batch,
+                        int64_t bsa, int64_t bsb, int64_t bsc, int64_t bs_row, int64_t bs_col,
+                        void* stream);
 
 /* FP8 byte transpose: dst (C, R) <- src (R, C); row strides lds, ldd.  No
  * counterpart in the reference; turns a (K, N) weight into the (N, K)

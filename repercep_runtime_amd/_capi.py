@@ -45,6 +45,8 @@ EXPORTS = (
     "rp_fp8_attn_blocks_per_workgroup",
     "rp_fp8_attn_fwd_split", "rp_fp8_rmsnorm_quant_workspace_bytes",
     "rp_fp8_rmsnorm_scale_quantize", "rp_fp8_gemm", "rp_fp8_linear", "rp_fp8_transpose",
+    "rp_fp8_gemm_rowwise", "rp_fp8_rowwise_quantize", "rp_transpose16",
+    "rp_fp8_softmax_rowwise_quantize",
     "rp_selftest_e4m3", "rp_selftest_scale",
 )
 
@@ -112,6 +114,16 @@ def _declare(L: ctypes.CDLL) -> None:
     L.rp_fp8_linear.restype = _int
     L.rp_fp8_linear.argtypes = [_vp, _vp, _int, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64,
                                 _f32, _f32, _vp, _vp, _vp]
+    L.rp_fp8_gemm_rowwise.restype = _int
+    L.rp_fp8_gemm_rowwise.argtypes = ([_vp, _vp, _int, _vp] + [_i64] * 6 + [_vp, _vp]
+                                      + [_i64] * 6 + [_vp])
+    L.rp_fp8_rowwise_quantize.restype = _int
+    L.rp_fp8_rowwise_quantize.argtypes = [_vp, _int, _i64, _i64, _i64, _vp, _vp, _i64, _vp]
+    L.rp_transpose16.restype = _int
+    L.rp_transpose16.argtypes = [_vp, _vp] + [_i64] * 7 + [_vp]
+    L.rp_fp8_softmax_rowwise_quantize.restype = _int
+    L.rp_fp8_softmax_rowwise_quantize.argtypes = [_vp, _i64, _i64, _i64, _i64, _int, _f32, _vp,
+                                                  _vp, _i64, _vp]
     L.rp_fp8_transpose.restype = _int
     L.rp_fp8_transpose.argtypes = [_vp, _vp, _i64, _i64, _i64, _i64, _vp]
     L.rp_selftest_e4m3.restype = _int

@@ -4,6 +4,7 @@ from __future__ import annotations
 
 from repercep_runtime_amd.attention import diffusers_backend as _diffusers_backend  # noqa: F401
 from repercep_runtime_amd.attention.fp8_hip import FP8HipAttention
+from repercep_runtime_amd.attention.fp8_scaled_mm import FP8HipScaledMMAttention
 from repercep_runtime_amd.attention.naive import NaiveAttention
 from repercep_runtime_amd.attention.protocol import AttentionOp
 from repercep_runtime_amd.attention.registry import select_attention_op
@@ -14,6 +15,7 @@ __all__ = [
     "AttentionOp",
     "AttentionShape",
     "FP8HipAttention",
+    "FP8HipScaledMMAttention",
     "NaiveAttention",
     "select_attention_op",
 ]

@@ -65,7 +65,8 @@ class ROCmBackend:
     def capabilities(self) -> BackendCapabilities:
         from repercep_runtime_amd import _capi
 
-        ops = ("fp8-hip-flash", "naive-sdpa") if _capi.available() else ("naive-sdpa",)
+        ops = (("fp8-hip-flash", "fp8-hip-scaled-mm", "naive-sdpa") if _capi.available()
+               else ("naive-sdpa",))
         return BackendCapabilities(
             dtypes=frozenset({DType.FP32, DType.FP16, DType.BF16, DType.FP8_E4M3,
                               DType.FP8_E5M2, DType.INT8}),

@@ -39,7 +39,8 @@ COMMON = [
     # the attention kernel's direct-to-LDS load is inline asm that sets M0
     "-Wno-inline-asm",
 ]
-SOURCES = ["rp_api.hip", "rp_quant.hip", "rp_prologue.hip", "rp_attn.hip", "rp_gemm.hip"]
+SOURCES = ["rp_api.hip", "rp_quant.hip", "rp_prologue.hip", "rp_attn.hip", "rp_gemm.hip",
+           "rp_rowwise.hip"]
 
 
 def _compile(src: Path, obj: Path, verbose: bool) -> None:

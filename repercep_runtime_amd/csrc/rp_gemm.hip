@@ -48,7 +48,41 @@ struct GemmArgs {
   const float* b_dev;
   int tiles_m, tiles_n;
   int b_kn;   // 1: B is (K, N) row-major, row stride ldb (RP_B_KN)
+  // row-wise scales (rp_fp8_gemm_rowwise): C = bf16((acc * row_scale[m]) *
+  // col_scale[n]) instead of the per-tensor scales; null otherwise
+  const float* row_scale;
+  const float* col_scale;
+  // batched launches (blockIdx.y = batch): strides of A and B (bytes), C
+  // (elements) and the two scale vectors (elements)
+  int64_t bsa, bsb, bsc, bsr, bss;
 };
+
+// The batch a workgroup works on: offsets every operand pointer (one batch
+// unless blockIdx.y > 0).
+__device__ __forceinline__ void gemm_batch(GemmArgs& g) {
+  const int64_t z = blockIdx.y;
+  g.a += z * g.bsa;
+  g.bt += z * g.bsb;
+  g.c += z * g.bsc;
+  if (g.row_scale) g.row_scale += z * g.bsr;
+  if (g.col_scale) g.col_scale += z * g.bss;
+}
+
+// Row-wise epilogue values: fp32(fp32(acc * row scale) * column scale), then
+// the bias as in epi4.
+__device__ __forceinline__ void epi4_rows(bool has_bias, uint2 bb, float sm, const float4& sn,
+                                          float v0, float v1, float v2, float v3, float (&o)[4]) {
+  o[0] = v0 * sm; o[1] = v1 * sm; o[2] = v2 * sm; o[3] = v3 * sm;
+  asm("" : "+v"(o[0]), "+v"(o[1]), "+v"(o[2]), "+v"(o[3]));
+  o[0] *= sn.x; o[1] *= sn.y; o[2] *= sn.z; o[3] *= sn.w;
+  if (has_bias) {
+    asm("" : "+v"(o[0]), "+v"(o[1]), "+v"(o[2]), "+v"(o[3]));
+    o[0] += bf16_to_f32(bb.x & 0xffffu);
+    o[1] += bf16_to_f32(bb.x >> 16);
+    o[2] += bf16_to_f32(bb.y & 0xffffu);
+    o[3] += bf16_to_f32(bb.y >> 16);
+  }
+}
 
 // Bias values of the 4 columns n..n+3 (bf16 pairs), or zeros past N.  Every
 // thread loads its columns before the first output store: the bias and C are
@@ -175,6 +209,7 @@ void gemm_kernel(GemmArgs g) {
   using G = GGeo<BM, BN>;
   __shared__ __attribute__((aligned(16))) uint8_t smem[2 * G::STAGE];
 
+  gemm_batch(g);
   // XCD-aware remap, then column-major walk over 8-tile-tall bands of C so
   // consecutive workgroups reuse the same B^T rows.
   const int nwork = g.tiles_m * g.tiles_n;
@@ -229,7 +264,8 @@ void gemm_kernel(GemmArgs g) {
     __syncthreads();
   }
 
-  const float scale = (g.a_dev ? *g.a_dev : g.a_scale) * (g.b_dev ? *g.b_dev : g.b_scale);
+  const float scale = g.row_scale ? 1.0f
+                    : (g.a_dev ? *g.a_dev : g.a_scale) * (g.b_dev ? *g.b_dev : g.b_scale);
   const bool has_bias = g.bias != nullptr;
   uint2 bb[G::TN];
 #pragma unroll
@@ -245,7 +281,11 @@ void gemm_kernel(GemmArgs g) {
       if (n >= g.N) continue;
       const f32x4 v = acc[j][i];
       float o[4];
-      epi4(has_bias, bb[j], scale, v[0], v[1], v[2], v[3], o);
+      if (g.row_scale)
+        epi4_rows(has_bias, bb[j], g.row_scale[m], *reinterpret_cast<const float4*>(g.col_scale + n),
+                  v[0], v[1], v[2], v[3], o);
+      else
+        epi4(has_bias, bb[j], scale, v[0], v[1], v[2], v[3], o);
       uint2 pk;
       pk.x = f32_to_bf16_bits(o[0]) | (f32_to_bf16_bits(o[1]) << 16);
       pk.y = f32_to_bf16_bits(o[2]) | (f32_to_bf16_bits(o[3]) << 16);
@@ -365,6 +405,7 @@ void gemm256_kernel(GemmArgs g) {
   __shared__ __attribute__((aligned(1024))) uint8_t smem[kG2Stages * kG2Stage];
   const uint32_t smem_lds = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)smem;
 
+  gemm_batch(g);
   // XCD-aware remap, then a column-major walk over 4-tile-tall bands of C:
   // the 32 workgroups resident on one XCD cover a 4 x 8 patch and share
   // its A and B^T rows in that XCD's L2 (4-tall measured best of 1, 2, 4,
@@ -539,8 +580,10 @@ void gemm256_kernel(GemmArgs g) {
   }
   if (half_tail) sub(nfull, std::integral_constant<int, 0>{}, o0, o1);
 
-  // epilogue: C[m][n] = bf16(acc * a_scale * b_scale)
-  const float scale = (g.a_dev ? *g.a_dev : g.a_scale) * (g.b_dev ? *g.b_dev : g.b_scale);
+  // epilogue: C[m][n] = bf16(acc * a_scale * b_scale), or with row-wise
+  // scales bf16((acc * row_scale[m]) * col_scale[n])
+  const float scale = g.row_scale ? 1.0f
+                    : (g.a_dev ? *g.a_dev : g.a_scale) * (g.b_dev ? *g.b_dev : g.b_scale);
   const bool has_bias = g.bias != nullptr;
   uint2 bb[4][4];
 #pragma unroll
@@ -553,6 +596,7 @@ void gemm256_kernel(GemmArgs g) {
   for (int i = 0; i < 4; ++i) {
     const int64_t m = m0 + wm * 128 + 32 * i + lq;
     if (m >= g.M) continue;
+    const float sm = g.row_scale ? g.row_scale[m] : 1.0f;
 #pragma unroll
     for (int j = 0; j < 4; ++j)
 #pragma unroll
@@ -561,8 +605,12 @@ void gemm256_kernel(GemmArgs g) {
         if (n >= g.N) continue;
         const f32x16& v = acc[i][j];
         float o[4];
-        epi4(has_bias, bb[j][q], scale, v[4 * q + 0], v[4 * q + 1], v[4 * q + 2],
-             v[4 * q + 3], o);
+        if (g.row_scale)
+          epi4_rows(has_bias, bb[j][q], sm, *reinterpret_cast<const float4*>(g.col_scale + n),
+                    v[4 * q + 0], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3], o);
+        else
+          epi4(has_bias, bb[j][q], scale, v[4 * q + 0], v[4 * q + 1], v[4 * q + 2],
+               v[4 * q + 3], o);
         uint2 pk;
         pk.x = g2_pack_bf16(o[0], o[1]);
         pk.y = g2_pack_bf16(o[2], o[3]);
@@ -571,7 +619,7 @@ void gemm256_kernel(GemmArgs g) {
   }
 }
 
-int launch_gemm256(GemmArgs g, hipStream_t st) {
+int launch_gemm256(GemmArgs g, int64_t batch, hipStream_t st) {
   g.tiles_m = (int)((g.M + kG2Tile - 1) / kG2Tile);
   g.tiles_n = (int)((g.N + kG2Tile - 1) / kG2Tile);
   const int64_t nwork = (int64_t)g.tiles_m * g.tiles_n;
@@ -579,10 +627,11 @@ int launch_gemm256(GemmArgs g, hipStream_t st) {
     rp_set_error("gemm: grid too large");
     return RP_ERR_UNSUPPORTED;
   }
+  const dim3 grid((unsigned)nwork, (unsigned)batch);
   if (g.b_kn)
-    hipLaunchKernelGGL(gemm256_kernel<true>, dim3((unsigned)nwork), dim3(kG2Threads), 0, st, g);
+    hipLaunchKernelGGL(gemm256_kernel<true>, grid, dim3(kG2Threads), 0, st, g);
   else
-    hipLaunchKernelGGL(gemm256_kernel<false>, dim3((unsigned)nwork), dim3(kG2Threads), 0, st, g);
+    hipLaunchKernelGGL(gemm256_kernel<false>, grid, dim3(kG2Threads), 0, st, g);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) {
     rp_set_error("gemm: launch failed: %s", hipGetErrorString(e));
@@ -609,7 +658,7 @@ __global__ __launch_bounds__(256) void transpose_u8_kernel(const uint8_t* src, u
 }
 
 template <int BM, int BN>
-int launch_gemm(GemmArgs g, hipStream_t st) {
+int launch_gemm(GemmArgs g, int64_t batch, hipStream_t st) {
   g.tiles_m = (int)((g.M + BM - 1) / BM);
   g.tiles_n = (int)((g.N + BN - 1) / BN);
   const int64_t nwork = (int64_t)g.tiles_m * g.tiles_n;
@@ -617,12 +666,11 @@ int launch_gemm(GemmArgs g, hipStream_t st) {
     rp_set_error("gemm: grid too large");
     return RP_ERR_UNSUPPORTED;
   }
+  const dim3 grid((unsigned)nwork, (unsigned)batch);
   if (g.b_kn)
-    hipLaunchKernelGGL((gemm_kernel<BM, BN, true>), dim3((unsigned)nwork), dim3(kGThreads), 0, st,
-                       g);
+    hipLaunchKernelGGL((gemm_kernel<BM, BN, true>), grid, dim3(kGThreads), 0, st, g);
   else
-    hipLaunchKernelGGL((gemm_kernel<BM, BN, false>), dim3((unsigned)nwork), dim3(kGThreads), 0,
-                       st, g);
+    hipLaunchKernelGGL((gemm_kernel<BM, BN, false>), grid, dim3(kGThreads), 0, st, g);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) {
     rp_set_error("gemm: launch failed: %s", hipGetErrorString(e));
@@ -636,10 +684,17 @@ int launch_gemm(GemmArgs g, hipStream_t st) {
 
 using namespace rp;
 
+// Row-wise scales and batching of rp_fp8_gemm_rowwise (none for the others).
+struct RowwiseBatch {
+  const float* row_scale = nullptr;
+  const float* col_scale = nullptr;
+  int64_t batch = 1, bsa = 0, bsb = 0, bsc = 0, bsr = 0, bss = 0;
+};
+
 static int gemm_run(const uint8_t* a8, const uint8_t* b8, int b_layout, const void* bias,
                     void* c, int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldb,
                     int64_t ldc, float a_scale, float b_scale, const float* a_scale_dev,
-                    const float* b_scale_dev, void* stream) {
+                    const float* b_scale_dev, void* stream, const RowwiseBatch& rb = {}) {
   if (!a8 || !b8 || !c) {
     rp_set_error("gemm: null pointer");
     return RP_ERR_INVALID_ARGUMENT;
@@ -670,7 +725,25 @@ static int gemm_run(const uint8_t* a8, const uint8_t* b8, int b_layout, const vo
     rp_set_error("gemm: bias must be 8-byte aligned");
     return RP_ERR_UNSUPPORTED;
   }
+  if (rb.batch < 1 || rb.batch > 65535) {
+    rp_set_error("gemm: batch count %lld outside 1..65535", (long long)rb.batch);
+    return RP_ERR_UNSUPPORTED;
+  }
+  if ((rb.row_scale == nullptr) != (rb.col_scale == nullptr) ||
+      reinterpret_cast<uintptr_t>(rb.col_scale) % 16 != 0 || rb.bss % 4 != 0) {
+    rp_set_error("gemm: row-wise scales need both vectors, the column scales 16-byte aligned "
+                 "per batch");
+    return RP_ERR_INVALID_ARGUMENT;
+  }
+  if (rb.batch > 1 && (rb.bsc % 4 != 0 || rb.bsa % 16 != 0 || (!kn && rb.bsb % 16 != 0) ||
+                       (kn && rb.bsb % 16 != 0))) {
+    rp_set_error("gemm: batch strides of A and B must be multiples of 16 bytes, of C of 4 "
+                 "elements");
+    return RP_ERR_UNSUPPORTED;
+  }
   GemmArgs g{};
+  g.row_scale = rb.row_scale; g.col_scale = rb.col_scale;
+  g.bsa = rb.bsa; g.bsb = rb.bsb; g.bsc = rb.bsc; g.bsr = rb.bsr; g.bss = rb.bss;
   g.a = a8; g.bt = b8; g.c = static_cast<uint16_t*>(c);
   g.bias = static_cast<const uint16_t*>(bias);
   g.M = M; g.N = N; g.K = K; g.lda = lda; g.ldb = ldb; g.ldc = ldc;
@@ -682,8 +755,8 @@ static int gemm_run(const uint8_t* a8, const uint8_t* b8, int b_layout, const vo
                    (kn ? (N % 16 == 0 && ldb % 16 == 0 && reinterpret_cast<uintptr_t>(b8) % 16 == 0 &&
                           ldb * (int64_t)kG2K < (int64_t)1 << 32)
                        : ldb * (int64_t)kG2Tile < (int64_t)1 << 32);
-  if (big) return launch_gemm256(g, static_cast<hipStream_t>(stream));
-  return launch_gemm<256, 128>(g, static_cast<hipStream_t>(stream));
+  if (big) return launch_gemm256(g, rb.batch, static_cast<hipStream_t>(stream));
+  return launch_gemm<256, 128>(g, rb.batch, static_cast<hipStream_t>(stream));
 }
 
 extern "C" int rp_fp8_gemm(const uint8_t* a8, const uint8_t* b8, int b_layout, void* c, int64_t M,
@@ -700,6 +773,22 @@ extern "C" int rp_fp8_linear(const uint8_t* a8, const uint8_t* b8, int b_layout,
                              const float* b_scale_dev, void* stream) {
   return gemm_run(a8, b8, b_layout, bias, c, M, N, K, lda, ldb, ldc, a_scale, b_scale,
                   a_scale_dev, b_scale_dev, stream);
+}
+
+extern "C" int rp_fp8_gemm_rowwise(const uint8_t* a8, const uint8_t* b8, int b_layout, void* c,
+                                   int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldb,
+                                   int64_t ldc, const float* row_scale, const float* col_scale,
+                                   int64_t batch, int64_t bsa, int64_t bsb, int64_t bsc,
+                                   int64_t bs_row, int64_t bs_col, void* stream) {
+  if (row_scale == nullptr || col_scale == nullptr) {
+    rp_set_error("gemm_rowwise: null scale vector");
+    return RP_ERR_INVALID_ARGUMENT;
+  }
+  RowwiseBatch rb;
+  rb.row_scale = row_scale; rb.col_scale = col_scale;
+  rb.batch = batch; rb.bsa = bsa; rb.bsb = bsb; rb.bsc = bsc; rb.bsr = bs_row; rb.bss = bs_col;
+  return gemm_run(a8, b8, b_layout, nullptr, c, M, N, K, lda, ldb, ldc, 1.0f, 1.0f, nullptr,
+                  nullptr, stream, rb);
 }
 
 extern "C" int rp_fp8_transpose(const uint8_t* src, uint8_t* dst, int64_t R, int64_t C,

@@ -578,6 +578,128 @@ def fp8_linear_weight(w: torch.Tensor, layout: Literal["nk", "kn"] = "nk"
     return dq, codes.view(torch.uint8)[0, 0, :, :K]
 
 
+# --------------------------------------------------------------- row-wise FP8
+# The reference's unfused FP8 attention (src/repercep/attention/
+# fp8_scaled_mm.py:58-221): per-row scales, two scaled grouped GEMMs around a
+# bf16 softmax.  Each step is one library call here.
+
+def rowwise_quantize(x: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """(dequant scales x.shape[:-1] fp32, codes x.shape e4m3fn): one scale per
+    row of the last axis, as the reference's ``_rowwise_quantize``
+    (fp8_scaled_mm.py:107-133) computes it with the OCP constants
+    (``rp_fp8_rowwise_quantize``).  ``x`` is bf16 or fp16 with a unit stride
+    on its last axis and rows that flatten to one row stride."""
+    dt = _in_dtype("x", x)
+    if x.dim() < 1 or x.stride(-1) != 1:
+        raise ValueError("x needs a unit stride along its last axis")
+    cols = x.shape[-1]
+    x2 = x.reshape(-1, cols)      # a view whenever the rows share one stride
+    rows = x2.shape[0]
+    ldx = x2.stride(0) if rows > 1 else cols
+    dq = torch.empty(rows, dtype=torch.float32, device=x.device)
+    codes = torch.empty((rows, cols), dtype=torch.uint8, device=x.device)
+    C.check(C.lib().rp_fp8_rowwise_quantize(x2.data_ptr(), dt, rows, cols, ldx, dq.data_ptr(),
+                                            codes.data_ptr(), cols, _stream(x)),
+            "rp_fp8_rowwise_quantize")
+    return dq.reshape(x.shape[:-1]), codes.view(torch.float8_e4m3fn).reshape(x.shape)
+
+
+def transpose16(x: torch.Tensor) -> torch.Tensor:
+    """(..., R, C) -> contiguous (..., C, R) for a 16-bit tensor (``rp_transpose16``)."""
+    _check_cuda("x", x)
+    if x.element_size() != 2 or x.dim() < 2:
+        raise TypeError("transpose16 takes a 16-bit tensor of at least 2 dims")
+    x3 = x.contiguous().reshape(-1, x.shape[-2], x.shape[-1])
+    nb, R, Cc = x3.shape
+    out = torch.empty((nb, Cc, R), dtype=x.dtype, device=x.device)
+    C.check(C.lib().rp_transpose16(x3.data_ptr(), out.data_ptr(), nb, R, Cc, Cc, R, R * Cc,
+                                   R * Cc, _stream(x)), "rp_transpose16")
+    return out.reshape(*x.shape[:-2], Cc, R)
+
+
+def gemm_rowwise(a8: torch.Tensor, bt8: torch.Tensor, row_scale: torch.Tensor,
+                 col_scale: torch.Tensor) -> torch.Tensor:
+    """Batched C (Z, M, N) bf16 = bf16((fp32(A8 . B8) * row_scale[m]) * col_scale[n])
+    for A8 (Z, M, K) and B^T (Z, N, K) e4m3fn codes, row_scale (Z, M),
+    col_scale (Z, N): the reference's ``torch._scaled_grouped_mm(A, B^T.t(),
+    scale_a, scale_b, out_dtype=bf16)`` (fp8_scaled_mm.py:149-157, 172-178),
+    on ``rp_fp8_gemm_rowwise``."""
+    _check_cuda("a8", a8)
+    _on_device_of(a8, bt8=bt8, row_scale=row_scale, col_scale=col_scale)
+    if a8.dim() != 3 or bt8.dim() != 3:
+        raise ValueError("a8 and bt8 must be (Z, M, K) and (Z, N, K)")
+    for name, t in (("a8", a8), ("bt8", bt8)):
+        if t.dtype not in (torch.float8_e4m3fn, torch.uint8) or not t.is_contiguous():
+            raise TypeError(f"{name} must be contiguous e4m3fn codes")
+    Z, M, K = a8.shape
+    Zb, N, Kb = bt8.shape
+    if Zb != Z or Kb != K:
+        raise ValueError(f"shapes disagree: a8 {tuple(a8.shape)}, bt8 {tuple(bt8.shape)}")
+    rs = row_scale.to(torch.float32).contiguous()
+    cs = col_scale.to(torch.float32).contiguous()
+    if rs.shape != (Z, M) or cs.shape != (Z, N):
+        raise ValueError(f"row_scale must be ({Z}, {M}) and col_scale ({Z}, {N})")
+    if N % 4 != 0:
+        raise ValueError(f"N = {N} must be a multiple of 4")
+    out = torch.empty((Z, M, N), dtype=torch.bfloat16, device=a8.device)
+    C.check(C.lib().rp_fp8_gemm_rowwise(a8.data_ptr(), bt8.data_ptr(), C.RP_B_NK, out.data_ptr(),
+                                        M, N, K, K, K, N, rs.data_ptr(), cs.data_ptr(), Z, M * K,
+                                        N * K, M * N, M, N, _stream(a8)), "rp_fp8_gemm_rowwise")
+    return out
+
+
+def softmax_rowwise_quantize(scores: torch.Tensor, scale: float, causal: bool = False
+                             ) -> tuple[torch.Tensor, torch.Tensor]:
+    """(dequant (Z, Sq) fp32, P codes (Z, Sq, Skv) e4m3fn) of
+    P = softmax(bf16(scores * scale)) in bf16 (causal: key j visible to query
+    q iff j <= q), row-wise quantized -- the reference's ``scores * scale``,
+    masked_fill, torch.softmax and ``_rowwise_quantize(p)``
+    (fp8_scaled_mm.py:159-171) in one pass per row."""
+    _check_bf16("scores", scores)
+    if scores.dim() != 3 or not scores.is_contiguous():
+        raise ValueError("scores must be a contiguous (Z, Sq, Skv) tensor")
+    Z, Sq, Skv = scores.shape
+    dq = torch.empty((Z, Sq), dtype=torch.float32, device=scores.device)
+    codes = torch.empty((Z, Sq, Skv), dtype=torch.uint8, device=scores.device)
+    C.check(C.lib().rp_fp8_softmax_rowwise_quantize(scores.data_ptr(), Z * Sq, Skv, Skv, Sq,
+                                                    int(causal), float(scale), dq.data_ptr(),
+                                                    codes.data_ptr(), Skv, _stream(scores)),
+            "rp_fp8_softmax_rowwise_quantize")
+    return dq, codes.view(torch.float8_e4m3fn)
+
+
+def fp8_scaled_mm_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *,
+                            causal: bool = False, scale: float | None = None) -> torch.Tensor:
+    """The unfused FP8 attention of the reference's ``FP8ScaledMMAttention``
+    (fp8_scaled_mm.py:135-221) on the gfx950 kernels, (B, H, S, D) bf16 or
+    fp16 in, q's dtype out: row-wise Q and K codes, scores = the row-scaled
+    FP8 GEMM in bf16, P = softmax(scores * scale) in bf16 with its row-wise
+    codes, V^T's row-wise codes (one scale per head-dim index), and the
+    row-scaled P.V GEMM.  The (B*H, Sq, Skv) bf16 scores are materialised,
+    as in the reference."""
+    for name, t in (("q", q), ("k", k), ("v", v)):
+        _in_dtype(name, t)
+    if q.dim() != 4 or k.shape != v.shape or k.shape[0] != q.shape[0] or \
+            k.shape[1] != q.shape[1] or k.shape[3] != q.shape[3]:
+        raise ValueError(f"shape mismatch: q {tuple(q.shape)}, k {tuple(k.shape)}, "
+                         f"v {tuple(v.shape)}")
+    b, h, sq, d = q.shape
+    skv = k.shape[2]
+    bh = b * h
+    if scale is None:
+        scale = 1.0 / math.sqrt(d)
+    cdt = torch.bfloat16     # the reference computes in bf16 (fp8_scaled_mm.py:146-149)
+    qs, q8 = rowwise_quantize(q.to(cdt).reshape(bh, sq, d))
+    ks, k8 = rowwise_quantize(k.to(cdt).reshape(bh, skv, d))
+    scores = gemm_rowwise(q8.view(torch.uint8), k8.view(torch.uint8), qs, ks)
+    ps, p8 = softmax_rowwise_quantize(scores, scale, causal)
+    del scores
+    vt = transpose16(v.to(cdt).reshape(bh, skv, d))          # (bh, d, skv)
+    vs, vt8 = rowwise_quantize(vt)
+    out = gemm_rowwise(p8.view(torch.uint8), vt8.view(torch.uint8), ps, vs)
+    return out.reshape(b, h, sq, d).to(q.dtype)
+
+
 def selftest_e4m3(x: torch.Tensor) -> torch.Tensor:
     """Device e4m3fn code of clamp(x, -448, 448) for fp32 x (pins the hardware cvt)."""
     _check_cuda("x", x)

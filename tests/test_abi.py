@@ -222,3 +222,25 @@ def test_qkv_quantizer_argument_checks() -> None:
     assert L.rp_fp8_scale_quantize_qkv(*bad) == 1 and "dtype" in L.rp_last_error().decode()
     bad = list(args); bad[23] = 100                      # ldv < Skv
     assert L.rp_fp8_scale_quantize_qkv(*bad) == 2 and "ldv" in L.rp_last_error().decode()
+
+
+def test_rowwise_argument_checks() -> None:
+    """The row-wise entry points check their arguments before any launch."""
+    L = _capi.lib()
+    bf16 = _capi.RP_DTYPE_BF16
+    assert L.rp_fp8_rowwise_quantize(None, bf16, 4, 64, 64, FAKE, FAKE, 64, None) == 1
+    assert L.rp_fp8_rowwise_quantize(FAKE, 7, 4, 64, 64, FAKE, FAKE, 64, None) == 1
+    assert L.rp_fp8_rowwise_quantize(FAKE, bf16, 4, 60, 64, FAKE, FAKE, 64, None) == 2
+    assert "multiples of 8" in L.rp_last_error().decode()
+    assert L.rp_fp8_rowwise_quantize(FAKE, bf16, 4, 64, 32, FAKE, FAKE, 64, None) == 1
+    assert L.rp_transpose16(FAKE, FAKE, 1, 8, 8, 4, 8, 64, 64, None) == 1
+    assert L.rp_fp8_softmax_rowwise_quantize(FAKE, 4, 63, 64, 4, 0, 0.1, FAKE, FAKE, 64,
+                                             None) == 2
+    assert L.rp_fp8_softmax_rowwise_quantize(FAKE, 4, 64, 64, 4, 0, float("nan"), FAKE, FAKE,
+                                             64, None) == 1
+    # row-wise GEMM: both scale vectors, aligned column scales, a sane batch
+    args = (FAKE, FAKE, _capi.RP_B_NK, FAKE, 64, 64, 64, 64, 64, 64)
+    assert L.rp_fp8_gemm_rowwise(*args, None, FAKE, 1, 0, 0, 0, 0, 0, None) == 1
+    assert L.rp_fp8_gemm_rowwise(*args, FAKE, FAKE + 4, 1, 0, 0, 0, 0, 0, None) == 1
+    assert L.rp_fp8_gemm_rowwise(*args, FAKE, FAKE, 0, 0, 0, 0, 0, 0, None) == 2
+    assert L.rp_fp8_gemm_rowwise(*args, FAKE, FAKE, 2, 8, 0, 0, 0, 0, None) == 2

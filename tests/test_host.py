@@ -128,8 +128,13 @@ _SELECT = (
 
 @pytest.mark.parametrize("env,want", [
     ({}, "naive-sdpa naive-sdpa naive-sdpa"),
-    ({"REPERCEP_FP8_ATTENTION": "1"}, "fp8-hip-flash naive-sdpa naive-sdpa"),
+    # the fused kernel where it qualifies (Skv >= 128), the unfused scaled-mm
+    # op below that, the floor on other vendors (reference registry.py:84-92)
+    ({"REPERCEP_FP8_ATTENTION": "1"}, "fp8-hip-flash fp8-hip-scaled-mm naive-sdpa"),
     ({"REPERCEP_FP8_ATTENTION": "triton"}, "fp8-hip-flash naive-sdpa naive-sdpa"),
+    # scaled_mm: the unfused op only -- its 4 GiB scores cap rules out the Wan shape
+    ({"REPERCEP_FP8_ATTENTION": "scaled_mm"}, "naive-sdpa fp8-hip-scaled-mm naive-sdpa"),
+    ({"REPERCEP_FP8_ATTENTION": "te"}, "naive-sdpa naive-sdpa naive-sdpa"),
     ({"REPERCEP_FP8_ATTENTION": "off"}, "naive-sdpa naive-sdpa naive-sdpa"),
 ])
 def test_registry_env_selection(env: dict, want: str) -> None:
@@ -243,3 +248,27 @@ def test_traffic_profile_is_well_formed() -> None:
         k["hbm_write_bytes_per_launch"]
     # the kernel writes the bf16 output once: 40 x 75600 x 128 x 2 bytes
     assert abs(k["hbm_write_bytes_per_launch"] - 774_144_000) < 1e6
+
+
+def test_scaled_mm_op_contract() -> None:
+    """FP8HipScaledMMAttention keeps the reference's supports() rules
+    (src/repercep/attention/fp8_scaled_mm.py:87-105): head dims {64, 96, 128,
+    192, 256}, FULL/CAUSAL, lengths >= 16 and multiples of 16, bf16 scores at
+    most 4 GiB."""
+    from repercep_runtime_amd.attention import AttentionOp, FP8HipScaledMMAttention
+    from repercep_runtime_amd.attention.types import AttentionKind
+
+    op = FP8HipScaledMMAttention()
+    assert isinstance(op, AttentionOp) and op.name == "fp8-hip-scaled-mm"
+    assert op.available        # the library loads on a CPU host too
+    ok = AttentionShape(1, 4, 512, 512, 128)
+    assert op.supports(ok, DType.BF16) and op.supports(ok, DType.FP16)
+    assert not op.supports(ok, DType.FP32)
+    assert not op.supports(AttentionShape(1, 4, 512, 512, 32), DType.BF16)
+    assert op.supports(AttentionShape(1, 4, 512, 512, 96), DType.BF16)
+    assert not op.supports(AttentionShape(1, 4, 520, 512, 128), DType.BF16)
+    assert not op.supports(AttentionShape(1, 4, 8, 8, 128), DType.BF16)
+    assert not op.supports(AttentionShape(1, 4, 512, 512, 128, kind=AttentionKind.NEIGHBORHOOD),
+                           DType.BF16)
+    assert op.supports(AttentionShape(1, 1, 46336, 46336, 128), DType.BF16)   # 4.0 GiB
+    assert not op.supports(AttentionShape(1, 1, 46352, 46352, 128), DType.BF16)
