@@ -6,9 +6,10 @@ The oracle runs with the kernel's key-tile width (BLOCK_N = 128) because the
 running max after each tile sets P's quantization grid.
 
 Tolerances: BASELINE.json's max-abs 2e-2 / mean-abs 2e-3 against the
-torch-emulated FP8 result (scaled by the output's peak magnitude when that
-exceeds 1, see tests/_helpers.baseline_tolerance), plus a relative mean error
-bound of 1e-2: the kernel and the oracle run the same algorithm, so they differ
+torch-emulated FP8 result -- scaled by the output's peak magnitude only in
+the tests that declare ``scaled=True`` because their outputs exceed 1 by
+construction (see tests/_helpers.baseline_tolerance) -- plus a relative mean
+error bound of 1e-2: the kernel and the oracle run the same algorithm, so they differ
 only by fp32 rounding (exp2 vs exp, summation order) and the rare P code
 that rounding flips.
 """
@@ -49,10 +50,17 @@ def _oracle_rows(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, heads: list[
     return np.stack(outs), {"q8": q8, "k8": k8, "v8": v8, "qs": qs, "ks": ks, "vs": vs}
 
 
-def _check(got: np.ndarray, ref: np.ndarray, what: str, rel_tol: float = REL_TOL) -> dict:
+def _check(got: np.ndarray, ref: np.ndarray, what: str, rel_tol: float = REL_TOL,
+           scaled: bool = False) -> dict:
+    """BASELINE's absolute bounds (max-abs 2e-2, mean-abs 2e-3) and the
+    relative mean bound.  ``scaled=True`` -- declared only by tests whose
+    outputs exceed 1 by construction (a handful of keys, peaked rows) --
+    scales the absolute bounds by the output's peak (see
+    tests/_helpers.baseline_tolerance); the relative bound never scales."""
     st = err_stats(got, ref)
-    max_tol, mean_tol = baseline_tolerance(ref)
-    print(f"{what}: {st} (tol max {max_tol:.3g}, mean {mean_tol:.3g})", flush=True)
+    max_tol, mean_tol = baseline_tolerance(ref) if scaled else (2e-2, 2e-3)
+    print(f"{what}: {st} (tol max {max_tol:.3g}, mean {mean_tol:.3g}"
+          f"{', scaled by the output peak' if scaled else ''})", flush=True)
     assert np.isfinite(got).all(), f"{what}: non-finite output"
     assert st["max_abs"] <= max_tol, f"{what}: {st}"
     assert st["mean_abs"] <= mean_tol, f"{what}: {st}"
@@ -215,7 +223,8 @@ def test_per_tensor_granularity(gpu: torch.device) -> None:
                                   out_dtype=torch.float32).cpu().numpy()[0]
     ref, _ = _oracle_rows(q, k, v, [0, 1, 2, 3], np.arange(600), sm_scale=128 ** -0.5,
                           granularity="tensor")
-    _check(out, ref, "per-tensor")
+    # V = 3 N(0, 1): outputs reach ~3, so one flipped P code moves them ~3x more
+    _check(out, ref, "per-tensor", scaled=True)
 
 
 def test_custom_softmax_scale(gpu: torch.device) -> None:
@@ -224,7 +233,8 @@ def test_custom_softmax_scale(gpu: torch.device) -> None:
     out = ops.fp8_flash_attention(q.to(gpu), k.to(gpu), v.to(gpu), scale=0.3,
                                   out_dtype=torch.float32).cpu().numpy()[0]
     ref, _ = _oracle_rows(q, k, v, [0, 1], np.arange(256), sm_scale=0.3)
-    _check(out, ref, "scale=0.3")
+    # 2.4x the default temperature: peaked rows whose outputs exceed 1
+    _check(out, ref, "scale=0.3", scaled=True)
 
 
 def test_shared_prefix_candidates_c5(gpu: torch.device) -> None:
@@ -235,6 +245,31 @@ def test_shared_prefix_candidates_c5(gpu: torch.device) -> None:
     ref, _ = _oracle_rows(q, k, v, list(range(C5.H)), np.arange(C5.Sq),
                           sm_scale=C5.D ** -0.5, mask=2, prefix=C5.prefix, suffix=C5.suffix)
     _check(out.cpu().numpy()[0], ref, "c5 shared prefix")
+
+
+def test_shared_prefix_candidates_are_isolated_on_gpu(gpu: torch.device) -> None:
+    """C5 layout: exchanging two candidates' suffix keys and values (a
+    permutation: scales and codes of everything else unchanged) leaves every
+    other candidate's kernel output bit-identical and changes the two
+    exchanged ones -- a candidate attends to the shared prefix and its own
+    suffix only."""
+    q, k, v = attn_inputs(C5)
+    P, L = C5.prefix, C5.suffix
+    n_cand = C5.Sq // L
+    a, b = 2, 11
+    idx = torch.arange(C5.Skv)
+    ia = torch.arange(P + a * L, P + (a + 1) * L)
+    ib = torch.arange(P + b * L, P + (b + 1) * L)
+    idx[ia], idx[ib] = ib, ia
+    run = lambda kk, vv: ops.fp8_flash_attention(  # noqa: E731
+        q.to(gpu), kk.to(gpu), vv.to(gpu), prefix_len=P, suffix_len=L,
+        out_dtype=torch.float32, kv_splits=1).cpu()
+    base = run(k, v)
+    swapped = run(k[:, :, idx], v[:, :, idx])
+    for c in range(n_cand):
+        rows = slice(c * L, (c + 1) * L)
+        same = torch.equal(swapped[:, :, rows], base[:, :, rows])
+        assert same == (c not in (a, b)), c
 
 
 SPLIT_CASES = [
@@ -633,4 +668,5 @@ def test_softmax_extremes_vs_oracle(gpu: torch.device, kind: str) -> None:
     out = ops.fp8_flash_attention(q.to(gpu), k.to(gpu), v.to(gpu),
                                   out_dtype=torch.float32).cpu().numpy()[0]
     ref, _ = _oracle_rows(q, k, v, list(range(H)), np.arange(S), sm_scale=D ** -0.5)
-    _check(out, ref, f"{kind} (1, {H}, {S}, {D})")
+    # both kinds make peaked rows (one or a few dominant keys): outputs exceed 1
+    _check(out, ref, f"{kind} (1, {H}, {S}, {D})", scaled=True)

@@ -241,3 +241,73 @@ def test_key_split_merge_is_exact_softmax_without_pquant(mask: int, Sq: int, Skv
                                             mask=mask, prefix=prefix, suffix=suffix)
     assert np.isfinite(got).all()
     assert np.abs(got - ref).max() / np.abs(ref).max() < 2e-5
+
+
+# --------------------------------------------------- shared-prefix mask
+def _block_mask(prefix: int, n_cand: int, suffix: int) -> np.ndarray:
+    """The shared-prefix candidate mask built from its block structure (the
+    token-VLA decode layout of BASELINE config 5): every query sees the whole
+    prefix, and candidate c's queries (rows c*suffix ..) see their own suffix
+    block causally -- a lower triangle on the block diagonal -- and nothing
+    of the other candidates."""
+    Sq, Skv = n_cand * suffix, prefix + n_cand * suffix
+    m = np.zeros((Sq, Skv), dtype=bool)
+    m[:, :prefix] = True
+    tri = np.tril(np.ones((suffix, suffix), dtype=bool))
+    for c in range(n_cand):
+        rows = slice(c * suffix, (c + 1) * suffix)
+        m[rows, prefix + c * suffix: prefix + (c + 1) * suffix] = tri
+    return m
+
+
+@pytest.mark.parametrize("prefix,n_cand,suffix", [(512, 16, 8), (16, 3, 8), (5, 4, 3),
+                                                  (0, 2, 4), (7, 1, 1)])
+def test_shared_prefix_mask_is_the_block_structure(prefix: int, n_cand: int, suffix: int) -> None:
+    Sq, Skv = n_cand * suffix, prefix + n_cand * suffix
+    got = attention.visible(np.arange(Sq), np.arange(Skv), 2, prefix, suffix)
+    assert np.array_equal(got, _block_mask(prefix, n_cand, suffix))
+
+
+def test_block_structure_catches_a_candidate_swap() -> None:
+    """Negative control: a mask that gives candidate c the suffix block of
+    candidate c+1 (same visible-pair count) differs from the block structure."""
+    prefix, n_cand, suffix = 16, 3, 8
+    Sq, Skv = n_cand * suffix, prefix + n_cand * suffix
+    q, kv = np.arange(Sq)[:, None], np.arange(Skv)[None, :]
+    j = kv - prefix
+    swapped = (kv < prefix) | ((j >= 0) & (j // suffix == (q // suffix + 1) % n_cand)
+                               & (j % suffix <= q % suffix))
+    assert swapped.sum() == _block_mask(prefix, n_cand, suffix).sum()
+    assert not np.array_equal(swapped, _block_mask(prefix, n_cand, suffix))
+
+
+def test_shared_prefix_candidates_are_isolated() -> None:
+    """Through the attention oracle: exchanging two candidates' suffix keys
+    and values leaves every other candidate's output unchanged bit for bit and
+    changes the two exchanged ones; the first query of a candidate equals
+    attention over the prefix plus that candidate's first suffix key."""
+    prefix, n_cand, suffix, D = 32, 4, 8, 64
+    Sq, Skv = n_cand * suffix, prefix + n_cand * suffix
+    rng = np.random.default_rng(12)
+    q8 = quant.encode_e4m3fn(rng.normal(size=(Sq, D)) * 8)
+    k8 = quant.encode_e4m3fn(rng.normal(size=(Skv, D)) * 8)
+    v8 = quant.encode_e4m3fn(rng.normal(size=(Skv, D)) * 8)
+    args = (0.02, 0.02, 0.03, D ** -0.5)
+    base = attention.emulate(q8, k8, v8, *args, mask=2, prefix=prefix, suffix=suffix)
+    a, b = 1, 3
+    idx = np.arange(Skv)
+    sa = slice(prefix + a * suffix, prefix + (a + 1) * suffix)
+    sb = slice(prefix + b * suffix, prefix + (b + 1) * suffix)
+    idx[sa], idx[sb] = np.arange(Skv)[sb], np.arange(Skv)[sa]
+    swapped = attention.emulate(q8, k8[idx], v8[idx], *args, mask=2, prefix=prefix,
+                                suffix=suffix)
+    for c in range(n_cand):
+        rows = slice(c * suffix, (c + 1) * suffix)
+        same = np.array_equal(swapped[rows], base[rows])
+        assert same == (c not in (a, b)), c
+    for c in range(n_cand):
+        keep = np.r_[np.arange(prefix), prefix + c * suffix]
+        first = attention.emulate(q8[[c * suffix]], k8[keep], v8[keep], *args, block_n=Skv)
+        ref = attention.emulate(q8, k8, v8, *args, rows=np.array([c * suffix]), mask=2,
+                                prefix=prefix, suffix=suffix, block_n=Skv)
+        np.testing.assert_allclose(first, ref, rtol=1e-6, atol=1e-7)
