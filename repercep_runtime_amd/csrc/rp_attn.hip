@@ -321,11 +321,11 @@ __device__ __forceinline__ i32x8 lds_op(uint32_t lds_addr) {
 // register sets, kRing-1 MFMAs ahead of their use.  Consecutive MFMAs write
 // different accumulators, so none waits for its predecessor's result.
 //
-// Before the stream, O^T *= alpha(i-1): the rescale owed since the previous
-// phase's row max, skipped when no row of the wave raised its max.  Between
-// the MFMAs the wave issues the phase's other work, which would otherwise
-// wait for the stream to drain:
-//   during S^T:  the loads of tile i+1 (LOADS);
+// Between the MFMAs the wave issues the phase's other work, which would
+// otherwise wait for the stream to drain:
+//   during S^T:  the loads of tile i+1 (LOADS) and O^T *= alpha(i-1), the
+//                rescale owed since the previous phase's row max (skipped
+//                when no row of the wave raised its max);
 //   during PV:   partial row maxima of S^T(i) (MAX), 64 / NP scores per step.
 constexpr int kRing = 3;
 
@@ -350,10 +350,14 @@ __device__ __forceinline__ void mfma_phase(uint32_t kl, uint32_t vl,
     const int u = t - NS, e = u % G::ETILES, m = u / G::ETILES;
     return vl + 32 * e * G::V_PITCH + 64 * m;
   };
-  if (__any(alpha_prev != 1.0f)) {
-#pragma unroll
-    for (int e = 0; e < G::ETILES; ++e) acc[e] *= alpha_prev;
-  }
+  // O^T *= alpha(i-1), unless no lane of the wave raised its max (the vote
+  // is one SGPR branch per S^T step): the multiplies are spread between the
+  // S^T MFMAs, which do not read O^T, so they run in the MFMAs' shadow and
+  // finish before the first P.V MFMA.  (Done up front, they delayed that
+  // MFMA stream by their own issue time: 1.4% slower at the Wan shape.)
+  constexpr int RPS = G::ETILES * 16 / NS;   // rescale multiplies per S^T step
+  static_assert(RPS * NS == G::ETILES * 16, "rescale spread");
+  const bool rescale = __any(alpha_prev != 1.0f);
   i32x8 ring[kRing];
 #pragma unroll
   for (int t = 0; t < kRing - 1; ++t) ring[t] = lds_op(addr(t));
@@ -369,6 +373,10 @@ __device__ __forceinline__ void mfma_phase(uint32_t kl, uint32_t vl,
 #pragma unroll
         for (int n = t * NLD / NS; n < (t + 1) * NLD / NS; ++n)
           issue_slot<DK, DV, 4, false>(n, L, dst);
+      }
+      if (rescale) {
+#pragma unroll
+        for (int v = t * RPS; v < (t + 1) * RPS; ++v) acc[v / 16][v % 16] *= alpha_prev;
       }
     } else {
       const int u = t - NS, e = u % G::ETILES, m = u / G::ETILES;
@@ -431,14 +439,19 @@ void attn_fwd_kernel(AttnArgs a) {
   // of BLOCK_M rows (the block being switched to, and the one after)
   constexpr int Q_BYTES = MULTI ? BLOCK_M * DK : 0;
   constexpr int Q_LOADS = Q_BYTES / 1024 / 4;   // per loading wave
-  static_assert(G::LDS_BYTES + 2 * Q_BYTES <= 160 * 1024, "LDS");
-  __shared__ __attribute__((aligned(1024))) uint8_t smem[G::LDS_BYTES + 2 * Q_BYTES];
-  uint8_t* const kbuf = smem;                              // K_STAGES x K_BYTES
-  uint8_t* const vbuf = smem + G::K_STAGES * G::K_BYTES;   // V_STAGES x V_BYTES
+  // K and V^T stages.  (Three and four, loading each tile one step earlier,
+  // measured 6% slower at the Wan shape: the tile loads' latency is hidden.)
+  constexpr int KST = 2, VST = 3;
+  constexpr int NLD = TileLoads<DK, DV, 4>::N;
+  constexpr int LDS_TILES = KST * G::K_BYTES + VST * G::V_BYTES;
+  static_assert(LDS_TILES + 2 * Q_BYTES <= 160 * 1024, "LDS");
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[LDS_TILES + 2 * Q_BYTES];
+  uint8_t* const kbuf = smem;                        // KST x K_BYTES
+  uint8_t* const vbuf = smem + KST * G::K_BYTES;     // VST x V_BYTES
   // the same two regions as LDS byte addresses, for the direct-to-LDS loads
   const uint32_t kbuf_lds = (uint32_t)(uintptr_t)(lds_ptr_t)smem;
-  const uint32_t vbuf_lds = kbuf_lds + G::K_STAGES * G::K_BYTES;
-  const uint32_t qbuf_lds = kbuf_lds + G::LDS_BYTES;   // multi-block launches only
+  const uint32_t vbuf_lds = kbuf_lds + KST * G::K_BYTES;
+  const uint32_t qbuf_lds = kbuf_lds + LDS_TILES;   // multi-block launches only
 
   // ---- work item (XCD-aware remap of the linear workgroup id)
   const int w = blockIdx.x;
@@ -528,19 +541,20 @@ void attn_fwd_kernel(AttnArgs a) {
     t.kt = kh + (int64_t)kbeg * D;
     t.vt = vh + kbeg;
     t.klim = a.Skv - 1 - kbeg;
-    t.kst = kbuf_lds + (stage & 1) * G::K_BYTES;
-    t.vst = vbuf_lds + (stage % 3) * G::V_BYTES;
+    t.kst = kbuf_lds + (stage % KST) * G::K_BYTES;
+    t.vst = vbuf_lds + (stage % VST) * G::V_BYTES;
     return t;
   };
   if (group == 0) {
     const TileDst t0 = tile_dst(0, 0);
 #pragma unroll
-    for (int n = 0; n < TileLoads<DK, DV, 4>::N; ++n) issue_slot<DK, DV, 4, true>(n, tl, t0);
+    for (int n = 0; n < NLD; ++n) issue_slot<DK, DV, 4, true>(n, tl, t0);
   }
-  // V^T stage 2 is read (times P = 0) by the first MFMA phase before tile 2
-  // lands there: clear it so that no stale NaN code can reach the accumulator.
+  // V^T stage VST-1 is read (times P = 0) by the first MFMA phase before
+  // tile VST-1 lands there: clear it so that no stale NaN code can reach the
+  // accumulator.
   for (int o = tid * 16; o < G::V_BYTES; o += G::THREADS * 16)
-    *reinterpret_cast<i32x4*>(vbuf + 2 * G::V_BYTES + o) = i32x4{0, 0, 0, 0};
+    *reinterpret_cast<i32x4*>(vbuf + (VST - 1) * G::V_BYTES + o) = i32x4{0, 0, 0, 0};
 
   // ---- Q^T operand (B operand of S^T), resident for the whole kernel
   auto load_q = [&](i32x8 (&dst)[G::KSTEPS], int qrow) {
@@ -691,8 +705,8 @@ void attn_fwd_kernel(AttnArgs a) {
       const bool tail = kv0 + kBlockN > a.Skv;
       // operand base addresses of this phase's K and V^T stages; opaque to
       // the compiler, so every read is one register plus an immediate
-      uint32_t kl = kbuf_lds + (i & 1) * G::K_BYTES + k_base;
-      uint32_t vl = vbuf_lds + ((i + 2) % 3) * G::V_BYTES + v_base;
+      uint32_t kl = kbuf_lds + (i % KST) * G::K_BYTES + k_base;
+      uint32_t vl = vbuf_lds + ((i + VST - 1) % VST) * G::V_BYTES + v_base;
       asm("" : "+v"(kl), "+v"(vl));
       // group 0 issues tile i+1; past the last tile it re-reads the last one
       // into the stages tile i+1 would use, which are free (see above)
