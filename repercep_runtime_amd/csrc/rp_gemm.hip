@@ -300,26 +300,29 @@ void gemm_kernel(GemmArgs g) {
 // v_mfma_f32_32x32x64_f8f6f4, four waves (one per SIMD) of 128 x 128 each,
 // accumulators in AGPRs.  Operands reach LDS by global_load_lds_dwordx4 (no
 // VGPR staging) in K slices of 128 bytes -- eight lanes read one row's whole
-// cache line -- double-buffered: slice k+2 loads while slices k and k+1 are
-// read, with one wait and barrier per slice.  Each slice is two MFMA depths
-// (sub-slices of 64 bytes); operands are double-buffered in registers a
-// sub-slice ahead.  LDS rows are unpadded; the eight 16-byte granules of a
-// row are XOR-swizzled by (row >> 1) & 7, so the 16-lane ds_read_b128 groups
-// are conflict-free.  The MFMA computes C^T tiles (A operand = rows of B^T,
-// B operand = rows of A), so each lane ends with 4 consecutive output
-// columns of one row per register group: one 8-byte bf16 store.
+// cache line -- through a ring of five 32 KiB slots, each holding the A or
+// the B^T part of one slice: while slice k is multiplied, slice k+1 lands and
+// slice k+2 loads, its A part during the first half of slice k and its B^T
+// part during the second, so the loads leave at an even rate (issuing a
+// whole slice at once measured 4% slower).  One wait and barrier per slice.
+// Each slice is two MFMA depths (sub-slices of 64 bytes); operands are
+// double-buffered in registers a sub-slice ahead.  LDS rows are unpadded;
+// the eight 16-byte granules of a row are XOR-swizzled by (row >> 1) & 7, so
+// the 16-lane ds_read_b128 groups are conflict-free.  The MFMA computes C^T
+// tiles (A operand = rows of B^T, B operand = rows of A); the epilogue
+// re-stages the bf16 tile through LDS so that each output row leaves as one
+// 256-byte run.
 constexpr int kG2Threads = 256;
 constexpr int kG2Tile = 256;                        // BM = BN
 constexpr int kG2K = 128;                           // K bytes per slice (two MFMA depths)
 constexpr int kG2Sub = 64;                          // K bytes per MFMA (a sub-slice)
 constexpr int kG2Pitch = kG2K;                      // LDS row pitch (no pad)
 constexpr int kG2Half = kG2Tile * kG2Pitch;         // A (or B^T) part of a stage
-constexpr int kG2Stage = 2 * kG2Half;
-constexpr int kG2Stages = 2;
-constexpr int kG2Loads = kG2Stage / 1024 / 4;       // 1 KiB loads per wave per slice
+constexpr int kG2Slots = 5;                         // LDS ring of slice halves (A or B^T)
+constexpr int kG2Loads = 2 * kG2Half / 1024 / 4;    // 1 KiB loads per wave per slice
 constexpr int kG2ALoads = kG2Half / 1024 / 4;       // of which A
 static_assert(kG2Half % 4096 == 0, "A and B^T parts split evenly over the waves");
-static_assert(kG2Stages * kG2Stage <= 160 * 1024, "LDS");
+static_assert(kG2Slots * kG2Half <= 160 * 1024, "LDS");
 
 #pragma clang diagnostic push
 #pragma clang diagnostic ignored "-Winline-asm"
@@ -329,7 +332,8 @@ static_assert(kG2Stages * kG2Stage <= 160 * 1024, "LDS");
 // Inline asm keeps the load out of the compiler's waitcnt bookkeeping,
 // which would otherwise order every later ds_read behind it; the kernel
 // waits for its loads explicitly (vmcnt) before the barrier that precedes
-// their first read.  Nothing else in this kernel uses M0.
+// their first read.  Nothing else in this kernel uses M0.  (The buffer-
+// resource form of this load measured 4-8% slower at the Wan FFN shape.)
 __device__ __forceinline__ void g2_gload_lds16_s(const void* base, uint32_t voff,
                                                  uint32_t lds_block) {
   // readfirstlane states the uniformity where the compiler cannot prove it
@@ -374,6 +378,8 @@ struct G2Ops {
 };
 
 typedef int i32x2 __attribute__((ext_vector_type(2)));
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
 // ds_read_b64_tr_b8: each group of 16 lanes reads an 8 x 16 byte block --
 // lane i supplies the address of bytes 8(i%2) .. 8(i%2)+7 of row i/2 -- and
@@ -402,7 +408,7 @@ __device__ __forceinline__ i32x8 kn_operand(uint32_t base) {
 template <bool KN>
 __global__ __launch_bounds__(kG2Threads) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void gemm256_kernel(GemmArgs g) {
-  __shared__ __attribute__((aligned(1024))) uint8_t smem[kG2Stages * kG2Stage];
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[kG2Slots * kG2Half];
   const uint32_t smem_lds = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)smem;
 
   gemm_batch(g);
@@ -431,8 +437,8 @@ void gemm256_kernel(GemmArgs g) {
   const int lq = lane & 31, lg = lane >> 5;
   const int wm = wave >> 1, wn = wave & 1;
 
-  // This lane's direct-to-LDS loads: load n fills LDS KiB block n*4 + wave
-  // of a stage; blocks [0, kG2Half/1024) hold A rows, the rest B.
+  // This lane's direct-to-LDS loads: load n fills KiB block (n % 8) * 4 +
+  // wave of a slot; loads 0..7 the A part, 8..15 the B^T part.
   // A and (N, K) B^T: eight consecutive lanes read one row's 128-byte K slice
   // (a whole cache line); LDS granule `slot` of row r holds K granule
   // slot ^ ((r >> 1) & 7).  Rows past M or N re-read the last row (their
@@ -477,7 +483,8 @@ void gemm256_kernel(GemmArgs g) {
   const uint32_t tail_back = (uint32_t)(((lane >> 2) ^ wave) & 1) * 64;
   // (K, N) B: loads n >= kG2ALoads + 4 fill K rows 64..127 of the slice
   const uint32_t tail_back_kn = (uint32_t)(64 * g.ldb);
-  auto issue = [&](int n, int kk) __attribute__((always_inline)) {
+  // load n of slice kk into `slot`
+  auto issue = [&](int n, int kk, int slot) __attribute__((always_inline)) {
     uint32_t off = gofs[n];
     const bool is_a = n < kG2ALoads;
     if (half_tail && kk == nslice - 1) {
@@ -487,10 +494,10 @@ void gemm256_kernel(GemmArgs g) {
     const uint8_t* src = is_a ? abase + (int64_t)kk * kG2K
                               : bbase + (int64_t)kk * kG2K * (KN ? g.ldb : 1);
     g2_gload_lds16_s(src, off,
-                     smem_lds + (uint32_t)((kk & 1) * kG2Stage + (n * 4 + wave) * 1024));
+                     smem_lds + (uint32_t)(slot * kG2Half + ((n % kG2ALoads) * 4 + wave) * 1024));
   };
 
-  // Per-lane operand offsets inside a stage: row lq of each 32-row block,
+  // Per-lane operand offsets inside a slot: row lq of each 32-row block,
   // K granules 4h + 2lg and 4h + 2lg + 1 of sub-slice h at their swizzled
   // slots (the swizzle term (row >> 1) & 7 depends on lq only, as block
   // bases are multiples of 32 rows).  Sixteen consecutive lanes then hit
@@ -499,7 +506,7 @@ void gemm256_kernel(GemmArgs g) {
   const int h00 = ((2 * lg) ^ swz) * 16, h01 = ((2 * lg + 1) ^ swz) * 16;
   const int h10 = ((4 + 2 * lg) ^ swz) * 16, h11 = ((4 + 2 * lg + 1) ^ swz) * 16;
   const int a_off = (wm * 128 + lq) * kG2Pitch;
-  const int b_off = kG2Half + (wn * 128 + lq) * kG2Pitch;
+  const int b_off = (wn * 128 + lq) * kG2Pitch;
   // (K, N) B: per-lane LDS offsets of the four B^T operands' transpose reads
   // (see kn_operand); sub-slice h adds 64 K rows, an immediate
   uint32_t kn_off[4];
@@ -509,7 +516,7 @@ void gemm256_kernel(GemmArgs g) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int gr = 8 * wn + 2 * j + ((lane >> 4) & 1);
-      kn_off[j] = (uint32_t)(kG2Half + row * kG2Tile + ((gr ^ (i & 14)) << 4) + 8 * (i & 1));
+      kn_off[j] = (uint32_t)(row * kG2Tile + ((gr ^ (i & 14)) << 4) + 8 * (i & 1));
     }
   }
   auto b_op = [&](const uint8_t* st, int j, int h, int c0, int c1) __attribute__((always_inline)) {
@@ -520,6 +527,7 @@ void gemm256_kernel(GemmArgs g) {
       return g2_op(st + b_off + 32 * j * kG2Pitch, c0, c1);
     }
   };
+  auto wrap = [](int x) { return x >= kG2Slots ? x - kG2Slots : x; };
 
   f32x16 acc[4][4];
 #pragma unroll
@@ -527,12 +535,14 @@ void gemm256_kernel(GemmArgs g) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = f32x16{};
 
-  // prologue: slices 0 and 1 in flight, wait for slice 0, read sub-slice 0
+  // Slice kk's A part sits in slot 2kk % 5 and its B^T part in slot
+  // (2kk + 1) % 5.  prologue: slices 0 and 1 in flight, wait for slice 0,
+  // read sub-slice 0
 #pragma unroll
-  for (int n = 0; n < kG2Loads; ++n) issue(n, 0);
+  for (int n = 0; n < kG2Loads; ++n) issue(n, 0, n < kG2ALoads ? 0 : 1);
   if (nslice > 1) {
 #pragma unroll
-    for (int n = 0; n < kG2Loads; ++n) issue(n, 1);
+    for (int n = 0; n < kG2Loads; ++n) issue(n, 1, n < kG2ALoads ? 2 : 3);
     g2_wait_vmem<kG2Loads>();
   } else {
     g2_wait_vmem<0>();
@@ -542,36 +552,47 @@ void gemm256_kernel(GemmArgs g) {
 #pragma unroll
   for (int i = 0; i < 4; ++i) o0.a[i] = g2_op(smem + a_off + 32 * i * kG2Pitch, h00, h01);
 #pragma unroll
-  for (int j = 0; j < 4; ++j) o0.b[j] = b_op(smem, j, 0, h00, h01);
+  for (int j = 0; j < 4; ++j) o0.b[j] = b_op(smem + kG2Half, j, 0, h00, h01);
 
   // Sub-step (kk, H): 16 MFMAs on `cur` (sub-slice 2kk + H) with the operand
-  // reads of the next sub-slice into `nxt` spread between them.  Sub-step
-  // (kk, 1) begins with the slice's one wait and barrier: slice kk+1 (read
-  // from here on) has landed, and every wave has finished reading slice kk,
-  // whose stage then takes slice kk+2's loads, one between consecutive MFMAs.
+  // reads of the next sub-slice into `nxt` and eight loads of slice kk + 2
+  // spread between them: its A part in (kk, 0), into the slot of slice
+  // kk - 1's B^T part, and its B^T part in (kk, 1), into the slot of slice
+  // kk's A part -- an even stream of loads, each with two to three
+  // sub-steps to land.  Sub-step (kk, 1) begins with the slice's one wait
+  // and barrier: slice kk + 1 (read from here on) has landed, and every wave
+  // has finished reading slice kk.
+  int sa = 0;   // slot of slice kk's A part
   auto sub = [&](int kk, auto Hc, G2Ops& cur, G2Ops& nxt) __attribute__((always_inline)) {
     constexpr int H = decltype(Hc)::value;
     const int u = 2 * kk + H;
     const bool more = u + 1 < nsub;
-    const bool load = H == 1 && kk + 2 < nslice;
+    const bool load = kk + 2 < nslice;
     if (H == 1) {
-      if (more) g2_wait_vmem<0>();
+      // in flight behind slice kk + 1: the A part of slice kk + 2
+      if (more) {
+        if (load) g2_wait_vmem<kG2ALoads>();
+        else g2_wait_vmem<0>();
+      }
       __syncthreads();
     }
     // the next sub-slice: (kk, 1) when H == 0, else (kk + 1, 0)
-    const uint8_t* st = smem + ((H == 0 ? kk : kk + 1) & 1) * kG2Stage;
+    const uint8_t* sta = smem + (H == 0 ? sa : wrap(sa + 2)) * kG2Half;
+    const uint8_t* stb = smem + (H == 0 ? wrap(sa + 1) : wrap(sa + 3)) * kG2Half;
+    const int lslot = H == 0 ? wrap(sa + 4) : sa;
     const int r0 = H == 0 ? h10 : h00, r1 = H == 0 ? h11 : h01;
 #pragma unroll
     for (int t = 0; t < 16; ++t) {
       const int i = t >> 2, j = t & 3;
       acc[i][j] = mfma_32x32x64(cur.b[j], cur.a[i], acc[i][j]);
-      if (load) issue(t, kk + 2);
+      if ((t & 1) == 1 && load) issue(H * kG2ALoads + (t >> 1), kk + 2, lslot);
       if ((t & 1) == 0 && more) {
         const int v = t >> 2;
-        if ((t & 2) == 0) nxt.a[v] = g2_op(st + a_off + 32 * v * kG2Pitch, r0, r1);
-        else nxt.b[v] = b_op(st, v, H == 0 ? 1 : 0, r0, r1);
+        if ((t & 2) == 0) nxt.a[v] = g2_op(sta + a_off + 32 * v * kG2Pitch, r0, r1);
+        else nxt.b[v] = b_op(stb, v, H == 0 ? 1 : 0, r0, r1);
       }
     }
+    if (H == 1) sa = wrap(sa + 2);
   };
   const int nfull = nsub >> 1;
   for (int kk = 0; kk < nfull; ++kk) {
@@ -581,41 +602,81 @@ void gemm256_kernel(GemmArgs g) {
   if (half_tail) sub(nfull, std::integral_constant<int, 0>{}, o0, o1);
 
   // epilogue: C[m][n] = bf16(acc * a_scale * b_scale), or with row-wise
-  // scales bf16((acc * row_scale[m]) * col_scale[n])
+  // scales bf16((acc * row_scale[m]) * col_scale[n]).  The bf16 tile goes
+  // through LDS so that every store writes whole rows: each wave puts its
+  // 128 x 128 part (32 KiB) in its own LDS region, row r at 256 r, 8-byte
+  // slot s (columns 4s .. 4s+3) at slot s ^ (r & 31) -- the 32 rows of one
+  // write instruction then cover all 64 banks -- and reads it back 16 bytes
+  // per lane, 16 lanes per row (16 distinct granules), so each row leaves
+  // as one 256-byte run instead of sixteen 16-byte pieces.  The stores are
+  // non-temporal: C is not read again, and the L2 keeps the operand rows
+  // that other tiles still need.
   const float scale = g.row_scale ? 1.0f
                     : (g.a_dev ? *g.a_dev : g.a_scale) * (g.b_dev ? *g.b_dev : g.b_scale);
   const bool has_bias = g.bias != nullptr;
-  uint2 bb[4][4];
-#pragma unroll
-  for (int j = 0; j < 4; ++j)
-#pragma unroll
-    for (int q = 0; q < 4; ++q)
-      bb[j][q] = has_bias ? bias4(g, n0 + wn * 128 + 32 * j + 8 * q + 4 * lg)
-                          : make_uint2(0u, 0u);
+  constexpr int kCPitch = 128 * 2;                  // bytes per row of a wave's C part
+  static_assert(4 * 128 * kCPitch <= kG2Slots * kG2Half, "C staging fits the slots");
+  uint8_t* ct = smem + wave * 128 * kCPitch;
+  float sm[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int64_t m = m0 + wm * 128 + 32 * i + lq;
-    if (m >= g.M) continue;
-    const float sm = g.row_scale ? g.row_scale[m] : 1.0f;
+    sm[i] = g.row_scale && m < g.M ? g.row_scale[m] : 1.0f;
+  }
+  __syncthreads();   // every wave has finished reading the operand slots
+  // (no global store precedes these loads of bias and column scales)
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+  for (int j = 0; j < 4; ++j)
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int64_t n = n0 + wn * 128 + 32 * j + 8 * q + 4 * lg;
-        if (n >= g.N) continue;
+    for (int q = 0; q < 4; ++q) {
+      const int64_t n = n0 + wn * 128 + 32 * j + 8 * q + 4 * lg;
+      if (n >= g.N) continue;   // columns past N are never stored
+      const uint2 bb = has_bias ? bias4(g, n) : make_uint2(0u, 0u);
+      const float4 sn = g.row_scale ? *reinterpret_cast<const float4*>(g.col_scale + n)
+                                    : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        // rows past M are written here but never stored
         const f32x16& v = acc[i][j];
         float o[4];
         if (g.row_scale)
-          epi4_rows(has_bias, bb[j][q], sm, *reinterpret_cast<const float4*>(g.col_scale + n),
-                    v[4 * q + 0], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3], o);
+          epi4_rows(has_bias, bb, sm[i], sn, v[4 * q + 0], v[4 * q + 1], v[4 * q + 2],
+                    v[4 * q + 3], o);
         else
-          epi4(has_bias, bb[j][q], scale, v[4 * q + 0], v[4 * q + 1], v[4 * q + 2],
-               v[4 * q + 3], o);
+          epi4(has_bias, bb, scale, v[4 * q + 0], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3], o);
         uint2 pk;
         pk.x = g2_pack_bf16(o[0], o[1]);
         pk.y = g2_pack_bf16(o[2], o[3]);
-        *reinterpret_cast<uint2*>(g.c + m * g.ldc + n) = pk;
+        const int cs = ((8 * j + 2 * q + lg) ^ lq);
+        *reinterpret_cast<uint2*>(ct + (32 * i + lq) * kCPitch + cs * 8) = pk;
       }
+    }
+  __syncthreads();
+  // 16-byte stores need C, its row stride and batch stride 16-byte aligned;
+  // otherwise each run is stored as 8-byte halves
+  const bool c16 = reinterpret_cast<uintptr_t>(g.c) % 16 == 0 && g.ldc % 8 == 0;
+  const int c = lane & 15;
+  const bool odd = (lane >> 4) & 1;   // the parity of every row this lane reads
+  const int64_t n = n0 + wn * 128 + 8 * c;
+#pragma unroll 4
+  for (int k = 0; k < 32; ++k) {
+    const int r = 4 * k + (lane >> 4);
+    const int64_t m = m0 + wm * 128 + r;
+    // logical slots 2c, 2c+1 sit in granule c ^ ((r & 31) >> 1), swapped when r is odd
+    const int cg = (c ^ ((r & 31) >> 1));
+    const uint4 t = *reinterpret_cast<const uint4*>(ct + r * kCPitch + cg * 16);
+    const uint32_t lo0 = odd ? t.z : t.x, lo1 = odd ? t.w : t.y;
+    const uint32_t hi0 = odd ? t.x : t.z, hi1 = odd ? t.y : t.w;
+    if (m >= g.M || n >= g.N) continue;
+    uint16_t* dst = g.c + m * g.ldc + n;
+    if (c16 && n + 8 <= g.N) {
+      __builtin_nontemporal_store(u32x4{lo0, lo1, hi0, hi1}, reinterpret_cast<u32x4*>(dst));
+    } else {
+      // n + 4 <= N (N % 4 == 0)
+      __builtin_nontemporal_store(u32x2{lo0, lo1}, reinterpret_cast<u32x2*>(dst));
+      if (n + 8 <= g.N)
+        __builtin_nontemporal_store(u32x2{hi0, hi1}, reinterpret_cast<u32x2*>(dst + 4));
+    }
   }
 }
 

@@ -241,6 +241,24 @@ def test_out_argument_is_checked(gpu: torch.device) -> None:
     assert torch.equal(wide[:, 16:], torch.full((64, 8), 7.0, dtype=torch.bfloat16, device=gpu))
 
 
+@pytest.mark.parametrize("mnk", [(300, 260, 128), (513, 516, 192)])
+def test_output_row_stride_and_offset(gpu: torch.device, mnk: tuple[int, int, int]) -> None:
+    """C written into views of a wider buffer -- row strides that are and are
+    not multiples of 8 elements, a base 8 but not 16 bytes aligned, N % 8 == 4
+    -- equals the packed output, and the padding around it is untouched."""
+    M, N, K = mnk
+    g = torch.Generator().manual_seed(M + N)
+    a8 = torch.randn(M, K, generator=g).mul(30).to(torch.float8_e4m3fn).to(gpu)
+    bt8 = torch.randn(N, K, generator=g).mul(30).to(torch.float8_e4m3fn).to(gpu)
+    plain = ops.fp8_gemm(a8, bt8, 0.01, 0.02, b_transposed=True)
+    for extra, off in ((4, 0), (4, 4), (8, 4), (12, 8)):
+        wide = torch.full((M, off + N + extra), 7.0, dtype=torch.bfloat16, device=gpu)
+        c = ops.fp8_gemm(a8, bt8, 0.01, 0.02, b_transposed=True, out=wide[:, off:off + N])
+        assert torch.equal(c, plain), (extra, off)
+        pad = torch.cat([wide[:, :off], wide[:, off + N:]], dim=1)
+        assert (pad == 7.0).all(), (extra, off)
+
+
 def test_device_reproduces_golden_vectors(gpu: torch.device,
                                          monkeypatch: pytest.MonkeyPatch) -> None:
     """The committed known-answer vectors through the reference's (K, N)

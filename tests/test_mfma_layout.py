@@ -152,8 +152,7 @@ SW_KN = _fn(_expr(GEMM, r"const int gran = min\((slot \^ \(2 \* \(row & 7\)\)), 
 KN_ROW = _fn(_expr(GEMM, r"const int row = (32 \* lg \+ \(i >> 1\));"), "lg", "i")
 KN_GR = _fn(_expr(GEMM, r"const int gr = (8 \* wn \+ 2 \* j \+ \(\(lane >> 4\) & 1\));"),
             "wn", "j", "lane")
-KN_OFF = _fn(_expr(GEMM, r"kn_off\[j\] = \(uint32_t\)\(kG2Half \+ ([^;]+)\);"), "row", "kG2Tile",
-             "gr", "i")
+KN_OFF = _fn(_expr(GEMM, r"kn_off\[j\] = \(uint32_t\)\(([^;]+)\);"), "row", "kG2Tile", "gr", "i")
 TILE = 256   # kG2Tile
 
 
@@ -238,3 +237,138 @@ def test_kn_swizzle_is_a_permutation_and_reads_conflict_free() -> None:
             assert groups == list(range(16)), (wn, j)
     # negative control: an unswizzled slice puts a group's eight rows in one bank group
     assert len({((r * TILE + 16 * 3) // 16) % 16 for r in range(8)}) == 1
+
+
+# ------------------------------------------- GEMM epilogue: C through LDS
+EPI_W = _fn(_expr(GEMM, r"const int cs = (\(\(8 \* j \+ 2 \* q \+ lg\) \^ lq\));"),
+            "j", "q", "lg", "lq")
+EPI_R = _fn(_expr(GEMM, r"const int cg = (\(c \^ \(\(r & 31\) >> 1\)\));"), "c", "r")
+C_PITCH = 256   # kCPitch: 128 bf16 columns of a wave's part
+
+
+def test_epilogue_staging_round_trip_and_conflict_free() -> None:
+    """The 128 x 128 bf16 part of a wave: lane (lq, lg) writes the 4 columns
+    32j + 8q + 4lg .. +3 of row 32i + lq (the 32x32 accumulator map) as 8-byte
+    slot cs of the row; reading 16 bytes at granule cg of row r (halves
+    swapped for odd r) returns columns 8c .. 8c+7 in order.  One write
+    instruction's 32 lanes of a half-wave fill 32 distinct 8-byte slots (all
+    64 banks), one read's 16 lanes of a row 16 distinct granules."""
+    lds = {}
+    for i in range(4):
+        for j in range(4):
+            for q in range(4):
+                slots = {0: [], 1: []}
+                for lane in range(64):
+                    lq, lg = lane & 31, lane >> 5
+                    row = 32 * i + lq
+                    off = row * C_PITCH + 8 * EPI_W(j, q, lg, lq)
+                    assert 0 <= off - row * C_PITCH < C_PITCH
+                    cols = [32 * j + 8 * q + 4 * lg + e for e in range(4)]
+                    for e in range(4):
+                        assert off + 2 * e not in lds
+                        lds[off + 2 * e] = (row, cols[e])
+                    slots[lg].append((off % 256) // 8)
+                assert all(sorted(v) == list(range(32)) for v in slots.values())
+    assert len(lds) == 128 * 128
+    for k in range(32):
+        for lane in range(64):
+            r, c = 4 * k + (lane >> 4), lane & 15
+            base = r * C_PITCH + 16 * EPI_R(c, r)
+            got = [lds[base + 2 * e] for e in range(8)]
+            if r & 1:
+                got = got[4:] + got[:4]
+            assert got == [(r, 8 * c + e) for e in range(8)], (k, lane)
+        for grp in range(4):
+            r = 4 * k + grp
+            assert sorted(EPI_R(c, r) for c in range(16)) == list(range(16))
+    # negative control: without the XOR the 32 rows of one write instruction
+    # (pitch 256 bytes = one sweep of the banks) all land on the same slot
+    plain = {((32 + lq) * C_PITCH + 8 * (8 * 1 + 2 * 2 + 0)) % 256 for lq in range(32)}
+    assert len(plain) == 1
+
+
+# --------------------------------------- GEMM: the slot ring of the loads
+RING_LINES = (
+    "const uint8_t* sta = smem + (H == 0 ? sa : wrap(sa + 2)) * kG2Half;",
+    "const uint8_t* stb = smem + (H == 0 ? wrap(sa + 1) : wrap(sa + 3)) * kG2Half;",
+    "const int lslot = H == 0 ? wrap(sa + 4) : sa;",
+    "if ((t & 1) == 1 && load) issue(H * kG2ALoads + (t >> 1), kk + 2, lslot);",
+    "const bool load = kk + 2 < nslice;",
+    "if (load) g2_wait_vmem<kG2ALoads>();",
+    "for (int n = 0; n < kG2Loads; ++n) issue(n, 0, n < kG2ALoads ? 0 : 1);",
+    "for (int n = 0; n < kG2Loads; ++n) issue(n, 1, n < kG2ALoads ? 2 : 3);",
+    "if (H == 1) sa = wrap(sa + 2);",
+    "constexpr int kG2Slots = 5;",
+)
+
+
+def _ring_schedule(nsub: int, slots: int = 5) -> None:
+    """Replays the large-tile kernel's load/read schedule (the lines above)
+    for one tile: every operand read finds its slice part landed (the vmcnt
+    waits) and in its slot, and no load overwrites a part that some wave may
+    still read (the last read of a part precedes a barrier that precedes the
+    load).  Units are the A (0) or B^T (1) part of a slice, 8 loads each."""
+    nslice, half, nfull = (nsub + 1) // 2, nsub & 1, nsub // 2
+    wrap = lambda x: x - slots if x >= slots else x   # noqa: E731
+    issued, landed, slot, reads, pending = [], set(), {}, {}, set()
+    need = lambda s: 1 if (half and s == nslice - 1) else 2   # noqa: E731
+
+    def issue(unit, sl):
+        old = slot.get(sl)
+        assert old is None or (reads.get(old, 0) == need(old[0]) and old not in pending), \
+            (nsub, unit, sl, old)
+        slot[sl] = unit
+        issued.append(unit)
+
+    def wait(k):                       # all but the k most recent units landed
+        landed.update(issued[:len(issued) - k])
+
+    def read(s, sla, slb):
+        for part, sl in ((0, sla), (1, slb)):
+            assert slot[sl] == (s, part) and (s, part) in landed, (nsub, s, part)
+            reads[(s, part)] = reads.get((s, part), 0) + 1
+            pending.add((s, part))
+
+    issue((0, 0), 0)
+    issue((0, 1), 1)
+    if nslice > 1:
+        issue((1, 0), 2)
+        issue((1, 1), 3)
+        wait(2)
+    else:
+        wait(0)
+    pending.clear()                    # barrier
+    read(0, 0, 1)
+    sa = 0
+    steps = [(kk, h) for kk in range(nfull) for h in (0, 1)] + ([(nfull, 0)] if half else [])
+    for kk, h in steps:
+        more, load = 2 * kk + h + 1 < nsub, kk + 2 < nslice
+        if h == 1:
+            if more:
+                wait(1 if load else 0)
+            pending.clear()            # barrier
+        if more:
+            if h == 0:
+                read(kk, sa, wrap(sa + 1))
+            else:
+                read(kk + 1, wrap(sa + 2), wrap(sa + 3))
+        if load:
+            issue((kk + 2, h), wrap(sa + 4) if h == 0 else sa)
+        if h == 1:
+            sa = wrap(sa + 2)
+    assert len(issued) == 2 * nslice
+    assert all(reads[(s, p)] == need(s) for s in range(nslice) for p in (0, 1))
+
+
+def test_gemm_slot_ring_schedule() -> None:
+    for line in RING_LINES:
+        assert line in GEMM, line
+    for nsub in range(1, 41):
+        _ring_schedule(nsub)
+
+
+def test_gemm_slot_ring_negative_controls() -> None:
+    """With four slots the same schedule puts slice k+2's A part over a part
+    that is still read (or has not been read yet): the replay fails."""
+    with pytest.raises(AssertionError):
+        _ring_schedule(12, slots=4)
