@@ -426,13 +426,15 @@ __device__ __forceinline__ void mfma_phase(uint32_t kl, uint32_t vl,
 // before barrier 2j.  Only group 0 loads: the slot in which a group issues
 // loads costs its SIMD VALU time, and in this slot the MFMA group, not the
 // softmax group, has VALU time to spare.
-template <int DK, int DV, int OUT, bool WINDOW, bool MULTI>
+template <int DK, int DV, int OUT, bool WINDOW, bool MULTI, bool STAGE = false>
 __global__ __launch_bounds__(512, 1)
 void attn_fwd_kernel(AttnArgs a) {
   constexpr int NW = 8;
   using G = Geo<DK, DV, NW>;
   constexpr int D = DK;
   static_assert(!MULTI || (OUT != kOutSplit && !WINDOW && DV == DK), "multi-block launches");
+  static_assert(!STAGE || (MULTI && DK == 128 && (OUT == kOutBf16 || OUT == kOutF16)),
+                "staged output stores");
   constexpr int QROWS = 32;
   constexpr int BLOCK_M = QROWS * NW;
   // multi-block launches stage the next query block's Q in LDS: two buffers
@@ -613,16 +615,33 @@ void attn_fwd_kernel(AttnArgs a) {
   if (group == 1) __syncthreads();  // group 1 starts half a step behind
 
   // out = acc * v_scale / l for query row qrow (acc carries P*448, l sums
-  // P*448); every lane takes part (the row sum combines lane pairs)
-  auto store_out = [&](int qrow, float l_lane) __attribute__((always_inline)) {
+  // P*448); every lane takes part (the row sum combines lane pairs).
+  // STAGE (multi-block launches, D = 128, 16-bit output, two or more key
+  // tiles per block): the rows go out through Q buffer sbuf, whose
+  // block has been read by every wave and which no load refills before the
+  // next block switch.  Each wave stages its 32 rows in a 4 KiB share, 64
+  // columns at a time: row r (128 bytes) at 128 r, 16-byte chunk c at
+  // granule c ^ ((r >> 1) & 7) -- the 16 lanes of a write group cover the 16
+  // bank groups -- then reads them back eight lanes to a row, so every
+  // store instruction writes whole 128-byte lines (the unstaged stores write
+  // 32-byte pieces, which the L2 has to merge).
+  auto store_out = [&](int qrow, float l_lane, int sbuf) __attribute__((always_inline)) {
     const float l = xhalf_sum(l_lane);
     const float inv = v_scale / l;
     uint2 pend = make_uint2(0u, 0u);
-    if (qrow < a.Sq) {
+    if (STAGE || qrow < a.Sq) {
       const int64_t obase =
           (int64_t)b * a.osb + (int64_t)h * a.osh + (int64_t)qrow * a.oss + dv_off;
+      // the wave's first row of the block, and its staging share.  The
+      // staging addresses derive from `ln`, opaque to the compiler here, so
+      // that they are computed at the store and not hoisted out of the tile
+      // loop (where they would hold registers through every phase).
+      const int row0 = __builtin_amdgcn_readfirstlane(qrow - lq);
+      int ln = lane;
+      asm volatile("" : "+v"(ln));
+      uint8_t* const st = smem + LDS_TILES + sbuf * Q_BYTES + wave * 4096;
 #pragma unroll
-      for (int e = 0; e < G::ETILES; ++e)
+      for (int e = 0; e < G::ETILES; ++e) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int d = 32 * e + 8 * i + 4 * lg;
@@ -655,10 +674,39 @@ void attn_fwd_kernel(AttnArgs a) {
               const auto y = __builtin_amdgcn_permlane32_swap(pend.y, pk.y, false, false);
               const uint4 v = make_uint4(x[0], y[0], x[1], y[1]);
               const int c = 4 * e + i - 1 + lg;   // the chunk this lane now holds
-              *reinterpret_cast<uint4*>(static_cast<uint16_t*>(a.out) + obase + 8 * c) = v;
+              if constexpr (STAGE) {
+                const int cl = c & 7;               // chunk within the 64 staged columns
+                const int lr = ln & 31;             // = lq, the row this lane holds
+                *reinterpret_cast<uint4*>(st + lr * 128 + ((cl ^ ((lr >> 1) & 7)) << 4)) = v;
+              } else {
+                *reinterpret_cast<uint4*>(static_cast<uint16_t*>(a.out) + obase + 8 * c) = v;
+              }
             }
           }
         }
+        if constexpr (STAGE) {
+          if ((e & 1) == 1) {
+            // 64 columns (chunks 8(e/2) .. +7) of the wave's 32 rows staged
+            __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0): the writes are done
+            __builtin_amdgcn_wave_barrier();
+            const int cl = ln & 7;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+              const int r = 8 * k + (ln >> 3);
+              const uint4 v =
+                  *reinterpret_cast<const uint4*>(st + r * 128 + ((cl ^ ((r >> 1) & 7)) << 4));
+              const int qr = row0 + r;
+              if (qr < a.Sq) {
+                const int64_t ob = (int64_t)b * a.osb + (int64_t)h * a.osh +
+                                   (int64_t)qr * a.oss + dv_off + 8 * (8 * (e >> 1) + cl);
+                *reinterpret_cast<uint4*>(static_cast<uint16_t*>(a.out) + ob) = v;
+              }
+            }
+            __builtin_amdgcn_s_waitcnt(0xC07F);   // the reads are done before the next writes
+            __builtin_amdgcn_wave_barrier();
+          }
+        }
+      }
     }
   };
 
@@ -686,7 +734,7 @@ void attn_fwd_kernel(AttnArgs a) {
         // the loading group stores the finished block here, ahead of this
         // phase's tile loads (its counted waits then never cover stores)
         if (LOADS && i >= 2 && (i - 1) % n_kb == 0 && i - 1 < T)
-          store_out(q - BLOCK_M, l_done);
+          store_out(q - BLOCK_M, l_done, blk & 1);
         if (j == 0 && i > 0 && i < T) {
           read_q(blk);
           m_run = -__builtin_inff();
@@ -789,7 +837,7 @@ void attn_fwd_kernel(AttnArgs a) {
       if constexpr (MULTI) {
         if (j == 0 && i > 0 && i < T) {
           l_done = l_run;   // the finished block's row sum, before this tile's update
-          if (!LOADS) store_out(q - BLOCK_M, l_done);
+          if (!LOADS) store_out(q - BLOCK_M, l_done, blk & 1);
         }
       }
       if (i < T) {
@@ -846,7 +894,7 @@ void attn_fwd_kernel(AttnArgs a) {
     }
     return;
   }
-  store_out(q, l_run);
+  store_out(q, l_run, (nblk - 1) & 1);
 }
 
 // Merge the key splits of one query row: with m_j, l_j, O_j the running
@@ -912,6 +960,14 @@ void launch_fwd(const AttnArgs& a, hipStream_t st) {
   const dim3 grid(a.n_work), block(512);
   if constexpr (OUT != kOutSplit && DV == D) {
     if (a.qb_per_wg > 1) {
+      // staged output stores need a block's Q buffer idle from its switch
+      // to the next one: two or more key tiles per block
+      if constexpr (D == 128 && OUT != kOutF32) {
+        if (a.Skv > kBlockN) {
+          hipLaunchKernelGGL((attn_fwd_kernel<D, DV, OUT, false, true, true>), grid, block, 0, st, a);
+          return;
+        }
+      }
       hipLaunchKernelGGL((attn_fwd_kernel<D, DV, OUT, false, true>), grid, block, 0, st, a);
       return;
     }

@@ -176,6 +176,11 @@ MULTI_CASES = [
     ("d128_shifted_tail", 2, 20, 12000, 300, 128, torch.bfloat16, torch.bfloat16),
     ("d32_fp16", 1, 48, 8192 + 5, 512, 32, torch.float16, torch.float16),
     ("d128_wan_cross_like", 1, 40, 9000, 512, 128, torch.bfloat16, torch.float32),
+    # 16-bit outputs at D = 128 with two or more key tiles per block leave
+    # through the staged (whole-line) stores; two tiles is the shortest
+    # window the Q buffer they borrow stays idle
+    ("d128_wan_cross_like_bf16", 1, 40, 9000, 512, 128, torch.bfloat16, torch.bfloat16),
+    ("d128_two_tiles_fp16", 1, 24, 7003, 256, 128, torch.float16, torch.float16),
 ]
 
 
