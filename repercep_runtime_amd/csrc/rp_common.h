@@ -96,7 +96,48 @@ __device__ __forceinline__ T shfl_xor(T v, int mask) {
   return __shfl_xor(v, mask, kWave);
 }
 
+// v + (v of the lane N places further round this lane's 16-lane row), by a
+// DPP row rotation (no LDS round trip).  Sums over a 16-lane row in the
+// order of the xor butterfly (xor 8, 4, 2, 1) come out bit for bit when the
+// rotations go 8, 4, 2, 1: after the xor-8 step lanes 8 apart hold equal
+// values, so lane i + 4 (mod 16) holds the value of lane i ^ 4, and so on
+// down; every lane adds the same two operands in the same order.
+template <int N>
+__device__ __forceinline__ float add_row_ror(float v) {
+  static_assert(N >= 1 && N <= 15, "row rotation");
+  const int r = __builtin_amdgcn_mov_dpp(__float_as_int(v), 0x120 + N, 0xf, 0xf, false);
+  return v + __int_as_float(r);
+}
+
 __device__ __forceinline__ uint32_t umax32(uint32_t a, uint32_t b) { return a > b ? a : b; }
+
+// Max of n uint32 values at v, by one workgroup of NT threads; the result is
+// valid in thread 0.  Each thread keeps eight independent loads in flight
+// (a per-tensor scale reduces ~10^4 block maxima: one load at a time, that is
+// a chain of ~50 memory latencies per thread).
+template <int NT>
+__device__ __forceinline__ uint32_t block_max_u32(const uint32_t* v, int64_t n) {
+  uint32_t m = 0;
+  for (int64_t i0 = threadIdx.x; i0 < n; i0 += 8 * NT) {
+    uint32_t x[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int64_t i = i0 + (int64_t)u * NT;
+      x[u] = i < n ? v[i] : 0u;
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) m = umax32(m, x[u]);
+  }
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) m = umax32(m, (uint32_t)__shfl_xor((int)m, o, 64));
+  __shared__ uint32_t wmax[NT / 64];
+  if ((threadIdx.x & 63) == 0) wmax[threadIdx.x / 64] = m;
+  __syncthreads();
+  uint32_t r = wmax[0];
+#pragma unroll
+  for (int w = 1; w < NT / 64; ++w) r = umax32(r, wmax[w]);
+  return r;
+}
 
 // Dequant scale from the bf16 bit pattern of a group's |x| maximum, as the
 // reference computes it: clamp in bf16 against bf16(1e-6), divide by 425.6

@@ -92,10 +92,21 @@ __device__ __forceinline__ void prologue_rows(const PParams& p, const uint16_t* 
 #pragma unroll
       for (int i = 1; i < 8; ++i) ss[u] = ss[u] + x[u][i] * x[u][i];
     }
+    if constexpr (D == 128) {
+      // a row is one 16-lane DPP row: the butterfly by row rotations
 #pragma unroll
-    for (int o = D / 16; o >= 1; o >>= 1)
+      for (int u = 0; u < U; ++u) {
+        ss[u] = add_row_ror<8>(ss[u]);
+        ss[u] = add_row_ror<4>(ss[u]);
+        ss[u] = add_row_ror<2>(ss[u]);
+        ss[u] = add_row_ror<1>(ss[u]);
+      }
+    } else {
 #pragma unroll
-      for (int u = 0; u < U; ++u) ss[u] = ss[u] + shfl_xor(ss[u], o);
+      for (int o = D / 16; o >= 1; o >>= 1)
+#pragma unroll
+        for (int u = 0; u < U; ++u) ss[u] = ss[u] + shfl_xor(ss[u], o);
+    }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       r[u] = 1.0f / __builtin_sqrtf(ss[u] * (1.0f / D) + p.eps);
@@ -248,19 +259,8 @@ __global__ __launch_bounds__(kPThreads) void prologue_finalize_kernel(const uint
                                                                       int64_t nbg,
                                                                       float* dequant) {
   const int64_t g = blockIdx.x;
-  uint32_t m = 0;
-  for (int64_t i = threadIdx.x; i < nbg; i += kPThreads) m = umax32(m, partial[g * nbg + i]);
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) m = umax32(m, (uint32_t)shfl_xor((int)m, o));
-  __shared__ uint32_t wmax[kPThreads / kWave];
-  if ((threadIdx.x & (kWave - 1)) == 0) wmax[threadIdx.x / kWave] = m;
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    uint32_t r = wmax[0];
-#pragma unroll
-    for (int w = 1; w < kPThreads / kWave; ++w) r = umax32(r, wmax[w]);
-    dequant[g] = dequant_from_amax_bits(r);
-  }
+  const uint32_t r = block_max_u32<kPThreads>(partial + g * nbg, nbg);
+  if (threadIdx.x == 0) dequant[g] = dequant_from_amax_bits(r);
 }
 
 template <int D, int ROPE>

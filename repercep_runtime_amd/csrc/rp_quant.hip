@@ -123,19 +123,8 @@ template <int DT>
 __device__ __forceinline__ void scale_finalize_body(int64_t blk_id, const uint32_t* partial,
                                                                    int64_t nbg, float* dequant) {
   const int64_t g = blk_id;
-  uint32_t m = 0;
-  for (int64_t i = threadIdx.x; i < nbg; i += kQThreads) m = umax32(m, partial[g * nbg + i]);
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) m = umax32(m, (uint32_t)shfl_xor((int)m, o));
-  __shared__ uint32_t wmax[kQThreads / kWave];
-  if ((threadIdx.x & (kWave - 1)) == 0) wmax[threadIdx.x / kWave] = m;
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    uint32_t r = wmax[0];
-#pragma unroll
-    for (int w = 1; w < kQThreads / kWave; ++w) r = umax32(r, wmax[w]);
-    dequant[g] = dequant_from_amax<DT>(r);
-  }
+  const uint32_t r = block_max_u32<kQThreads>(partial + g * nbg, nbg);
+  if (threadIdx.x == 0) dequant[g] = dequant_from_amax<DT>(r);
 }
 
 template <int DT>
