@@ -64,12 +64,13 @@ __device__ __forceinline__ float bf16r(float f) { return (float)(__bf16)f; }
 // The rotary layout is a template parameter: with it as a runtime branch,
 // hipcc 7.2 merged the two layouts' code so that the interleaved path
 // skipped its own sign flips (rotated with stale registers).
-template <int D, int ROPE, int U, bool LOAD, bool STORE>
-__device__ __forceinline__ void prologue_rows(const PParams& p, const uint16_t* const (&xrow)[U],
-                                              const int64_t (&s)[U], const int64_t (&row)[U],
-                                              int c, float (&y)[U][8]) {
+// The first steps of prologue_rows: the 8 elements of each row as fp32 and
+// each row's r = 1/sqrt(mean(x^2) + eps).
+template <int D, int U, bool LOAD, bool STORE>
+__device__ __forceinline__ void load_norm(const PParams& p, const uint16_t* const (&xrow)[U],
+                                          const int64_t (&row)[U], int c, float (&x)[U][8],
+                                          float (&r)[U]) {
 #pragma clang fp contract(off)
-  float x[U][8];
 #pragma unroll
   for (int u = 0; u < U; ++u) {
     const uint4 v = *reinterpret_cast<const uint4*>(xrow[u] + 8 * c);
@@ -80,7 +81,6 @@ __device__ __forceinline__ void prologue_rows(const PParams& p, const uint16_t* 
       x[u][2 * i + 1] = bf16_to_f32(w4[i] >> 16);
     }
   }
-  float r[U];
   if constexpr (LOAD) {
 #pragma unroll
     for (int u = 0; u < U; ++u) r[u] = p.rinv[row[u]];
@@ -113,6 +113,15 @@ __device__ __forceinline__ void prologue_rows(const PParams& p, const uint16_t* 
       if (STORE && c == 0) p.rinv[row[u]] = r[u];
     }
   }
+}
+
+template <int D, int ROPE, int U, bool LOAD, bool STORE>
+__device__ __forceinline__ void prologue_rows(const PParams& p, const uint16_t* const (&xrow)[U],
+                                              const int64_t (&s)[U], const int64_t (&row)[U],
+                                              int c, float (&y)[U][8]) {
+#pragma clang fp contract(off)
+  float x[U][8], r[U];
+  load_norm<D, U, LOAD, STORE>(p, xrow, row, c, x, r);
 #pragma unroll
   for (int u = 0; u < U; ++u)
 #pragma unroll
@@ -200,6 +209,35 @@ __device__ __forceinline__ void for_rows(const PParams& p, F&& fn) {
   const int c = threadIdx.x % TPR;
   int64_t k = threadIdx.x / TPR;
   if (k >= nrows) return;
+  // Fast path: the block's rows all lie in one (b, h), so a thread's rows
+  // are STEP apart in s and their addresses advance by a fixed stride.
+  {
+    const int64_t rb = g * p.rows_per_group + first;   // the block's first row
+    const int64_t bhb = rb / p.S;
+    const int64_t sb0 = rb - bhb * p.S;
+    if (sb0 + nrows <= p.S) {
+      const int64_t bb = bhb / p.H;
+      const uint16_t* xp = p.x + bb * p.sb + (bhb - bb * p.H) * p.sh + (sb0 + k) * p.ss;
+      const int64_t dstep = (int64_t)STEP * p.ss;
+      for (; k < nrows; k += U * STEP, xp += U * dstep) {
+        int64_t rr[U], bh[U], sv[U];
+        const uint16_t* xr[U];
+        bool ok[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          ok[u] = k + u * STEP < nrows;
+          // a row past the range repeats the step's first row (never used)
+          const int64_t du = ok[u] ? u * STEP : 0;
+          rr[u] = rb + k + du;
+          bh[u] = bhb;
+          sv[u] = sb0 + k + du;
+          xr[u] = xp + (ok[u] ? u * dstep : 0);
+        }
+        fn(rr, bh, sv, xr, ok, c);
+      }
+      return;
+    }
+  }
   int64_t r = g * p.rows_per_group + first + k;  // global row bh*S + s
   PCursor cur;
   {
@@ -232,16 +270,35 @@ template <int D, int ROPE>
 __global__ __launch_bounds__(kPThreads) void prologue_amax_kernel(PParams p, uint32_t* partial) {
   constexpr int U = kPRowsPerStep<ROPE>;
   uint32_t m = 0;
-  for_rows<D, U>(p, [&](const int64_t (&r)[U], const int64_t (&)[U], const int64_t (&s)[U],
-                     const uint16_t* const (&xrow)[U], const bool (&ok)[U], int c) {
-    float y[U][8];
-    prologue_rows<D, ROPE, U, false, kStoreNorm<ROPE>>(p, xrow, s, r, c, y);
+  if (ROPE == RP_ROPE_NONE && p.weight == nullptr) {
+    // y = bf16(x * r) is only needed for its maximum: take it from the
+    // packed bf16 pairs, two per packed 16-bit max.  A row past the range
+    // repeats a row of the range (the same maximum), so it needs no mask.
+    uint32_t m2 = 0;
+    for_rows<D, U>(p, [&](const int64_t (&r)[U], const int64_t (&)[U], const int64_t (&)[U],
+                       const uint16_t* const (&xrow)[U], const bool (&)[U], int c) {
+#pragma clang fp contract(off)
+      float x[U][8], rn[U];
+      load_norm<D, U, false, kStoreNorm<ROPE>>(p, xrow, r, c, x, rn);
 #pragma unroll
-    for (int u = 0; u < U; ++u)
+      for (int u = 0; u < U; ++u)
 #pragma unroll
-      for (int i = 0; i < 8; ++i)
-        m = umax32(m, ok[u] ? (__float_as_uint(y[u][i]) >> 16) & 0x7fffu : 0u);
-  });
+        for (int i = 0; i < 8; i += 2)
+          m2 = pk_max_u16(m2, pk_bf16(x[u][i] * rn[u], x[u][i + 1] * rn[u]) & 0x7fff7fffu);
+    });
+    m = umax32(m2 & 0xffffu, m2 >> 16);
+  } else {
+    for_rows<D, U>(p, [&](const int64_t (&r)[U], const int64_t (&)[U], const int64_t (&s)[U],
+                       const uint16_t* const (&xrow)[U], const bool (&ok)[U], int c) {
+      float y[U][8];
+      prologue_rows<D, ROPE, U, false, kStoreNorm<ROPE>>(p, xrow, s, r, c, y);
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+          m = umax32(m, ok[u] ? (__float_as_uint(y[u][i]) >> 16) & 0x7fffu : 0u);
+    });
+  }
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) m = umax32(m, (uint32_t)shfl_xor((int)m, o));
   __shared__ uint32_t wmax[kPThreads / kWave];

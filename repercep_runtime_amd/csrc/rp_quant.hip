@@ -268,10 +268,13 @@ __global__ __launch_bounds__(kQThreads) void quant_apply_kernel(QParams p, const
 
 // BHDS output: per head, codes[(bh*D + d)*ld + s]; columns [S, ld) zeroed.
 // Tile: 128 rows (s) x 64 columns (d), or 32 for the last block of a head
-// dim that is an odd multiple of 32.  Thread t loads rows 4*(t&31)+i,
-// column chunk t>>5 (8 elements), transposes its 4x8 codes in registers and
-// writes 8 dwords [d][s..s+3] into LDS; the tile then leaves as 64 rows of
-// 128 contiguous codes.
+// dim that is an odd multiple of 32.  Thread t loads column chunk t & 7 (8
+// elements) of rows 4*(t >> 3) + i, so the eight lanes of a chunk group
+// read one row's 128 bytes (a whole line per 8 lanes), transposes its 4x8
+// codes in registers and writes 8 dwords [d][s..s+3] into LDS; the tile
+// then leaves as 64 rows of 128 contiguous codes.  In LDS, dword q of row d
+// sits at q ^ 8((d >> 3) & 3): the 64 lanes of a write instruction (rows of
+// one parity: 32 banks) land two to a bank, the minimum.
 template <int DT>
 __global__ __launch_bounds__(kQThreads) void quant_apply_t_kernel(QParams p, const float* dequant,
                                                                   int per_bh, uint8_t* codes,
@@ -283,13 +286,13 @@ __global__ __launch_bounds__(kQThreads) void quant_apply_t_kernel(QParams p, con
   const int64_t bh = blockIdx.z;
   const float qm = 1.0f / dequant[per_bh ? bh : 0];
   const int64_t base = (bh / p.H) * p.sb + (bh % p.H) * p.sh + d0;
-  const int r4 = threadIdx.x & 31;
-  const int c = threadIdx.x >> 5;
+  const int q = threadIdx.x >> 3;   // row quad: rows 4q .. 4q+3 of the tile
+  const int c = threadIdx.x & 7;    // column chunk: columns 8c .. 8c+7
 
   uint32_t w[4][2];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const int64_t s = s0 + 4 * r4 + i;
+    const int64_t s = s0 + 4 * q + i;
     if (s < p.S && c * 8 < dcols) {
       const uint4 v = *reinterpret_cast<const uint4*>(p.x + base + s * p.ss + c * 8);
       w[i][0] = quant4<DT>(v.x, v.y, qm);
@@ -300,6 +303,7 @@ __global__ __launch_bounds__(kQThreads) void quant_apply_t_kernel(QParams p, con
     }
   }
   // 4x4 byte transposes: rows i (s) x columns e (d) -> dword per column.
+  const int qs = 4 * (q ^ (8 * (c & 3)));   // byte offset of this quad's dword in its row
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
     const uint32_t t0 = __builtin_amdgcn_perm(w[1][h], w[0][h], 0x05010400u);
@@ -311,10 +315,10 @@ __global__ __launch_bounds__(kQThreads) void quant_apply_t_kernel(QParams p, con
     const uint32_t col2 = __builtin_amdgcn_perm(t3, t1, 0x05040100u);
     const uint32_t col3 = __builtin_amdgcn_perm(t3, t1, 0x07060302u);
     const int d = c * 8 + h * 4;
-    *reinterpret_cast<uint32_t*>(&tile[(d + 0) * 128 + 4 * r4]) = col0;
-    *reinterpret_cast<uint32_t*>(&tile[(d + 1) * 128 + 4 * r4]) = col1;
-    *reinterpret_cast<uint32_t*>(&tile[(d + 2) * 128 + 4 * r4]) = col2;
-    *reinterpret_cast<uint32_t*>(&tile[(d + 3) * 128 + 4 * r4]) = col3;
+    *reinterpret_cast<uint32_t*>(&tile[(d + 0) * 128 + qs]) = col0;
+    *reinterpret_cast<uint32_t*>(&tile[(d + 1) * 128 + qs]) = col1;
+    *reinterpret_cast<uint32_t*>(&tile[(d + 2) * 128 + qs]) = col2;
+    *reinterpret_cast<uint32_t*>(&tile[(d + 3) * 128 + qs]) = col3;
   }
   __syncthreads();
 #pragma unroll
@@ -322,8 +326,11 @@ __global__ __launch_bounds__(kQThreads) void quant_apply_t_kernel(QParams p, con
     const int dr = (threadIdx.x >> 3) + 32 * k;
     if (dr >= dcols) break;
     const int ch = threadIdx.x & 7;
+    // physical 16-byte chunk ch of row dr holds the codes of s chunk
+    // ch ^ 2((dr >> 3) & 3)
+    const int sch = ch ^ (2 * ((dr >> 3) & 3));
     const uint4 v = *reinterpret_cast<const uint4*>(&tile[dr * 128 + ch * 16]);
-    *reinterpret_cast<uint4*>(codes + (bh * p.D + d0 + dr) * ld + s0 + ch * 16) = v;
+    *reinterpret_cast<uint4*>(codes + (bh * p.D + d0 + dr) * ld + s0 + sch * 16) = v;
   }
 }
 

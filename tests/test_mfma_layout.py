@@ -372,3 +372,36 @@ def test_gemm_slot_ring_negative_controls() -> None:
     that is still read (or has not been read yet): the replay fails."""
     with pytest.raises(AssertionError):
         _ring_schedule(12, slots=4)
+
+
+# ----------------------------- quantizer: the V^T tile's LDS swizzle
+QUANT = (CSRC / "rp_quant.hip").read_text()
+VT_W = _fn(_expr(QUANT, r"const int qs = (4 \* \(q \^ \(8 \* \(c & 3\)\)\));"), "q", "c")
+VT_R = _fn(_expr(QUANT, r"const int sch = (ch \^ \(2 \* \(\(dr >> 3\) & 3\)\));"), "ch", "dr")
+
+
+def test_vt_tile_round_trip_and_banks() -> None:
+    """quant_apply_t_kernel: thread (q = t >> 3, c = t & 7) writes the dword of
+    codes s = 4q .. 4q+3 of each column d in [8c, 8c+8) at byte qs of row d;
+    reading 16 bytes at chunk ch of row dr gives the codes of s chunk sch.
+    Write instructions hit each bank at most twice, reads never twice."""
+    lds = {}
+    for t in range(256):
+        q, c = t >> 3, t & 7
+        for d in range(8 * c, 8 * c + 8):
+            off = d * 128 + VT_W(q, c)
+            assert off not in lds
+            lds[off] = (d, q)
+    for t in range(256):
+        for k in range(2):
+            dr, ch = (t >> 3) + 32 * k, t & 7
+            got = [lds[dr * 128 + 16 * ch + 4 * i] for i in range(4)]
+            assert got == [(dr, 4 * VT_R(ch, dr) + i) for i in range(4)]
+    for w in range(4):                         # one wave's write of column offset e
+        for e in range(8):
+            banks = [((8 * (l & 7) + e) * 128 + VT_W(8 * w + (l >> 3), l & 7)) // 4 % 64
+                     for l in range(64)]
+            assert max(banks.count(b) for b in set(banks)) <= 2
+    # negative control: the unswizzled dword (4q) piles eight lanes on a bank
+    banks = [((8 * (l & 7)) * 128 + 4 * (l >> 3)) // 4 % 64 for l in range(64)]
+    assert max(banks.count(b) for b in set(banks)) == 8
