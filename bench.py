@@ -289,6 +289,34 @@ def bench_attention(args, cfg) -> dict:
     return res
 
 
+def cpu_gemm_baseline(cfg, budget_s: float) -> dict:
+    """The GEMM row's CPU path: the layer the FP8 GEMM replaces, a bf16
+    nn.Linear, is one torch matmul on the host -- timed on all host cores over
+    a slice of the activation rows against the whole weight, scaled to the
+    workload's FLOPs."""
+    import torch
+
+    from oracle.cpu_sdpa import cpu_model, cpu_threads
+
+    threads = cpu_threads()
+    gen = torch.Generator().manual_seed(cfg.seed)
+    w = (torch.randn(cfg.K, cfg.N, generator=gen) * 0.02).to(torch.bfloat16)
+
+    def run(rows: int) -> float:
+        a = torch.randn(rows, cfg.K, generator=gen).to(torch.bfloat16)
+        t0 = time.perf_counter()
+        torch.matmul(a, w)
+        return time.perf_counter() - t0
+
+    rows, t = _grow(run, 64, cfg.M, budget_s)
+    tflops = 2.0 * rows * cfg.N * cfg.K / t / 1e12
+    return {"value": round(tflops, 4), "unit": "TFLOP/s", "cores": threads, "kind": "port",
+            "sample": (f"the layer's CPU path (bf16 nn.Linear = one torch matmul, {threads} "
+                       f"threads, {cpu_model()}): {rows} rows x K={cfg.K} x N={cfg.N} in "
+                       f"{t:.2f} s; full {cfg.name} extrapolates to "
+                       f"{cfg.flops / (tflops * 1e12):.0f} s")}
+
+
 def bench_gemm(args, cfg) -> dict:
     import torch
 
@@ -457,6 +485,9 @@ def main() -> int:
         del src, dst
     if args.config == C4.name:
         res = bench_gemm(args, C4)
+        if args.cpu_budget > 0:
+            log("[bench] timing the CPU baseline")
+            res["cpu_baseline"] = cpu_gemm_baseline(C4, args.cpu_budget)
     else:
         cfg = ATTN_CONFIGS[args.config]
         res = bench_attention(args, cfg)
