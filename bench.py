@@ -144,7 +144,7 @@ def cpu_sdpa_baseline(cfg, budget_s: float) -> dict:
 def bench_attention(args, cfg) -> dict:
     import torch
 
-    from repercep_runtime_amd import ops
+    from repercep_runtime_amd import _capi, ops
     from repercep_runtime_amd.workloads import QUANT_BYTES_PER_ELEM, attn_inputs
 
     dev = torch.device("cuda", 0)
@@ -167,7 +167,7 @@ def bench_attention(args, cfg) -> dict:
         ops.fp8_flash_attention(q, k, v, causal=cfg.causal, prefix_len=prefix,
                                 suffix_len=cfg.suffix, out=out, granularity=gran)
     splits = ops.tuned_kv_splits(cfg.B, cfg.H, cfg.Sq, cfg.Skv, cfg.D, cfg.causal, prefix,
-                                 cfg.suffix)
+                                 cfg.suffix) if args.kv_splits is None else args.kv_splits
     log(f"[bench] kv_splits {splits}")
 
     def step(ev=None):
@@ -242,6 +242,13 @@ def bench_attention(args, cfg) -> dict:
 
     tflops_step = cfg.flops / (ms_per_step * 1e-3) / 1e12
     tflops_attn = cfg.flops / (attn_ms * 1e-3) / 1e12
+    # the launches between the attention events: a balanced launch whose plan
+    # splits the last round's blocks is followed by the merge of their rows
+    mask = 1 if cfg.causal else (2 if prefix is not None else 0)
+    merged = splits != 1 and (splits > 1 or _capi.lib().rp_fp8_attn_balanced_workspace_bytes(
+        cfg.B, cfg.H, cfg.Sq, cfg.Skv, cfg.D, mask, ops._stream(q)) > 0)
+    attn_launches = ("attn_fwd_kernel + attn_combine_kernel (the merge of the key-split rows)"
+                     if merged else "attn_fwd_kernel")
     qbytes = QUANT_BYTES_PER_ELEM * cfg.quant_elems
     q_gbps = qbytes / (quant_ms * 1e-3) / 1e9
     res = {
@@ -271,6 +278,7 @@ def bench_attention(args, cfg) -> dict:
             "traffic_source": TRAFFIC_SOURCE,
             "kernel": "attn_fwd_kernel",
             "kernel_ms": round(attn_ms, 4),
+            "kernel_ms_covers": attn_launches,
         },
         "quantize": {
             "achieved_GBps": round(q_gbps, 1),
@@ -452,6 +460,10 @@ def main() -> int:
     ap.add_argument("--b-layout", choices=("kn", "nk"), default="kn",
                     help="c4_wan_ffn_up: the weight operand as the reference's fp8_gemm takes B, "
                          "(K, N) row-major (kn), or transposed (nk); the other is timed beside it")
+    ap.add_argument("--kv-splits", type=int, default=None,
+                    help="attention configs: force a launch configuration (1: one key range, "
+                         "0: the balanced launch, n > 1: n key splits) instead of the one the "
+                         "op resolves")
     ap.add_argument("--cpu-budget", type=float, default=12.0,
                     help="seconds of CPU work for the cpu_baseline sample (0 disables)")
     args = ap.parse_args()

@@ -240,6 +240,36 @@ int rp_fp8_attn_fwd_split(const uint8_t* q8, const uint8_t* k8, const uint8_t* v
                           int mask, int prefix_len, int suffix_len, int kv_splits,
                           void* workspace, size_t workspace_bytes, void* stream);
 
+/* Balanced variant of rp_fp8_attn_fwd: the launch configuration the
+ * wrapper resolves for grids of two or more rounds (the role of the
+ * reference's per-shape config resolution, fp8_flash_attn.py:461-477, here
+ * KV_SPLITS = 0).  A launch of one 256-query block per workgroup runs in
+ * rounds of one workgroup per CU, so a last partial round costs about a
+ * whole one.  For unmasked shapes whose blocks do not fill whole rounds, the
+ * largest number of query blocks per head that does runs over the whole key
+ * range, and the keys of the remaining blocks are split 2, 4 or 8 ways; both
+ * kinds of workgroup run in one launch, the split ones dispatched last, and
+ * rp_fp8_attn_fwd_split's merge follows.  E.g. (1, 40, 75600, 75600, 128) on
+ * 256 CUs runs 288 blocks per head unsplit and the last 8 split 4 ways.  Rows
+ * of the unsplit blocks are rp_fp8_attn_fwd's bit for bit; rows of the split
+ * ones are what rp_fp8_attn_fwd_split computes for them.  Shapes with
+ * nothing to split run rp_fp8_attn_fwd.  rp_fp8_attn_balanced_plan reports the
+ * plan for `cus` CUs (main_blocks: query blocks per head run unsplit;
+ * splits: key splits of the rest, 1 = a plain launch);
+ * rp_fp8_attn_balanced_workspace_bytes the workspace for the CU count of the
+ * stream's device (0: none needed). */
+int rp_fp8_attn_balanced_plan(int B, int H, int Sq, int Skv, int D, int mask, int cus,
+                              int* main_blocks, int* splits);
+size_t rp_fp8_attn_balanced_workspace_bytes(int B, int H, int Sq, int Skv, int D, int mask,
+                                            void* stream);
+int rp_fp8_attn_fwd_balanced(const uint8_t* q8, const uint8_t* k8, const uint8_t* vt8,
+                             int64_t ldv, const float* q_scale, const float* k_scale,
+                             const float* v_scale, int scale_stride, float sm_scale, void* out,
+                             int out_dtype, int64_t osb, int64_t osh, int64_t oss,
+                             int B, int H, int Sq, int Skv, int D,
+                             int mask, int prefix_len, int suffix_len,
+                             void* workspace, size_t workspace_bytes, void* stream);
+
 /* ------------------------------------------------- fused QK-norm prologue
  * rp_fp8_scale_quantize of y instead of x, where per row of D elements
  *   n = RMSNorm(x) = bf16(x * (1 / sqrt(mean(x^2) + eps)))   fp32 math

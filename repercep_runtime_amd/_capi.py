@@ -43,7 +43,9 @@ EXPORTS = (
     "rp_fp8_attn_fwd",
     "rp_fp8_attn_workspace_bytes",
     "rp_fp8_attn_blocks_per_workgroup",
-    "rp_fp8_attn_fwd_split", "rp_fp8_rmsnorm_quant_workspace_bytes",
+    "rp_fp8_attn_fwd_split", "rp_fp8_attn_balanced_plan",
+    "rp_fp8_attn_balanced_workspace_bytes", "rp_fp8_attn_fwd_balanced",
+    "rp_fp8_rmsnorm_quant_workspace_bytes",
     "rp_fp8_rmsnorm_scale_quantize", "rp_fp8_gemm", "rp_fp8_linear", "rp_fp8_transpose",
     "rp_fp8_gemm_rowwise", "rp_fp8_rowwise_quantize", "rp_transpose16",
     "rp_fp8_softmax_rowwise_quantize",
@@ -102,6 +104,13 @@ def _declare(L: ctypes.CDLL) -> None:
     L.rp_fp8_attn_fwd_split.restype = _int
     L.rp_fp8_attn_fwd_split.argtypes = (list(L.rp_fp8_attn_fwd.argtypes[:-1])
                                         + [_int, _vp, _sz, _vp])
+    L.rp_fp8_attn_balanced_plan.restype = _int
+    L.rp_fp8_attn_balanced_plan.argtypes = [_int] * 7 + [ctypes.POINTER(_int)] * 2
+    L.rp_fp8_attn_balanced_workspace_bytes.restype = _sz
+    L.rp_fp8_attn_balanced_workspace_bytes.argtypes = [_int] * 6 + [_vp]
+    L.rp_fp8_attn_fwd_balanced.restype = _int
+    L.rp_fp8_attn_fwd_balanced.argtypes = (list(L.rp_fp8_attn_fwd.argtypes[:-1])
+                                           + [_vp, _sz, _vp])
     L.rp_fp8_rmsnorm_quant_workspace_bytes.restype = _sz
     L.rp_fp8_rmsnorm_quant_workspace_bytes.argtypes = [_i64, _i64, _i64, _i64, _int]
     L.rp_fp8_rmsnorm_scale_quantize.restype = _int

@@ -60,6 +60,7 @@ namespace rp {
 namespace {
 
 constexpr int kBlockN = 128;  // keys per tile = K depth of the P.V MFMA
+constexpr int kBlockM = 32 * 8;  // query rows per workgroup
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLog2PMax = 8.807354922057604f;  // log2(448)
 
@@ -89,8 +90,16 @@ struct AttnArgs {
   // and writes partial results (running max, row sum, unnormalised O) to
   // ws_ml / ws_acc, which attn_combine_kernel merges
   int kv_splits, split_tiles;
-  float* ws_ml;   // [split][B*H][Sq] x {m, l}
-  float* ws_acc;  // [split][B*H][Sq][D]
+  float* ws_ml;   // [split][B*H][ws_rows] x {m, l}
+  float* ws_acc;  // [split][B*H][ws_rows][D]
+  // Key-split partial rows are indexed from the first row of query block
+  // qb_begin, ws_rows rows per (split, head).  A mixed launch (the balanced
+  // launch) runs query blocks [0, qb_begin) of every head over the whole key
+  // range into the output (n_main workgroups, a multiple of 8) and blocks
+  // [qb_begin, n_qblocks) key-split into the workspace.
+  int qb_begin;
+  int ws_rows;
+  int n_main;
 };
 
 // Output kinds of the attention kernel.
@@ -426,7 +435,8 @@ __device__ __forceinline__ void mfma_phase(uint32_t kl, uint32_t vl,
 // before barrier 2j.  Only group 0 loads: the slot in which a group issues
 // loads costs its SIMD VALU time, and in this slot the MFMA group, not the
 // softmax group, has VALU time to spare.
-template <int DK, int DV, int OUT, bool WINDOW, bool MULTI, bool STAGE = false>
+template <int DK, int DV, int OUT, bool WINDOW, bool MULTI, bool STAGE = false,
+          bool MIXED = false>
 __global__ __launch_bounds__(512, 1)
 void attn_fwd_kernel(AttnArgs a) {
   constexpr int NW = 8;
@@ -435,6 +445,7 @@ void attn_fwd_kernel(AttnArgs a) {
   static_assert(!MULTI || (OUT != kOutSplit && !WINDOW && DV == DK), "multi-block launches");
   static_assert(!STAGE || (MULTI && DK == 128 && (OUT == kOutBf16 || OUT == kOutF16)),
                 "staged output stores");
+  static_assert(!MIXED || (OUT != kOutSplit && !WINDOW && !MULTI), "mixed launches");
   constexpr int QROWS = 32;
   constexpr int BLOCK_M = QROWS * NW;
   // multi-block launches stage the next query block's Q in LDS: two buffers
@@ -455,20 +466,31 @@ void attn_fwd_kernel(AttnArgs a) {
   const uint32_t vbuf_lds = kbuf_lds + KST * G::K_BYTES;
   const uint32_t qbuf_lds = kbuf_lds + LDS_TILES;   // multi-block launches only
 
-  // ---- work item (XCD-aware remap of the linear workgroup id)
+  // ---- work item (XCD-aware remap of the linear workgroup id: XCD x runs
+  // the x-th contiguous share of the items, k-th item at its k-th dispatch)
   const int w = blockIdx.x;
-  const int per = a.n_work >> 3, rem = a.n_work & 7;
-  const int xcd = w & 7;
-  const int L2 = xcd * per + min(xcd, rem) + (w >> 3);
+  const int xcd = w & 7, k_x = w >> 3;
+  // a mixed launch's XCDs each run their share of the unsplit items first,
+  // then their share of the key-split ones, which fill the launch's end
+  const int pm = MIXED ? a.n_main >> 3 : 0;
+  const bool part = OUT == kOutSplit || (MIXED && k_x >= pm);
+  const int nw = MIXED && part ? a.n_work - a.n_main : a.n_work;
+  const int per = nw >> 3, rem = nw & 7;
+  const int L2 = MIXED && !part ? xcd * pm + k_x : xcd * per + min(xcd, rem) + (k_x - pm);
   // the two halves of a split query block are neighbours: same XCD, same
   // K tiles in its L2
   const int half = DV < DK ? L2 & 1 : 0;
   const int L = DV < DK ? L2 >> 1 : L2;
   const int dv_off = half * DV;  // first O column / V^T row of this workgroup
-  const int per_bh = MULTI ? a.wg_per_bh : a.n_qblocks * a.kv_splits;
+  // the items' query blocks [first_qb, first_qb + nqb) and key splits
+  const int first_qb = MIXED && !part ? 0 : a.qb_begin;
+  const int nqb = MIXED ? (part ? a.n_qblocks - a.qb_begin : a.qb_begin) : a.n_qblocks;
+  const int nsplit = MIXED && !part ? 1 : a.kv_splits;
+  const int per_bh = MULTI ? a.wg_per_bh : nqb * nsplit;
   const int bh = L / per_bh;
-  const int qb = MULTI ? (L - bh * per_bh) * a.qb_per_wg : (L - bh * per_bh) / a.kv_splits;
-  const int split = MULTI ? 0 : L - bh * per_bh - qb * a.kv_splits;
+  const int qb = MULTI ? (L - bh * per_bh) * a.qb_per_wg
+                       : (L - bh * per_bh) / nsplit + first_qb;
+  const int split = MULTI ? 0 : L - bh * per_bh - (qb - first_qb) * nsplit;
   const int nblk = MULTI ? min(a.qb_per_wg, a.n_qblocks - qb) : 1;  // query blocks
   const int b = bh / a.H, h = bh - b * a.H;
 
@@ -505,7 +527,7 @@ void attn_fwd_kernel(AttnArgs a) {
   // ---- key range [kv_begin, kv_end): this workgroup's split; causal blocks
   // past the block's last query are skipped
   const int kv_begin = split * a.split_tiles * kBlockN;
-  const int kv_end = min(a.Skv, kv_begin + a.split_tiles * kBlockN);
+  const int kv_end = MIXED && !part ? a.Skv : min(a.Skv, kv_begin + a.split_tiles * kBlockN);
   int n_kb = (kv_end - kv_begin + kBlockN - 1) / kBlockN;
   if (a.mask == RP_MASK_CAUSAL) {
     const int q_last = min(q_block0 + BLOCK_M, a.Sq) - 1;
@@ -515,7 +537,8 @@ void attn_fwd_kernel(AttnArgs a) {
     if (n_kb == 0) {  // a causal split wholly past this block's queries
       const int q0 = q_block0 + tid;
       if (tid < BLOCK_M && q0 < a.Sq) {
-        const int64_t row = ((int64_t)split * a.B * a.H + bh) * a.Sq + q0;
+        const int64_t row =
+            ((int64_t)split * a.B * a.H + bh) * a.ws_rows + (q0 - a.qb_begin * BLOCK_M);
         if (half == 0) {
           a.ws_ml[2 * row] = -__builtin_inff();
           a.ws_ml[2 * row + 1] = 0.0f;
@@ -877,24 +900,27 @@ void attn_fwd_kernel(AttnArgs a) {
   }
 
   // ---- epilogue: the (last) query block's output, or a split's partials
-  if constexpr (OUT == kOutSplit) {
-    const float l = xhalf_sum(l_run);
-    // partial result of this key split, relative to its own running max
-    if (q < a.Sq) {
-      const int64_t row = ((int64_t)split * a.B * a.H + bh) * a.Sq + q;
-      float* dst = a.ws_acc + row * D + dv_off;
+  if constexpr (OUT == kOutSplit || MIXED) {
+    if (part) {
+      const float l = xhalf_sum(l_run);
+      // partial result of this key split, relative to its own running max
+      if (q < a.Sq) {
+        const int64_t row =
+            ((int64_t)split * a.B * a.H + bh) * a.ws_rows + (q - a.qb_begin * BLOCK_M);
+        float* dst = a.ws_acc + row * D + dv_off;
 #pragma unroll
-      for (int e = 0; e < G::ETILES; ++e)
+        for (int e = 0; e < G::ETILES; ++e)
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-          *reinterpret_cast<float4*>(dst + 32 * e + 8 * i + 4 * lg) =
-              make_float4(acc[e][4 * i], acc[e][4 * i + 1], acc[e][4 * i + 2], acc[e][4 * i + 3]);
-      if (lg == 0 && half == 0)
-        *reinterpret_cast<float2*>(a.ws_ml + 2 * row) = make_float2(m_run, l);
+          for (int i = 0; i < 4; ++i)
+            *reinterpret_cast<float4*>(dst + 32 * e + 8 * i + 4 * lg) =
+                make_float4(acc[e][4 * i], acc[e][4 * i + 1], acc[e][4 * i + 2], acc[e][4 * i + 3]);
+        if (lg == 0 && half == 0)
+          *reinterpret_cast<float2*>(a.ws_ml + 2 * row) = make_float2(m_run, l);
+      }
+      return;
     }
-    return;
   }
-  store_out(q, l_run, (nblk - 1) & 1);
+  if constexpr (OUT != kOutSplit) store_out(q, l_run, (nblk - 1) & 1);
 }
 
 // Merge the key splits of one query row: with m_j, l_j, O_j the running
@@ -907,7 +933,7 @@ template <int D, int OUT>
 __global__ __launch_bounds__(256)
 void attn_combine_kernel(AttnArgs a) {
   constexpr int CH = D / 4;
-  const int64_t rows = (int64_t)a.B * a.H * a.Sq;
+  const int64_t rows = (int64_t)a.B * a.H * a.ws_rows;
   const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
   const int64_t row = t / CH;
   if (row >= rows) return;
@@ -930,7 +956,8 @@ void attn_combine_kernel(AttnArgs a) {
     l += w * v.y;
     o.x += w * x.x; o.y += w * x.y; o.z += w * x.z; o.w += w * x.w;
   }
-  const int bh = (int)(row / a.Sq), q = (int)(row - (int64_t)bh * a.Sq);
+  const int bh = (int)(row / a.ws_rows);
+  const int q = (int)(row - (int64_t)bh * a.ws_rows) + a.qb_begin * kBlockM;
   const int b = bh / a.H, h = bh - b * a.H;
   const float inv = a.vs[bh * a.scale_stride] / l;
   const int64_t obase = (int64_t)b * a.osb + (int64_t)h * a.osh + (int64_t)q * a.oss + d;
@@ -978,6 +1005,15 @@ void launch_fwd(const AttnArgs& a, hipStream_t st) {
     hipLaunchKernelGGL((attn_fwd_kernel<D, DV, OUT, false, false>), grid, block, 0, st, a);
 }
 
+// The balanced launch: the unsplit query blocks into the output, the rest
+// key-split into the workspace (attn_combine_kernel merges them after).
+template <int D, int OUT>
+void launch_fwd_mixed(const AttnArgs& a, hipStream_t st) {
+  constexpr int DV = kPVWidth<D>;
+  hipLaunchKernelGGL((attn_fwd_kernel<D, DV, OUT, false, false, false, true>), dim3(a.n_work),
+                     dim3(512), 0, st, a);
+}
+
 // Multi-block launches pay off where a workgroup's fixed cost (Q load,
 // first-tile latency, pipeline fill and drain, output store, all serialised
 // with one workgroup per CU) is large against its key tiles: short,
@@ -994,7 +1030,8 @@ constexpr int64_t kFixedTiles = 7, kSwitchTiles = 1;
 inline int multi_block_plan(const AttnArgs& a, int D) {
   const int n_kb = (a.Skv + kBlockN - 1) / kBlockN;
   const int64_t heads = (int64_t)a.B * a.H;
-  if (a.mask != RP_MASK_NONE || a.kv_splits != 1 || D > 128 || n_kb > kMultiMaxTiles)
+  if (a.mask != RP_MASK_NONE || a.kv_splits != 1 || D > 128 || n_kb > kMultiMaxTiles ||
+      a.qb_begin != 0)
     return 1;
   auto rounds = [&](int64_t wgs) { return (wgs + kCUs - 1) / kCUs; };
   int best = 1;
@@ -1010,7 +1047,6 @@ inline int multi_block_plan(const AttnArgs& a, int D) {
   return best;
 }
 
-constexpr int kBlockM = 32 * 8;  // query rows per workgroup
 
 // Key tiles per split and the number of non-empty splits for a request of
 // `kv_splits`.
@@ -1019,6 +1055,65 @@ inline void split_plan(int Skv, int kv_splits, int* split_tiles, int* n_splits) 
   const int want = max(1, min(kv_splits, n_kb));
   *split_tiles = (n_kb + want - 1) / want;
   *n_splits = (n_kb + *split_tiles - 1) / *split_tiles;
+}
+
+// Balanced launches.  A launch of W workgroups, one per CU, runs in
+// ceil(W / CUs) rounds of equal length (measured at the Wan shape: 45, 46
+// and 47 rounds take 48.7, 49.9 and 51.2 ms), so a last partial round costs
+// a whole one.  For an unmasked launch of one query block per workgroup the
+// plan keeps the largest number of query blocks per head whose workgroups
+// fill whole rounds, and splits the keys of the remaining blocks s ways
+// (s = 2, 4 or 8), so that their workgroups, each about 1/s of a whole one,
+// fill the last rounds; attn_combine_kernel merges their partial results.
+// C3 self (40 heads x 296 blocks on 256 CUs): 288 blocks per head in 45
+// rounds, the last 8 split 4 ways in 1.25 round-equivalents, against 47.
+// Both kinds of workgroup run in one launch, the split ones dispatched last
+// on every XCD: they also fill the uneven end of the unsplit rounds, which
+// a second launch would wait for.
+struct TailPlan {
+  int main_blocks;   // query blocks per head run unsplit
+  int splits;        // key splits of the remaining blocks (1: a plain launch)
+};
+inline TailPlan tail_plan(int B, int H, int Sq, int Skv, int D, int mask, int cus) {
+  const int nq = (Sq + kBlockM - 1) / kBlockM;
+  TailPlan t{nq, 1};
+  if (mask != RP_MASK_NONE || cus <= 0 || B <= 0 || H <= 0 || Sq <= 0 || Skv <= 0) return t;
+  AttnArgs a{};
+  a.B = B; a.H = H; a.Sq = Sq; a.Skv = Skv; a.mask = mask; a.kv_splits = 1; a.n_qblocks = nq;
+  if (multi_block_plan(a, D) > 1) return t;
+  const int n_kb = (Skv + kBlockN - 1) / kBlockN;
+  const int64_t per_block = (int64_t)B * H * (D == 256 ? 2 : 1);   // workgroups per block row
+  int64_t g = per_block, c = cus;
+  while (c) { const int64_t r = g % c; g = c; c = r; }             // gcd(per_block, cus)
+  const int64_t step = cus / g;      // blocks per head that fill whole rounds
+  const int64_t m = (nq / step) * step;
+  // the unsplit workgroups spread evenly over the 8 XCDs
+  if (m == nq || m == 0 || (per_block * m) % 8 != 0) return t;
+  const int64_t tail = per_block * (nq - m);
+  auto rounds = [&](int64_t w, int s) { return (double)((w + cus - 1) / cus) / s; };
+  double best = rounds(tail, 1);
+  int best_s = 1;
+  for (int sp = 2; sp <= 8 && 2 * sp <= n_kb; sp *= 2) {
+    // ~0.05 of a round for the partial results and the merge
+    const double cost = rounds(tail * sp, sp) + 0.05;
+    if (cost < best) {
+      best = cost;
+      best_s = sp;
+    }
+  }
+  if (best_s > 1) t = TailPlan{(int)m, best_s};
+  return t;
+}
+
+// CUs of the stream's device (its current device for a null stream); 0 when
+// the runtime cannot tell.
+inline int stream_cus(void* stream) {
+  int dev = 0, v = 0;
+  const hipError_t e = stream ? hipStreamGetDevice(static_cast<hipStream_t>(stream), &dev)
+                              : hipGetDevice(&dev);
+  if (e != hipSuccess) return 0;
+  if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+  return v;
 }
 
 // kOutBf16 / kOutF32 / kOutF16 for an RP_OUT_* value
@@ -1035,14 +1130,24 @@ int launch_attn(const AttnArgs& base, int out_dtype, hipStream_t st) {
   a.dv_halves = D / kPVWidth<D>;
   a.qb_per_wg = multi_block_plan(a, D);
   a.wg_per_bh = (a.n_qblocks + a.qb_per_wg - 1) / a.qb_per_wg;
-  const int64_t work = a.qb_per_wg > 1
-                           ? (int64_t)a.wg_per_bh * a.B * a.H
-                           : (int64_t)a.n_qblocks * a.B * a.H * a.kv_splits * a.dv_halves;
+  // a mixed launch: blocks [0, qb_begin) unsplit, the rest key-split
+  const bool mixed = a.qb_begin > 0;
+  const int64_t heads = (int64_t)a.B * a.H * a.dv_halves;
+  const int64_t work =
+      a.qb_per_wg > 1 ? (int64_t)a.wg_per_bh * a.B * a.H
+      : mixed ? heads * (a.qb_begin + (int64_t)(a.n_qblocks - a.qb_begin) * a.kv_splits)
+              : heads * a.n_qblocks * a.kv_splits;
   if (work > 0x7fffffff || (int64_t)a.B * a.H * a.Sq * (D / 4) > 0x7fffffffLL * 256) {
     rp_set_error("attn: grid too large");
     return RP_ERR_UNSUPPORTED;
   }
   a.n_work = (int)work;
+  a.n_main = mixed ? (int)(heads * a.qb_begin) : 0;
+  if (mixed && (a.n_main % 8 != 0 || a.kv_splits < 2 || a.mask != RP_MASK_NONE)) {
+    rp_set_error("attn: mixed launch needs unsplit workgroups in multiples of 8, key splits "
+                 "and no mask");
+    return RP_ERR_UNSUPPORTED;
+  }
   if (a.kv_splits == 1) {
     if (kind == kOutF32)
       launch_fwd<D, kOutF32>(a, st);
@@ -1051,8 +1156,15 @@ int launch_attn(const AttnArgs& base, int out_dtype, hipStream_t st) {
     else
       launch_fwd<D, kOutBf16>(a, st);
   } else {
-    launch_fwd<D, kOutSplit>(a, st);
-    const int64_t threads = (int64_t)a.B * a.H * a.Sq * (D / 4);
+    if (!mixed)
+      launch_fwd<D, kOutSplit>(a, st);
+    else if (kind == kOutF32)
+      launch_fwd_mixed<D, kOutF32>(a, st);
+    else if (kind == kOutF16)
+      launch_fwd_mixed<D, kOutF16>(a, st);
+    else
+      launch_fwd_mixed<D, kOutBf16>(a, st);
+    const int64_t threads = (int64_t)a.B * a.H * a.ws_rows * (D / 4);
     const dim3 cgrid((unsigned)((threads + 255) / 256)), cblock(256);
     if (kind == kOutF32)
       hipLaunchKernelGGL((attn_combine_kernel<D, kOutF32>), cgrid, cblock, 0, st, a);
@@ -1141,6 +1253,9 @@ int attn_setup(AttnArgs& a, const uint8_t* q8, const uint8_t* k8, const uint8_t*
   a.mask = mask; a.prefix = prefix_len; a.suffix = suffix_len > 0 ? suffix_len : 1;
   a.kv_splits = 1;
   a.split_tiles = (Skv + kBlockN - 1) / kBlockN;
+  a.qb_begin = 0;
+  a.ws_rows = Sq;
+  a.n_main = 0;
   return RP_OK;
 }
 
@@ -1221,5 +1336,68 @@ extern "C" int rp_fp8_attn_fwd_split(const uint8_t* q8, const uint8_t* k8, const
     a.ws_acc = reinterpret_cast<float*>(static_cast<char*>(workspace) +
                                         (rows * 2 * sizeof(float) + 255) / 256 * 256);
   }
+  return attn_run(a, D, out_dtype, stream);
+}
+
+extern "C" int rp_fp8_attn_balanced_plan(int B, int H, int Sq, int Skv, int D, int mask, int cus,
+                                         int* main_blocks, int* splits) {
+  if (!main_blocks || !splits) {
+    rp_set_error("attn: null pointer");
+    return RP_ERR_INVALID_ARGUMENT;
+  }
+  const TailPlan t = tail_plan(B, H, Sq, Skv, D, mask, cus);
+  *main_blocks = t.main_blocks;
+  *splits = t.splits;
+  return RP_OK;
+}
+
+// Workspace of rp_fp8_attn_fwd_balanced: the key-split partial results of
+// the rows past the unsplit blocks.
+static size_t balanced_ws_bytes(const TailPlan& t, int B, int H, int Sq, int Skv, int D) {
+  if (t.splits <= 1) return 0;
+  int split_tiles = 0, n_splits = 1;
+  split_plan(Skv, t.splits, &split_tiles, &n_splits);
+  return rp_fp8_attn_workspace_bytes(B, H, Sq - t.main_blocks * kBlockM, D, n_splits);
+}
+
+extern "C" size_t rp_fp8_attn_balanced_workspace_bytes(int B, int H, int Sq, int Skv, int D,
+                                                       int mask, void* stream) {
+  if (D != 32 && D != 64 && D != 128 && D != 256) return 0;
+  return balanced_ws_bytes(tail_plan(B, H, Sq, Skv, D, mask, stream_cus(stream)), B, H, Sq, Skv,
+                           D);
+}
+
+extern "C" int rp_fp8_attn_fwd_balanced(const uint8_t* q8, const uint8_t* k8, const uint8_t* vt8,
+                                        int64_t ldv, const float* q_scale, const float* k_scale,
+                                        const float* v_scale, int scale_stride, float sm_scale,
+                                        void* out, int out_dtype, int64_t osb, int64_t osh,
+                                        int64_t oss, int B, int H, int Sq, int Skv, int D,
+                                        int mask, int prefix_len, int suffix_len, void* workspace,
+                                        size_t workspace_bytes, void* stream) {
+  AttnArgs a;
+  int rc = attn_setup(a, q8, k8, vt8, ldv, q_scale, k_scale, v_scale, scale_stride, sm_scale,
+                      out, out_dtype, osb, osh, oss, B, H, Sq, Skv, D, mask, prefix_len,
+                      suffix_len);
+  if (rc != RP_OK) return rc;
+  const TailPlan t = tail_plan(B, H, Sq, Skv, D, mask, stream_cus(stream));
+  if (t.splits <= 1) return attn_run(a, D, out_dtype, stream);
+  const size_t need = balanced_ws_bytes(t, B, H, Sq, Skv, D);
+  if (!workspace || workspace_bytes < need || reinterpret_cast<uintptr_t>(workspace) % 256 != 0) {
+    rp_set_error("attn: workspace of %zu bytes (256-byte aligned) needed for the balanced launch "
+                 "(rp_fp8_attn_balanced_workspace_bytes)", need);
+    return RP_ERR_INVALID_ARGUMENT;
+  }
+  // one launch: query blocks [0, main_blocks) of every head unsplit, then
+  // rows [main_blocks * 256, Sq) of every head key-split; the merge after
+  int split_tiles = 0, n_splits = 1;
+  split_plan(Skv, t.splits, &split_tiles, &n_splits);
+  a.qb_begin = t.main_blocks;
+  a.ws_rows = Sq - t.main_blocks * kBlockM;
+  a.kv_splits = n_splits;
+  a.split_tiles = split_tiles;
+  const size_t rows = (size_t)n_splits * B * H * a.ws_rows;
+  a.ws_ml = static_cast<float*>(workspace);
+  a.ws_acc = reinterpret_cast<float*>(static_cast<char*>(workspace) +
+                                      (rows * 2 * sizeof(float) + 255) / 256 * 256);
   return attn_run(a, D, out_dtype, stream);
 }

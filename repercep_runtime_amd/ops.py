@@ -36,6 +36,8 @@ SUPPORTED_HEAD_DIMS = frozenset({32, 64, 128, 256})
 #: keys per tile of the attention kernel.  Numerically significant: the
 #: running max after each tile sets the grid P is quantized on.
 BLOCK_N = 128
+#: query rows per block of the attention kernel (one workgroup's rows)
+BLOCK_M = 256
 #: row padding of the transposed V operand
 V_PAD = 128
 
@@ -333,7 +335,10 @@ def attention_fp8(q8: torch.Tensor, k8: torch.Tensor, vt8: torch.Tensor, q_scale
     ``out`` may be any (B, H, Sq, D)-shaped view with a contiguous last dim
     (e.g. a permuted (B, S, H, D) buffer).  ``prefix_len``/``suffix_len``
     select the shared-prefix candidate mask.  ``kv_splits`` > 1 runs the key
-    range in that many parts and merges them (``rp_fp8_attn_fwd_split``).
+    range in that many parts and merges them (``rp_fp8_attn_fwd_split``);
+    0 runs the balanced launch (``rp_fp8_attn_fwd_balanced``): the query
+    blocks that fill whole rounds of workgroups over one key range, the rest
+    key-split.
     """
     _check_cuda("q8", q8)
     _on_device_of(q8, k8=k8, vt8=vt8, q_scale=q_scale, k_scale=k_scale, v_scale=v_scale,
@@ -370,8 +375,18 @@ def attention_fp8(q8: torch.Tensor, k8: torch.Tensor, vt8: torch.Tensor, q_scale
     args = (q8.data_ptr(), k8.data_ptr(), vt8.data_ptr(), ldv, qs.data_ptr(), ks.data_ptr(),
             vs.data_ptr(), stride, float(sm_scale), out.data_ptr(), odt, out.stride(0),
             out.stride(1), out.stride(2), B, H, Sq, Skv, D, mask, pre, suf)
+    if kv_splits < 0:
+        raise ValueError(f"kv_splits={kv_splits} must be >= 0")
     if kv_splits == 1:
         C.check(C.lib().rp_fp8_attn_fwd(*args, _stream(q8)), "rp_fp8_attn_fwd")
+    elif kv_splits == 0:
+        # whole rounds of workgroups over one key range, the query blocks of
+        # the last partial round key-split so that they fill the GPU
+        nbytes = C.lib().rp_fp8_attn_balanced_workspace_bytes(B, H, Sq, Skv, D, mask,
+                                                              _stream(q8))
+        ws = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=q8.device)
+        C.check(C.lib().rp_fp8_attn_fwd_balanced(*args, ws.data_ptr(), ws.numel(),
+                                                 _stream(q8)), "rp_fp8_attn_fwd_balanced")
     else:
         nbytes = C.lib().rp_fp8_attn_workspace_bytes(B, H, Sq, D, int(kv_splits))
         ws = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=q8.device)
@@ -453,11 +468,15 @@ def tuned_kv_splits(B: int, H: int, Sq: int, Skv: int, D: int, causal: bool = Fa
                     prefix_len: int | None = None, suffix_len: int | None = None) -> int:
     """The split count ``fp8_flash_attention`` uses for a shape without
     searching: the fallback when autotuning is disabled, else the cached
-    entry (1 on a miss)."""
+    entry; on a miss the one candidate of a shape that needs no search (the
+    balanced launch of a large grid), else 1."""
     if tuning.autotune_disabled():
         return int(tuning.FALLBACK_CONFIG["KV_SPLITS"])
     cfg = tuning.resolve_config(B, H, Sq, Skv, D, causal, prefix_len, suffix_len)
-    return int(cfg.get("KV_SPLITS", 1)) if cfg else 1
+    if cfg:
+        return int(cfg.get("KV_SPLITS", 1))
+    cands = tuning.candidate_configs(B, H, Sq, Skv)
+    return int(cands[0]["KV_SPLITS"]) if len(cands) == 1 else 1
 
 
 def _resolve_kv_splits(B: int, H: int, Sq: int, Skv: int, D: int, causal: bool,

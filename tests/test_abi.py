@@ -211,6 +211,42 @@ def test_multi_block_launch_plan() -> None:
     assert plan(0, 40, 75600, 512, 128, 0, 1) == 0           # invalid
 
 
+def test_balanced_launch_plan() -> None:
+    """rp_fp8_attn_balanced_plan: the query blocks per head that fill whole
+    rounds of workgroups on `cus` compute units run unsplit, the rest key-split
+    2, 4 or 8 ways when that shortens the last round; masks, multi-block
+    shapes, whole rounds and unknown CU counts keep one plain launch."""
+    L = _capi.lib()
+
+    def plan(B, H, Sq, Skv, D, mask=0, cus=256):
+        m, s = ctypes.c_int(), ctypes.c_int()
+        assert L.rp_fp8_attn_balanced_plan(B, H, Sq, Skv, D, mask, cus, ctypes.byref(m),
+                                           ctypes.byref(s)) == 0
+        return m.value, s.value
+
+    # C3 self: 40 heads x 296 blocks; 288 per head fill 45 rounds, the last
+    # 8 x 40 = 320 workgroups split 4 ways take 1.25 round-equivalents
+    assert plan(1, 40, 75600, 75600, 128) == (288, 4)
+    # C2: 32 heads x 220 blocks; 216 fill 27 rounds, 128 tail workgroups x 2
+    assert plan(1, 32, 56320, 56320, 128) == (216, 2)
+    assert plan(1, 20, 75600, 75600, 256) == (288, 4)        # D=256: two halves per block
+    assert plan(1, 8, 8860, 8192, 128) == (32, 8)            # 24 tail workgroups
+    assert plan(1, 40, 75600, 75600, 128, mask=1) == (296, 1)     # causal
+    assert plan(1, 40, 75600, 75600, 128, mask=2) == (296, 1)     # shared prefix
+    assert plan(1, 40, 75600, 512, 128) == (296, 1)          # multi-block launch instead
+    assert plan(1, 32, 65536, 65536, 128) == (256, 1)        # whole rounds already
+    assert plan(1, 8, 8860, 512, 128) == (35, 1)             # 4 key tiles: 8 ways too few
+    assert plan(1, 40, 75600, 75600, 128, cus=0) == (296, 1)      # CU count unknown
+    # 304 CUs: 266 blocks per head fill whole rounds, the other 1200
+    # workgroups take 3.95 rounds unsplit, which splitting cannot shorten
+    assert plan(1, 40, 75600, 75600, 128, cus=304) == (296, 1)
+    assert L.rp_fp8_attn_balanced_plan(1, 1, 1, 1, 128, 0, 256, None, None) != 0
+    # workspace for the split tail only: 4 splits x 40 heads x 1872 rows
+    rows = 4 * 40 * (75600 - 288 * 256)
+    ml = (rows * 8 + 255) // 256 * 256
+    assert L.rp_fp8_attn_workspace_bytes(1, 40, 75600 - 288 * 256, 128, 4) == ml + rows * 512
+
+
 def test_qkv_quantizer_argument_checks() -> None:
     L = _capi.lib()
     args = [FAKE, FAKE, FAKE, _capi.RP_DTYPE_BF16, 1, 2, 64, 128, 64,

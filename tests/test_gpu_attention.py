@@ -336,6 +336,63 @@ def test_key_splits_vs_oracle(gpu: torch.device, case: tuple) -> None:
             _check(out[b], ref1, f"{name} kv_splits={n} b={b} vs one range", rel_tol=5e-2)
 
 
+BALANCED_CASES = [
+    # name, B, H, Sq, Skv, D, out dtype; on 256 CUs the plans are (32, 8):
+    # 24 (D=128) / 16 (D=256, two halves) tail workgroups split 8 ways
+    ("d128", 1, 8, 8860, 8192, 128, torch.float32),
+    ("d128_bf16", 1, 8, 8860, 8192, 128, torch.bfloat16),
+    ("d256", 1, 4, 8548, 4096, 256, torch.float32),
+]
+
+
+@pytest.mark.parametrize("case", BALANCED_CASES, ids=[c[0] for c in BALANCED_CASES])
+def test_balanced_launch_vs_oracle(gpu: torch.device, case: tuple) -> None:
+    """rp_fp8_attn_fwd_balanced (kv_splits=0): the query blocks of the
+    unsplit launch are the plain launch's bits; the rows of the key-split
+    tail match the split emulation with the plan's split count (bit-exact
+    codes in, the usual tolerance out) and the one-range oracle to the FP8
+    tolerance."""
+    import ctypes
+
+    from repercep_runtime_amd import _capi
+
+    name, B, H, Sq, Skv, D, odt = case
+    cus = torch.cuda.get_device_properties(gpu).multi_processor_count
+    m, s = ctypes.c_int(), ctypes.c_int()
+    assert _capi.lib().rp_fp8_attn_balanced_plan(B, H, Sq, Skv, D, 0, cus, ctypes.byref(m),
+                                                 ctypes.byref(s)) == 0
+    main, splits = m.value, s.value
+    if cus == 256:
+        assert (main, splits) == (32, 8)
+    if splits == 1:
+        pytest.skip(f"no tail split on {cus} CUs")
+    g = torch.Generator().manual_seed(sum(map(ord, name)))
+    q = torch.randn(B, H, Sq, D, generator=g).to(torch.bfloat16)
+    k = torch.randn(B, H, Skv, D, generator=g).to(torch.bfloat16)
+    v = torch.randn(B, H, Skv, D, generator=g).to(torch.bfloat16)
+    qg, kg, vg = q.to(gpu), k.to(gpu), v.to(gpu)
+    one = ops.fp8_flash_attention(qg, kg, vg, out_dtype=odt, kv_splits=1)
+    bal = ops.fp8_flash_attention(qg, kg, vg, out_dtype=odt, kv_splits=0)
+    torch.cuda.synchronize()
+    r0 = main * ops.BLOCK_M
+    assert torch.equal(bal[:, :, :r0].view(torch.int16 if odt != torch.float32 else torch.int32),
+                       one[:, :, :r0].view(torch.int16 if odt != torch.float32 else torch.int32))
+    tail = np.arange(r0, Sq)
+    n_kb = -(-Skv // 128)
+    split_keys = -(-n_kb // min(splits, n_kb)) * 128
+    qs8, ks8, vs8 = (native.quantize_groups(bf16_bits(t), B * H) for t in (q, k, v))
+    got = bal[0, :, r0:].float().cpu().numpy()
+    for h in range(H):
+        ref = attention.emulate_key_splits(qs8[1][0, h], ks8[1][0, h], vs8[1][0, h], qs8[0][h],
+                                           ks8[0][h], vs8[0][h], D ** -0.5, tail,
+                                           split_keys=split_keys)
+        if odt != torch.float32:
+            ref = torch.from_numpy(ref).to(odt).float().numpy()
+        _check(got[h], ref, f"{name} tail h={h}")
+    ref1, _ = _oracle_rows(q, k, v, list(range(H)), tail, sm_scale=D ** -0.5)
+    _check(got, ref1, f"{name} tail vs one range", rel_tol=5e-2)
+
+
 def test_autotune_records_and_reuses_a_split_count(gpu: torch.device, tmp_path,
                                                    monkeypatch: pytest.MonkeyPatch) -> None:
     """Cache miss -> timed search over the candidates, winner recorded under
@@ -460,6 +517,53 @@ def test_wan_self_attention_full_shape_sampled_rows(gpu: torch.device, granulari
 def test_wan_cross_attention_full_shape_sampled_rows(gpu: torch.device, granularity: str) -> None:
     """C3 cross (Skv = 512): 512 rows x 4 heads vs oracle, both granularities."""
     _wan_sample(gpu, C3_CROSS, [0, 5, 20, 39], 512, granularity)
+
+
+def test_wan_self_balanced_launch_full_shape(gpu: torch.device) -> None:
+    """C3 self through the launch the op resolves for it when autotuning is on
+    (kv_splits=0, the balanced launch) with per-tensor scales, as the bench
+    runs it: 64 sampled rows of the unsplit query blocks against the
+    one-range oracle, 64 of the key-split tail against the split emulation
+    with the plan's count."""
+    import ctypes
+
+    from repercep_runtime_amd import _capi
+
+    cfg = C3_SELF
+    cus = torch.cuda.get_device_properties(gpu).multi_processor_count
+    m, s = ctypes.c_int(), ctypes.c_int()
+    assert _capi.lib().rp_fp8_attn_balanced_plan(cfg.B, cfg.H, cfg.Sq, cfg.Skv, cfg.D, 0, cus,
+                                                 ctypes.byref(m), ctypes.byref(s)) == 0
+    main, splits = m.value, s.value
+    if cus == 256:
+        assert (main, splits) == (288, 4)
+    if splits == 1:
+        pytest.skip(f"no tail split on {cus} CUs")
+    q, k, v = attn_inputs(cfg, device=gpu)
+    out = ops.fp8_flash_attention(q, k, v, out_dtype=torch.float32, granularity="tensor",
+                                  kv_splits=0)
+    torch.cuda.synchronize()
+    heads = [0, 21, 39]
+    r0 = main * ops.BLOCK_M
+    rng = np.random.default_rng(3)
+    rows_main = np.sort(rng.choice(r0, size=64, replace=False))
+    rows_tail = np.sort(rng.choice(np.arange(r0, cfg.Sq), size=64, replace=False))
+    ora = [_group_scales_codes(t.cpu(), heads, "tensor") for t in (q, k, v)]
+    n_kb = -(-cfg.Skv // 128)
+    split_keys = -(-n_kb // min(splits, n_kb)) * 128
+    sm = cfg.D ** -0.5
+    for rows, tail in ((rows_main, False), (rows_tail, True)):
+        got = out[0, heads][:, torch.from_numpy(rows).to(gpu)].cpu().numpy()
+        refs = []
+        for h in heads:
+            args = (ora[0][1][h], ora[1][1][h], ora[2][1][h], ora[0][0][h], ora[1][0][h],
+                    ora[2][0][h], sm, rows)
+            refs.append(attention.emulate_key_splits(*args, split_keys=split_keys) if tail
+                        else native.attn_rows(*args, block_n=ops.BLOCK_N))
+        _check(got, np.stack(refs), f"c3 balanced {'tail' if tail else 'unsplit'} rows")
+    assert torch.isfinite(out).all()
+    del q, k, v, out
+    torch.cuda.empty_cache()
 
 
 def test_cosmos_full_shape_per_tensor_through_fused_qknorm(gpu: torch.device) -> None:

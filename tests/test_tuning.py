@@ -69,7 +69,11 @@ def test_foreign_and_legacy_entries(cache_file: Path) -> None:
     cache_file.write_text(json.dumps({key: legacy}))
     assert tuning.resolve_config(1, 8, 8192, 8192, 128, False) == legacy
     assert ops.tuned_kv_splits(1, 8, 8192, 8192, 128) == 1
-    for bad in ({**legacy, "KV_SPLITS": 0}, {**legacy, "KV_SPLITS": "4"},
+    balanced = {**legacy, "KV_SPLITS": 0}       # the balanced launch
+    cache_file.write_text(json.dumps({key: balanced}))
+    assert tuning.resolve_config(1, 8, 8192, 8192, 128, False) == balanced
+    assert ops.tuned_kv_splits(1, 8, 8192, 8192, 128) == 0
+    for bad in ({**legacy, "KV_SPLITS": -1}, {**legacy, "KV_SPLITS": "4"},
                 {**legacy, "KV_SPLITS": True}, {"BLOCK_M": 256}):
         cache_file.write_text(json.dumps({key: bad}))
         assert tuning.resolve_config(1, 8, 8192, 8192, 128, False) == {}
@@ -97,10 +101,11 @@ def test_prefix_key_and_disable_switch(cache_file: Path, monkeypatch: pytest.Mon
 
 
 def test_candidates_only_split_small_grids() -> None:
-    big = tuning.candidate_configs(C3_SELF.B, C3_SELF.H, C3_SELF.Sq, C3_SELF.Skv)
-    assert big == [tuning.FALLBACK_CONFIG]                       # 11,840 workgroups: no search
+    # 11,840 workgroups: no search, the balanced launch
+    balanced = [{**tuning.FALLBACK_CONFIG, "KV_SPLITS": 0}]
+    assert tuning.candidate_configs(C3_SELF.B, C3_SELF.H, C3_SELF.Sq, C3_SELF.Skv) == balanced
     assert tuning.candidate_configs(C3_CROSS.B, C3_CROSS.H, C3_CROSS.Sq,
-                                    C3_CROSS.Skv) == [tuning.FALLBACK_CONFIG]
+                                    C3_CROSS.Skv) == balanced
     small = tuning.candidate_configs(C1.B, C1.H, C1.Sq, C1.Skv)   # 32 workgroups, 8 key tiles
     assert [c["KV_SPLITS"] for c in small] == [1, 2, 4, 8]
     # 5 key tiles: requests 1, 2, 4, 5 give ranges of 5, 3, 2, 1 tiles
@@ -110,6 +115,12 @@ def test_candidates_only_split_small_grids() -> None:
     assert [c["KV_SPLITS"] for c in tuning.candidate_configs(1, 1, 256, 17 * 128)] == \
         [1, 2, 4, 6, 9, 17]
     assert [c["KV_SPLITS"] for c in tuning.candidate_configs(1, 1, 256, 100)] == [1]
+
+
+def test_a_large_grid_resolves_to_the_balanced_launch_without_a_search(cache_file: Path) -> None:
+    assert ops.tuned_kv_splits(C3_SELF.B, C3_SELF.H, C3_SELF.Sq, C3_SELF.Skv, C3_SELF.D) == 0
+    assert ops.tuned_kv_splits(C1.B, C1.H, C1.Sq, C1.Skv, C1.D) == 1   # searched: 1 on a miss
+    assert not cache_file.exists()
 
 
 def test_autotune_picks_the_fastest() -> None:
