@@ -483,11 +483,12 @@ void gemm256_kernel(GemmArgs g) {
   const uint32_t tail_back = (uint32_t)(((lane >> 2) ^ wave) & 1) * 64;
   // (K, N) B: loads n >= kG2ALoads + 4 fill K rows 64..127 of the slice
   const uint32_t tail_back_kn = (uint32_t)(64 * g.ldb);
-  // load n of slice kk into `slot`
-  auto issue = [&](int n, int kk, int slot) __attribute__((always_inline)) {
+  // load n of slice kk into `slot` (FULL: kk is not a half tail slice)
+  auto issue = [&](int n, int kk, int slot, auto full_c) __attribute__((always_inline)) {
+    constexpr bool FULL = decltype(full_c)::value;
     uint32_t off = gofs[n];
     const bool is_a = n < kG2ALoads;
-    if (half_tail && kk == nslice - 1) {
+    if (!FULL && half_tail && kk == nslice - 1) {
       if (KN && !is_a) off -= n >= kG2ALoads + 4 ? tail_back_kn : 0u;
       else off -= tail_back;
     }
@@ -539,10 +540,10 @@ void gemm256_kernel(GemmArgs g) {
   // (2kk + 1) % 5.  prologue: slices 0 and 1 in flight, wait for slice 0,
   // read sub-slice 0
 #pragma unroll
-  for (int n = 0; n < kG2Loads; ++n) issue(n, 0, n < kG2ALoads ? 0 : 1);
+  for (int n = 0; n < kG2Loads; ++n) issue(n, 0, n < kG2ALoads ? 0 : 1, std::false_type{});
   if (nslice > 1) {
 #pragma unroll
-    for (int n = 0; n < kG2Loads; ++n) issue(n, 1, n < kG2ALoads ? 2 : 3);
+    for (int n = 0; n < kG2Loads; ++n) issue(n, 1, n < kG2ALoads ? 2 : 3, std::false_type{});
     g2_wait_vmem<kG2Loads>();
   } else {
     g2_wait_vmem<0>();
@@ -562,12 +563,15 @@ void gemm256_kernel(GemmArgs g) {
   // sub-steps to land.  Sub-step (kk, 1) begins with the slice's one wait
   // and barrier: slice kk + 1 (read from here on) has landed, and every wave
   // has finished reading slice kk.
+  // STEADY sub-steps (kk + 2 < nslice - 1) load a full slice and read a
+  // next sub-slice unconditionally: no branches between their MFMAs.
   int sa = 0;   // slot of slice kk's A part
-  auto sub = [&](int kk, auto Hc, G2Ops& cur, G2Ops& nxt) __attribute__((always_inline)) {
+  auto sub = [&](int kk, auto Hc, auto Sc, G2Ops& cur, G2Ops& nxt) __attribute__((always_inline)) {
     constexpr int H = decltype(Hc)::value;
+    constexpr bool STEADY = decltype(Sc)::value;
     const int u = 2 * kk + H;
-    const bool more = u + 1 < nsub;
-    const bool load = kk + 2 < nslice;
+    const bool more = STEADY || u + 1 < nsub;
+    const bool load = STEADY || kk + 2 < nslice;
     if (H == 1) {
       // in flight behind slice kk + 1: the A part of slice kk + 2
       if (more) {
@@ -585,7 +589,8 @@ void gemm256_kernel(GemmArgs g) {
     for (int t = 0; t < 16; ++t) {
       const int i = t >> 2, j = t & 3;
       acc[i][j] = mfma_32x32x64(cur.b[j], cur.a[i], acc[i][j]);
-      if ((t & 1) == 1 && load) issue(H * kG2ALoads + (t >> 1), kk + 2, lslot);
+      if ((t & 1) == 1 && load)
+        issue(H * kG2ALoads + (t >> 1), kk + 2, lslot, std::integral_constant<bool, STEADY>{});
       if ((t & 1) == 0 && more) {
         const int v = t >> 2;
         if ((t & 2) == 0) nxt.a[v] = g2_op(sta + a_off + 32 * v * kG2Pitch, r0, r1);
@@ -595,11 +600,19 @@ void gemm256_kernel(GemmArgs g) {
     if (H == 1) sa = wrap(sa + 2);
   };
   const int nfull = nsub >> 1;
-  for (int kk = 0; kk < nfull; ++kk) {
-    sub(kk, std::integral_constant<int, 0>{}, o0, o1);
-    sub(kk, std::integral_constant<int, 1>{}, o1, o0);
+  const int nsteady = max(0, nslice - 3);
+  using H0 = std::integral_constant<int, 0>;
+  using H1 = std::integral_constant<int, 1>;
+  int kk = 0;
+  for (; kk < nsteady; ++kk) {
+    sub(kk, H0{}, std::true_type{}, o0, o1);
+    sub(kk, H1{}, std::true_type{}, o1, o0);
   }
-  if (half_tail) sub(nfull, std::integral_constant<int, 0>{}, o0, o1);
+  for (; kk < nfull; ++kk) {
+    sub(kk, H0{}, std::false_type{}, o0, o1);
+    sub(kk, H1{}, std::false_type{}, o1, o0);
+  }
+  if (half_tail) sub(nfull, H0{}, std::false_type{}, o0, o1);
 
   // epilogue: C[m][n] = bf16(acc * a_scale * b_scale), or with row-wise
   // scales bf16((acc * row_scale[m]) * col_scale[n]).  The bf16 tile goes
