@@ -246,8 +246,17 @@ def test_traffic_profile_is_well_formed() -> None:
     k = data["c3_wan_self"]["attn_fwd_kernel"]
     assert k["hbm_bytes_per_launch"] == k["hbm_read_bytes_per_launch"] + \
         k["hbm_write_bytes_per_launch"]
-    # the kernel writes the bf16 output once: 40 x 75600 x 128 x 2 bytes
-    assert abs(k["hbm_write_bytes_per_launch"] - 774_144_000) < 1e6
+    # the balanced launch (288 of 296 query blocks per head unsplit, the
+    # rest split 4 ways): the kernel writes the bf16 output of the unsplit
+    # rows once and the fp32 partials (O, m, l) of the split rows; the merge
+    # reads those partials and writes the bf16 output of the split rows
+    main_rows, tail_rows = 288 * 256, 75600 - 288 * 256
+    out_main = 40 * main_rows * 128 * 2
+    partials = 4 * 40 * tail_rows * (128 + 2) * 4
+    assert abs(k["hbm_write_bytes_per_launch"] - (out_main + partials)) < 1e6
+    c = data["c3_wan_self"]["attn_combine_kernel"]
+    assert abs(c["hbm_write_bytes_per_launch"] - 40 * tail_rows * 128 * 2) < 1e6
+    assert abs(c["hbm_read_bytes_per_launch"] - partials) < 0.05 * partials
 
 
 def test_scaled_mm_op_contract() -> None:

@@ -292,11 +292,14 @@ RING_LINES = (
     "const uint8_t* sta = smem + (H == 0 ? sa : wrap(sa + 2)) * kG2Half;",
     "const uint8_t* stb = smem + (H == 0 ? wrap(sa + 1) : wrap(sa + 3)) * kG2Half;",
     "const int lslot = H == 0 ? wrap(sa + 4) : sa;",
-    "if ((t & 1) == 1 && load) issue(H * kG2ALoads + (t >> 1), kk + 2, lslot);",
-    "const bool load = kk + 2 < nslice;",
+    "if ((t & 1) == 1 && load)",
+    "issue(H * kG2ALoads + (t >> 1), kk + 2, lslot, std::integral_constant<bool, STEADY>{});",
+    "const bool more = STEADY || u + 1 < nsub;",
+    "const bool load = STEADY || kk + 2 < nslice;",
+    "const int nsteady = max(0, nslice - 3);",
     "if (load) g2_wait_vmem<kG2ALoads>();",
-    "for (int n = 0; n < kG2Loads; ++n) issue(n, 0, n < kG2ALoads ? 0 : 1);",
-    "for (int n = 0; n < kG2Loads; ++n) issue(n, 1, n < kG2ALoads ? 2 : 3);",
+    "for (int n = 0; n < kG2Loads; ++n) issue(n, 0, n < kG2ALoads ? 0 : 1, std::false_type{});",
+    "for (int n = 0; n < kG2Loads; ++n) issue(n, 1, n < kG2ALoads ? 2 : 3, std::false_type{});",
     "if (H == 1) sa = wrap(sa + 2);",
     "constexpr int kG2Slots = 5;",
 )
@@ -343,6 +346,8 @@ def _ring_schedule(nsub: int, slots: int = 5) -> None:
     steps = [(kk, h) for kk in range(nfull) for h in (0, 1)] + ([(nfull, 0)] if half else [])
     for kk, h in steps:
         more, load = 2 * kk + h + 1 < nsub, kk + 2 < nslice
+        if kk < max(0, nslice - 3):    # a steady sub-step: both taken as true,
+            assert more and load and kk + 2 < nslice - 1   # the slice loaded full
         if h == 1:
             if more:
                 wait(1 if load else 0)
