@@ -405,7 +405,11 @@ __device__ __forceinline__ i32x8 kn_operand(uint32_t base) {
   return i32x8{r0.x, r0.y, r1.x, r1.y, r2.x, r2.y, r3.x, r3.y};
 }
 
-template <bool KN>
+// Epilogue modes of gemm256_kernel, fixed at compile time: per-tensor
+// scales; per-tensor scales and a bias; row-wise scales (bias optional).
+constexpr int kEpiPlain = 0, kEpiBias = 1, kEpiRows = 2;
+
+template <bool KN, int EPI>
 __global__ __launch_bounds__(kG2Threads) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void gemm256_kernel(GemmArgs g) {
   __shared__ __attribute__((aligned(1024))) uint8_t smem[kG2Slots * kG2Half];
@@ -623,10 +627,15 @@ void gemm256_kernel(GemmArgs g) {
   // per lane, 16 lanes per row (16 distinct granules), so each row leaves
   // as one 256-byte run instead of sixteen 16-byte pieces.  The stores are
   // non-temporal: C is not read again, and the L2 keeps the operand rows
-  // that other tiles still need.
-  const float scale = g.row_scale ? 1.0f
+  // that other tiles still need.  The mode (EPI) is a template parameter
+  // and a tile wholly inside C skips every bound check, so the staging is
+  // straight-line code and the store loop reads eight rows from LDS before
+  // it stores them (a read, its wait and its store per row took ~4x as
+  // long).
+  constexpr bool ROWS = EPI == kEpiRows;
+  const float scale = ROWS ? 1.0f
                     : (g.a_dev ? *g.a_dev : g.a_scale) * (g.b_dev ? *g.b_dev : g.b_scale);
-  const bool has_bias = g.bias != nullptr;
+  const bool has_bias = EPI == kEpiBias || (ROWS && g.bias != nullptr);
   constexpr int kCPitch = 128 * 2;                  // bytes per row of a wave's C part
   static_assert(4 * 128 * kCPitch <= kG2Slots * kG2Half, "C staging fits the slots");
   uint8_t* ct = smem + wave * 128 * kCPitch;
@@ -634,7 +643,7 @@ void gemm256_kernel(GemmArgs g) {
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int64_t m = m0 + wm * 128 + 32 * i + lq;
-    sm[i] = g.row_scale && m < g.M ? g.row_scale[m] : 1.0f;
+    sm[i] = ROWS && m < g.M ? g.row_scale[m] : 1.0f;
   }
   __syncthreads();   // every wave has finished reading the operand slots
   // (no global store precedes these loads of bias and column scales)
@@ -643,20 +652,23 @@ void gemm256_kernel(GemmArgs g) {
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       const int64_t n = n0 + wn * 128 + 32 * j + 8 * q + 4 * lg;
-      if (n >= g.N) continue;   // columns past N are never stored
+      // columns past N are never stored; with a bias or column scales
+      // their (out-of-range) values are not read either
+      if (EPI != kEpiPlain && n >= g.N) continue;
       const uint2 bb = has_bias ? bias4(g, n) : make_uint2(0u, 0u);
-      const float4 sn = g.row_scale ? *reinterpret_cast<const float4*>(g.col_scale + n)
-                                    : make_float4(0.f, 0.f, 0.f, 0.f);
+      const float4 sn = ROWS ? *reinterpret_cast<const float4*>(g.col_scale + n)
+                             : make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         // rows past M are written here but never stored
         const f32x16& v = acc[i][j];
         float o[4];
-        if (g.row_scale)
+        if constexpr (ROWS)
           epi4_rows(has_bias, bb, sm[i], sn, v[4 * q + 0], v[4 * q + 1], v[4 * q + 2],
                     v[4 * q + 3], o);
         else
-          epi4(has_bias, bb, scale, v[4 * q + 0], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3], o);
+          epi4(EPI == kEpiBias, bb, scale, v[4 * q + 0], v[4 * q + 1], v[4 * q + 2],
+               v[4 * q + 3], o);
         uint2 pk;
         pk.x = g2_pack_bf16(o[0], o[1]);
         pk.y = g2_pack_bf16(o[2], o[3]);
@@ -671,26 +683,54 @@ void gemm256_kernel(GemmArgs g) {
   const int c = lane & 15;
   const bool odd = (lane >> 4) & 1;   // the parity of every row this lane reads
   const int64_t n = n0 + wn * 128 + 8 * c;
+  // row r of the wave's part: logical slots 2c, 2c+1 sit in granule
+  // c ^ ((r & 31) >> 1), swapped when r is odd
+  auto stage_row = [&](int r) __attribute__((always_inline)) {
+    const int cg = (c ^ ((r & 31) >> 1));
+    const uint4 t = *reinterpret_cast<const uint4*>(ct + r * kCPitch + cg * 16);
+    return odd ? u32x4{t.z, t.w, t.x, t.y} : u32x4{t.x, t.y, t.z, t.w};
+  };
+  uint16_t* const cw = g.c + (m0 + wm * 128) * g.ldc + n;
+  if (c16 && m0 + 256 <= g.M && n0 + 256 <= g.N) {
+    // a tile inside C: eight rows read, then eight whole-row stores
+#pragma unroll
+    for (int k8 = 0; k8 < 32; k8 += 8) {
+      u32x4 t[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) t[u] = stage_row(4 * (k8 + u) + (lane >> 4));
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+        __builtin_nontemporal_store(
+            t[u], reinterpret_cast<u32x4*>(cw + (int64_t)(4 * (k8 + u) + (lane >> 4)) * g.ldc));
+    }
+    return;
+  }
 #pragma unroll 4
   for (int k = 0; k < 32; ++k) {
     const int r = 4 * k + (lane >> 4);
     const int64_t m = m0 + wm * 128 + r;
-    // logical slots 2c, 2c+1 sit in granule c ^ ((r & 31) >> 1), swapped when r is odd
-    const int cg = (c ^ ((r & 31) >> 1));
-    const uint4 t = *reinterpret_cast<const uint4*>(ct + r * kCPitch + cg * 16);
-    const uint32_t lo0 = odd ? t.z : t.x, lo1 = odd ? t.w : t.y;
-    const uint32_t hi0 = odd ? t.x : t.z, hi1 = odd ? t.y : t.w;
+    const u32x4 t = stage_row(r);
     if (m >= g.M || n >= g.N) continue;
     uint16_t* dst = g.c + m * g.ldc + n;
     if (c16 && n + 8 <= g.N) {
-      __builtin_nontemporal_store(u32x4{lo0, lo1, hi0, hi1}, reinterpret_cast<u32x4*>(dst));
+      __builtin_nontemporal_store(t, reinterpret_cast<u32x4*>(dst));
     } else {
       // n + 4 <= N (N % 4 == 0)
-      __builtin_nontemporal_store(u32x2{lo0, lo1}, reinterpret_cast<u32x2*>(dst));
+      __builtin_nontemporal_store(u32x2{t.x, t.y}, reinterpret_cast<u32x2*>(dst));
       if (n + 8 <= g.N)
-        __builtin_nontemporal_store(u32x2{hi0, hi1}, reinterpret_cast<u32x2*>(dst + 4));
+        __builtin_nontemporal_store(u32x2{t.z, t.w}, reinterpret_cast<u32x2*>(dst + 4));
     }
   }
+}
+
+template <bool KN>
+void launch_g256(const GemmArgs& g, dim3 grid, hipStream_t st) {
+  if (g.row_scale)
+    hipLaunchKernelGGL((gemm256_kernel<KN, kEpiRows>), grid, dim3(kG2Threads), 0, st, g);
+  else if (g.bias)
+    hipLaunchKernelGGL((gemm256_kernel<KN, kEpiBias>), grid, dim3(kG2Threads), 0, st, g);
+  else
+    hipLaunchKernelGGL((gemm256_kernel<KN, kEpiPlain>), grid, dim3(kG2Threads), 0, st, g);
 }
 
 int launch_gemm256(GemmArgs g, int64_t batch, hipStream_t st) {
@@ -703,9 +743,9 @@ int launch_gemm256(GemmArgs g, int64_t batch, hipStream_t st) {
   }
   const dim3 grid((unsigned)nwork, (unsigned)batch);
   if (g.b_kn)
-    hipLaunchKernelGGL(gemm256_kernel<true>, grid, dim3(kG2Threads), 0, st, g);
+    launch_g256<true>(g, grid, st);
   else
-    hipLaunchKernelGGL(gemm256_kernel<false>, grid, dim3(kG2Threads), 0, st, g);
+    launch_g256<false>(g, grid, st);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) {
     rp_set_error("gemm: launch failed: %s", hipGetErrorString(e));
