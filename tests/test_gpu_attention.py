@@ -393,6 +393,34 @@ def test_balanced_launch_vs_oracle(gpu: torch.device, case: tuple) -> None:
     _check(got, ref1, f"{name} tail vs one range", rel_tol=5e-2)
 
 
+@pytest.mark.parametrize("shape", [(1, 4, 1000, 1000, 128, True), (1, 2, 3000, 512, 128, False),
+                                   (1, 32, 2048, 4224, 128, False), (1, 8, 2048, 2048, 64, False),
+                                   (2, 3, 700, 900, 256, True)],
+                         ids=["causal", "multi_block", "whole_rounds", "under_a_round",
+                              "d256_causal"])
+def test_balanced_launch_without_a_split_is_the_plain_launch(gpu: torch.device,
+                                                              shape: tuple) -> None:
+    """Where the balanced plan splits nothing (a mask, a multi-block launch,
+    rounds already full), kv_splits=0 runs exactly the one-range launch."""
+    import ctypes
+
+    from repercep_runtime_amd import _capi
+
+    B, H, Sq, Skv, D, causal = shape
+    cus = torch.cuda.get_device_properties(gpu).multi_processor_count
+    m, s = ctypes.c_int(), ctypes.c_int()
+    assert _capi.lib().rp_fp8_attn_balanced_plan(B, H, Sq, Skv, D, int(causal), cus,
+                                                 ctypes.byref(m), ctypes.byref(s)) == 0
+    assert s.value == 1
+    g = torch.Generator(device=gpu).manual_seed(Sq + Skv)
+    q = torch.randn(B, H, Sq, D, generator=g, device=gpu).to(torch.bfloat16)
+    k = torch.randn(B, H, Skv, D, generator=g, device=gpu).to(torch.bfloat16)
+    v = torch.randn(B, H, Skv, D, generator=g, device=gpu).to(torch.bfloat16)
+    one = ops.fp8_flash_attention(q, k, v, causal=causal, kv_splits=1)
+    bal = ops.fp8_flash_attention(q, k, v, causal=causal, kv_splits=0)
+    assert torch.equal(one, bal)
+
+
 def test_autotune_records_and_reuses_a_split_count(gpu: torch.device, tmp_path,
                                                    monkeypatch: pytest.MonkeyPatch) -> None:
     """Cache miss -> timed search over the candidates, winner recorded under

@@ -35,3 +35,28 @@ def test_captured_attention_replays_match_eager(gpu: torch.device, cfg, dtype) -
         want = ops.fp8_flash_attention(sq.clone(), sk.clone(), sv.clone(), kv_splits=1, **kw)
         _ = torch.randn(1024, device=gpu).sum().item()      # unrelated eager work + sync
         assert torch.equal(sout, want), f"replay {rep} differs from eager"
+
+
+def test_captured_balanced_launch_replays_match_eager(gpu: torch.device) -> None:
+    """The balanced launch (kv_splits=0) of a shape whose plan splits the last
+    round's blocks on 256 CUs: one mixed attention launch and the merge,
+    with its workspace from the capture's pool; every replay equals an eager
+    call bit for bit."""
+    q, k, v = (torch.randn(1, 8, n, 128, device=gpu).to(torch.bfloat16)
+               for n in (8860, 8192, 8192))
+    sq, sk, sv = q.clone(), k.clone(), v.clone()
+    ops.fp8_flash_attention(sq, sk, sv, kv_splits=0)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        sout = ops.fp8_flash_attention(sq, sk, sv, kv_splits=0)
+    g = torch.Generator(device=gpu).manual_seed(11)
+    for rep in range(3):
+        if rep:
+            for src in (sq, sk, sv):
+                src.copy_(torch.randn(src.shape, generator=g, device=gpu).to(torch.bfloat16))
+        graph.replay()
+        torch.cuda.synchronize()
+        want = ops.fp8_flash_attention(sq.clone(), sk.clone(), sv.clone(), kv_splits=0)
+        _ = torch.randn(1024, device=gpu).sum().item()
+        assert torch.equal(sout, want), f"replay {rep} differs from eager"
