@@ -53,6 +53,9 @@
 // * Grid: one workgroup per (head, query block), remapped so that the
 //   workgroups resident on one XCD (dispatch is round-robin over the 8
 //   XCDs) work on the same head and share its K/V through that XCD's L2.
+//   The balanced launch (tail_plan) adds key-split workgroups for the query
+//   blocks past the last whole round, dispatched last on every XCD; short
+//   key ranges run several query blocks per workgroup (multi_block_plan).
 
 #include "rp_common.h"
 

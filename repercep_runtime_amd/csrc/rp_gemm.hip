@@ -16,8 +16,9 @@
 //
 // * gemm256_kernel (K a multiple of 64, the production shapes): 256 x 256
 //   block tiles on v_mfma_f32_32x32x64_f8f6f4, four waves of 128 x 128 with
-//   their accumulators in AGPRs, operands streamed into two LDS stages of
-//   128-byte K slices by direct-to-LDS loads one slice ahead.
+//   their accumulators in AGPRs, operands streamed by direct-to-LDS loads
+//   through a ring of five 32 KiB slots (the A and B^T halves of 128-byte K
+//   slices), each slice loaded two slices ahead of its use.
 // * gemm_kernel (any K multiple of 16, any (K, N) B): 256 x 128 block tiles
 //   on v_mfma_f32_16x16x128_f8f6f4, operands staged through VGPRs into a
 //   double-buffered, XOR-swizzled LDS tile, K tail zero-filled; a (K, N) B
@@ -304,7 +305,8 @@ void gemm_kernel(GemmArgs g) {
 // the B^T part of one slice: while slice k is multiplied, slice k+1 lands and
 // slice k+2 loads, its A part during the first half of slice k and its B^T
 // part during the second, so the loads leave at an even rate (issuing a
-// whole slice at once measured 4% slower).  One wait and barrier per slice.
+// whole slice at once measured 4% slower).  One wait and barrier per slice;
+// all but the last three slices run a branch-free copy of the sub-step.
 // Each slice is two MFMA depths (sub-slices of 64 bytes); operands are
 // double-buffered in registers a sub-slice ahead.  LDS rows are unpadded;
 // the eight 16-byte granules of a row are XOR-swizzled by (row >> 1) & 7, so
