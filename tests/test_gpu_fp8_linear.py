@@ -18,7 +18,10 @@ pytestmark = pytest.mark.gpu
 
 
 @pytest.mark.parametrize("shape,bias", [((3, 77, 256), True), ((1000, 512), False),
-                                        ((2, 1, 128), True)])
+                                        ((2, 1, 128), True),
+                                        # row tiles wholly inside the output: the
+                                        # bias epilogue's unchecked store path
+                                        ((2, 300, 256), True)])
 def test_fp8_linear_matches_oracle(gpu: torch.device, shape: tuple[int, ...], bias: bool) -> None:
     K, N = shape[-1], 384
     g = torch.Generator().manual_seed(sum(shape))

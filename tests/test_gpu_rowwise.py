@@ -83,7 +83,9 @@ def test_transpose16_exact(gpu: torch.device) -> None:
 
 
 @pytest.mark.parametrize("zmnk", [(3, 128, 256, 128), (2, 300, 200, 64), (1, 64, 100, 48),
-                                  (4, 256, 64, 512)])
+                                  (4, 256, 64, 512),
+                                  # tiles wholly inside C: the unchecked store path
+                                  (1, 512, 512, 256), (2, 256, 272, 128)])
 def test_gemm_rowwise_one_rounding_of_exact(gpu: torch.device, zmnk: tuple) -> None:
     """Every output is the bf16 rounding of a value within
     2^-14 * sum|a||b| * s_m * s_n (the MFMA's sum) plus the two fp32 roundings
