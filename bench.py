@@ -151,7 +151,7 @@ def bench_attention(args, cfg) -> dict:
     torch.cuda.set_device(dev)
     log(f"[bench] generating {cfg.name} inputs on {dev}")
     # configs with QK RMSNorm take pre-norm Q/K: the norm runs fused into
-    # their quantizers inside the step (rmsnorm_scale_quantize)
+    # their quantizers inside the step (rmsnorm_scale_quantize_qkv)
     fused_norm = cfg.rmsnorm_qk
     gran = args.granularity
     q, k, v = attn_inputs(cfg, device=dev, normalize=not fused_norm)
@@ -174,9 +174,7 @@ def bench_attention(args, cfg) -> dict:
         if ev is not None:
             ev[0].record(st)
         if fused_norm:
-            qs, q8 = ops.rmsnorm_scale_quantize(q, granularity=gran)
-            ks, k8 = ops.rmsnorm_scale_quantize(k, granularity=gran)
-            vs, vt8 = ops.scale_quantize(v, gran, "bhds")
+            qs, q8, ks, k8, vs, vt8 = ops.rmsnorm_scale_quantize_qkv(q, k, v, granularity=gran)
         else:   # what fp8_flash_attention runs: one library call for Q, K, V
             qs, q8, ks, k8, vs, vt8 = ops.scale_quantize_qkv(q, k, v, gran)
         if ev is not None:
@@ -286,8 +284,8 @@ def bench_attention(args, cfg) -> dict:
             "frac": round(q_gbps / HBM_PEAK_GBPS, 4),
             "ms": round(quant_ms, 4),
             "bytes": qbytes,
-            "note": ("Q, K: RMSNorm fused into amax pass + finalize + apply; V: amax pass + "
-                     "finalize + apply (transposed); 5 B/element" if fused_norm else
+            "note": ("Q, K with RMSNorm fused, V plain: one multi-tensor amax pass + "
+                     "finalize + apply (V transposed); 5 B/element" if fused_norm else
                      "Q, K, V: one multi-tensor amax pass + finalize + apply (V "
                      "transposed), 5 B/element"),
         },

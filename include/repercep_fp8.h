@@ -295,6 +295,33 @@ int rp_fp8_rmsnorm_scale_quantize(const void* x, int64_t B, int64_t H, int64_t S
                                   uint8_t* codes, void* workspace, size_t workspace_bytes,
                                   void* stream);
 
+/* One attention call's three quantizers with the QK-norm prologue: Q and K
+ * as rp_fp8_rmsnorm_scale_quantize (each with its own weight, NULL for
+ * none, and its own cos/sin tables, Q's [Sq, D] and K's [Skv, D]; one
+ * rope_mode for both), V as rp_fp8_scale_quantize into transposed codes
+ * (RP_LAYOUT_BHDS, row stride ldv >= Skv, ldv % 128 == 0).  The same
+ * scales and codes as those three calls, bit for bit, from three kernel
+ * launches instead of nine.  Replaces, like the single-tensor call, the
+ * processor's norm_q/norm_k ahead of the FP8 path (reference docs/
+ * walkthroughs/02-architecture.md:114-123) together with the path's own
+ * quantizer of V (kernels/triton_kernels/fp8_flash_attn.py:526-528).
+ * bf16 inputs with a unit stride on D, D in {64, 128}; dequant_out holds
+ * Q's, K's, then V's scales (ngroups each: B*H per head, 1 per tensor).
+ * The workspace (256-byte aligned) must not be shared by calls that may
+ * overlap. */
+size_t rp_fp8_rmsnorm_quant_qkv_workspace_bytes(int64_t B, int64_t H, int64_t Sq, int64_t Skv,
+                                                int64_t D, int granularity);
+int rp_fp8_rmsnorm_scale_quantize_qkv(const void* q, const void* k, const void* v, int64_t B,
+                                      int64_t H, int64_t Sq, int64_t Skv, int64_t D, int64_t qsb,
+                                      int64_t qsh, int64_t qss, int64_t ksb, int64_t ksh,
+                                      int64_t kss, int64_t vsb, int64_t vsh, int64_t vss,
+                                      const void* q_weight, const void* k_weight, float eps,
+                                      const float* q_cos, const float* q_sin, const float* k_cos,
+                                      const float* k_sin, int rope_mode, int granularity,
+                                      float* dequant_out, uint8_t* q8, uint8_t* k8, uint8_t* vt8,
+                                      int64_t ldv, void* workspace, size_t workspace_bytes,
+                                      void* stream);
+
 /* --------------------------------------------------------------- GEMM
  * C (M, N) bf16 = bf16( fp32(A8 . B8) * (a_scale * b_scale) ).
  * Replaces fp8_gemm_launch, kernels/hip/fp8_attn/fp8_gemm.hip:162-179

@@ -46,7 +46,8 @@ EXPORTS = (
     "rp_fp8_attn_fwd_split", "rp_fp8_attn_balanced_plan",
     "rp_fp8_attn_balanced_workspace_bytes", "rp_fp8_attn_fwd_balanced",
     "rp_fp8_rmsnorm_quant_workspace_bytes",
-    "rp_fp8_rmsnorm_scale_quantize", "rp_fp8_gemm", "rp_fp8_linear", "rp_fp8_transpose",
+    "rp_fp8_rmsnorm_scale_quantize", "rp_fp8_rmsnorm_quant_qkv_workspace_bytes",
+    "rp_fp8_rmsnorm_scale_quantize_qkv", "rp_fp8_gemm", "rp_fp8_linear", "rp_fp8_transpose",
     "rp_fp8_gemm_rowwise", "rp_fp8_rowwise_quantize", "rp_transpose16",
     "rp_fp8_softmax_rowwise_quantize",
     "rp_selftest_e4m3", "rp_selftest_scale",
@@ -117,6 +118,12 @@ def _declare(L: ctypes.CDLL) -> None:
     L.rp_fp8_rmsnorm_scale_quantize.argtypes = [_vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
                                                 _vp, _f32, _vp, _vp, _int, _int, _vp, _vp, _vp,
                                                 _sz, _vp]
+    L.rp_fp8_rmsnorm_quant_qkv_workspace_bytes.restype = _sz
+    L.rp_fp8_rmsnorm_quant_qkv_workspace_bytes.argtypes = [_i64] * 5 + [_int]
+    L.rp_fp8_rmsnorm_scale_quantize_qkv.restype = _int
+    L.rp_fp8_rmsnorm_scale_quantize_qkv.argtypes = ([_vp] * 3 + [_i64] * 14 + [_vp, _vp, _f32]
+                                                    + [_vp] * 4 + [_int, _int] + [_vp] * 4
+                                                    + [_i64, _vp, _sz, _vp])
     L.rp_fp8_gemm.restype = _int
     L.rp_fp8_gemm.argtypes = [_vp, _vp, _int, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _f32,
                               _f32, _vp, _vp, _vp]

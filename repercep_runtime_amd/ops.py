@@ -234,6 +234,29 @@ def scale_quantize_qkv(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
 _ROPE = {None: C.RP_ROPE_NONE, "half": C.RP_ROPE_HALF, "interleaved": C.RP_ROPE_INTERLEAVED}
 
 
+def _norm_operands(x: torch.Tensor, weight: torch.Tensor | None,
+                   rope: tuple[torch.Tensor, torch.Tensor] | None
+                   ) -> tuple[int | None, int | None, int | None]:
+    """Device pointers of a prologue's weight and cos/sin tables (None when
+    absent), checked against x's (B, H, S, D) shape."""
+    _, _, S, D = x.shape
+    w_ptr = cos_ptr = sin_ptr = None
+    if weight is not None:
+        _check_bf16("weight", weight)
+        _on_device_of(x, weight=weight)
+        if weight.shape != (D,) or not weight.is_contiguous():
+            raise ValueError(f"weight must be a contiguous ({D},) bf16 vector")
+        w_ptr = weight.data_ptr()
+    if rope is not None:
+        cos, sin = rope
+        _on_device_of(x, cos=cos, sin=sin)
+        for name, t in (("cos", cos), ("sin", sin)):
+            if t.dtype != torch.float32 or t.shape != (S, D) or not t.is_contiguous():
+                raise ValueError(f"{name} must be a contiguous float32 ({S}, {D}) table")
+        cos_ptr, sin_ptr = cos.data_ptr(), sin.data_ptr()
+    return w_ptr, cos_ptr, sin_ptr
+
+
 def rmsnorm_scale_quantize(x: torch.Tensor, weight: torch.Tensor | None = None,
                            eps: float = 1e-6,
                            rope: tuple[torch.Tensor, torch.Tensor] | None = None,
@@ -253,22 +276,8 @@ def rmsnorm_scale_quantize(x: torch.Tensor, weight: torch.Tensor | None = None,
     if x.dim() != 4:
         raise ValueError("x must be (B, H, S, D)")
     B, H, S, D, sb, sh, ss = _bhsd_view(x)
-    w_ptr = None
-    if weight is not None:
-        _check_bf16("weight", weight)
-        _on_device_of(x, weight=weight)
-        if weight.shape != (D,) or not weight.is_contiguous():
-            raise ValueError(f"weight must be a contiguous ({D},) bf16 vector")
-        w_ptr = weight.data_ptr()
+    w_ptr, cos_ptr, sin_ptr = _norm_operands(x, weight, rope)
     mode = _ROPE[rope_layout if rope is not None else None]
-    cos_ptr = sin_ptr = None
-    if rope is not None:
-        cos, sin = rope
-        _on_device_of(x, cos=cos, sin=sin)
-        for name, t in (("cos", cos), ("sin", sin)):
-            if t.dtype != torch.float32 or t.shape != (S, D) or not t.is_contiguous():
-                raise ValueError(f"{name} must be a contiguous float32 ({S}, {D}) table")
-        cos_ptr, sin_ptr = cos.data_ptr(), sin.data_ptr()
     g = _GRAN[granularity]
     dq = torch.empty(B * H if granularity == "bh" else 1, dtype=torch.float32, device=x.device)
     codes = torch.empty((B, H, S, D), dtype=torch.uint8, device=x.device)
@@ -279,6 +288,59 @@ def rmsnorm_scale_quantize(x: torch.Tensor, weight: torch.Tensor | None = None,
         dq.data_ptr(), codes.data_ptr(), ws.data_ptr(), ws.numel(), _stream(x)),
         "rp_fp8_rmsnorm_scale_quantize")
     return dq, codes.view(torch.float8_e4m3fn)
+
+
+def rmsnorm_scale_quantize_qkv(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *,
+                               norm_q_weight: torch.Tensor | None = None,
+                               norm_k_weight: torch.Tensor | None = None, eps: float = 1e-6,
+                               rope_q: tuple[torch.Tensor, torch.Tensor] | None = None,
+                               rope_k: tuple[torch.Tensor, torch.Tensor] | None = None,
+                               rope_layout: Literal["half", "interleaved"] = "half",
+                               granularity: Granularity = "bh"
+                               ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor,
+                                          torch.Tensor, torch.Tensor]:
+    """(q_scale, q8, k_scale, k8, v_scale, vt8) of one attention call with the
+    QK-norm prologue, from one library call (rp_fp8_rmsnorm_scale_quantize_qkv:
+    three kernel launches instead of nine) into one device allocation: the
+    same scales and codes as ``rmsnorm_scale_quantize`` of Q and of K and
+    ``scale_quantize(v, granularity, "bhds")``.  (B, H, S, D) bf16 inputs
+    with a unit stride on D; K and V share their shape; rotary tables for
+    both Q and K or for neither."""
+    for name, t in (("q", q), ("k", k), ("v", v)):
+        _check_bf16(name, t)
+    B, H, Sq, D, qsb, qsh, qss = _bhsd_view(q)
+    _, _, Skv, _, ksb, ksh, kss = _bhsd_view(k)
+    _, _, _, _, vsb, vsh, vss = _bhsd_view(v)
+    if k.shape[:2] != q.shape[:2] or k.shape[3] != D or v.shape != k.shape:
+        raise ValueError(f"k and v must share one (B, H, Skv, D) shape with q's B, H and D "
+                         f"(q {tuple(q.shape)}, k {tuple(k.shape)}, v {tuple(v.shape)})")
+    if (rope_q is None) != (rope_k is None):
+        raise ValueError("rotary tables must be given for both q and k or for neither")
+    _on_device_of(q, k=k, v=v)
+    qw, qc, qsn = _norm_operands(q, norm_q_weight, rope_q)
+    kw, kc, ksn = _norm_operands(k, norm_k_weight, rope_k)
+    mode = _ROPE[rope_layout if rope_q is not None else None]
+    g = _GRAN[granularity]
+    G = B * H if granularity == "bh" else 1
+    ldv = _round_up(Skv, V_PAD)
+    nq, nk, nv = B * H * Sq * D, B * H * Skv * D, B * H * D * ldv
+    ws = int(C.lib().rp_fp8_rmsnorm_quant_qkv_workspace_bytes(B, H, Sq, Skv, D, g))
+    o_k = _align(nq)
+    o_v = o_k + _align(nk)
+    o_s = o_v + _align(nv)
+    o_w = o_s + _align(3 * G * 4)
+    arena = torch.empty(o_w + max(ws, 16), dtype=torch.uint8, device=q.device)
+    base = arena.data_ptr()
+    C.check(C.lib().rp_fp8_rmsnorm_scale_quantize_qkv(
+        q.data_ptr(), k.data_ptr(), v.data_ptr(), B, H, Sq, Skv, D, qsb, qsh, qss, ksb, ksh, kss,
+        vsb, vsh, vss, qw, kw, float(eps), qc, qsn, kc, ksn, mode, g, base + o_s, base,
+        base + o_k, base + o_v, ldv, base + o_w, ws, _stream(q)),
+        "rp_fp8_rmsnorm_scale_quantize_qkv")
+    dq = arena[o_s:o_s + 3 * G * 4].view(torch.float32)
+    q8 = arena[:nq].view(B, H, Sq, D).view(torch.float8_e4m3fn)
+    k8 = arena[o_k:o_k + nk].view(B, H, Skv, D).view(torch.float8_e4m3fn)
+    vt8 = arena[o_v:o_v + nv].view(B, H, D, ldv).view(torch.float8_e4m3fn)
+    return dq[:G], q8, dq[G:2 * G], k8, dq[2 * G:], vt8
 
 
 def fp8_flash_attention_qknorm(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *,
@@ -292,8 +354,8 @@ def fp8_flash_attention_qknorm(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor
                                out_dtype: torch.dtype | None = None,
                                kv_splits: int | None = None) -> torch.Tensor:
     """``fp8_flash_attention`` on pre-norm Q and K: the attention processor's
-    QK-RMSNorm (and rotary embedding) runs fused into Q's and K's quantizers
-    (``rmsnorm_scale_quantize``); V is quantized as usual.  Same result as
+    QK-RMSNorm (and rotary embedding) runs fused into Q's and K's quantizers,
+    and V's quantizer shares their launches (``rmsnorm_scale_quantize_qkv``).  Same result as
     normalising (and rotating) Q and K in torch first, up to the summation
     order of the RMSNorm's mean (see rp_prologue.hip)."""
     for name, t in (("q", q), ("k", k), ("v", v)):
@@ -308,9 +370,14 @@ def fp8_flash_attention_qknorm(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor
         raise ValueError(f"head_dim {D} not in compiled tile shapes {sorted(SUPPORTED_HEAD_DIMS)}")
     if scale is None:
         scale = 1.0 / math.sqrt(D)
-    qs, q8 = rmsnorm_scale_quantize(q, norm_q_weight, eps, rope_q, rope_layout, granularity)
-    ks, k8 = rmsnorm_scale_quantize(k, norm_k_weight, eps, rope_k, rope_layout, granularity)
-    vs, vt8 = scale_quantize(v, granularity, "bhds")
+    if (rope_q is None) == (rope_k is None):
+        qs, q8, ks, k8, vs, vt8 = rmsnorm_scale_quantize_qkv(
+            q, k, v, norm_q_weight=norm_q_weight, norm_k_weight=norm_k_weight, eps=eps,
+            rope_q=rope_q, rope_k=rope_k, rope_layout=rope_layout, granularity=granularity)
+    else:   # rotary tables for one of Q and K only
+        qs, q8 = rmsnorm_scale_quantize(q, norm_q_weight, eps, rope_q, rope_layout, granularity)
+        ks, k8 = rmsnorm_scale_quantize(k, norm_k_weight, eps, rope_k, rope_layout, granularity)
+        vs, vt8 = scale_quantize(v, granularity, "bhds")
     Skv = k.shape[2]
     if kv_splits is None:
         kv_splits = tuned_kv_splits(B, H, Sq, Skv, D, causal)

@@ -192,6 +192,59 @@ def test_rmsnorm_workspace_sizing() -> None:
     assert L.rp_fp8_rmsnorm_quant_workspace_bytes(1, 2, 64, 96, 0) == 0
 
 
+def _norm_qkv(L, **kw) -> int:
+    B, H, Sq, Skv, D = 1, 2, 64, 96, 128
+    a = dict(q=FAKE, k=FAKE, v=FAKE, B=B, H=H, Sq=Sq, Skv=Skv, D=D,
+             qsb=H * Sq * D, qsh=Sq * D, qss=D, ksb=H * Skv * D, ksh=Skv * D, kss=D,
+             vsb=H * Skv * D, vsh=Skv * D, vss=D, qw=None, kw=None, eps=1e-6,
+             qc=None, qs=None, kc=None, ks=None, rope=0, gran=0, dq=FAKE, q8=FAKE, k8=FAKE,
+             vt8=FAKE, ldv=128, ws=FAKE, nbytes=1 << 20, stream=None)
+    a.update(kw)
+    return L.rp_fp8_rmsnorm_scale_quantize_qkv(*a.values())
+
+
+@pytest.mark.parametrize("kw,status,msg", [
+    (dict(v=None), 1, "null pointer"),
+    (dict(vt8=None), 1, "null pointer"),
+    (dict(k8=None), 1, "null pointer"),
+    (dict(D=96), 2, "head dim"),
+    (dict(Skv=0), 1, "non-positive"),
+    (dict(gran=5), 1, "granularity"),
+    (dict(rope=3), 1, "rope_mode"),
+    (dict(rope=1, qc=FAKE, qs=FAKE), 1, "cos and sin"),     # K's tables missing
+    (dict(eps=-1.0), 1, "eps"),
+    (dict(kss=127), 2, "aligned"),
+    (dict(vss=127), 2, "aligned"),
+    (dict(ldv=64), 2, "ldv"),                                # below Skv
+    (dict(ldv=200), 2, "ldv"),                               # not a multiple of 128
+    (dict(nbytes=0), 3, "workspace"),
+    (dict(ws=FAKE + 16), 3, "workspace"),                    # not 256-byte aligned
+])
+def test_rmsnorm_quantize_qkv_argument_checks(kw: dict, status: int, msg: str) -> None:
+    """The fused Q/K-norm + V entry refuses bad arguments on the host, before
+    any launch, with the single-tensor call's messages."""
+    L = _capi.lib()
+    assert _norm_qkv(L, **kw) == status
+    assert msg in L.rp_last_error().decode()
+
+
+def test_rmsnorm_qkv_workspace_sizing() -> None:
+    """Q's, K's and V's partial maxima (one per 16384 elements of a group),
+    each run padded to 256 bytes, then Q's and K's fp32 inverse norms."""
+    L = _capi.lib()
+    pad = lambda n: (n + 255) // 256 * 256  # noqa: E731
+    B, H, Sq, Skv, D = 1, 40, 75600, 512, 128
+    nq = H * -(-Sq * D // 16384)
+    nk = H * -(-Skv * D // 16384)
+    assert L.rp_fp8_rmsnorm_quant_qkv_workspace_bytes(B, H, Sq, Skv, D, 0) == \
+        pad(4 * nq) + 2 * pad(4 * nk) + pad(4 * H * Sq) + 4 * H * Skv
+    # per tensor: one group, the same block count
+    assert L.rp_fp8_rmsnorm_quant_qkv_workspace_bytes(B, H, Sq, Skv, D, 1) == \
+        pad(4 * nq) + 2 * pad(4 * nk) + pad(4 * H * Sq) + 4 * H * Skv
+    assert L.rp_fp8_rmsnorm_quant_qkv_workspace_bytes(1, 2, 64, 64, 96, 0) == 0
+    assert L.rp_fp8_rmsnorm_quant_qkv_workspace_bytes(1, 2, 64, 0, 128, 0) == 0
+
+
 def test_multi_block_launch_plan() -> None:
     """Which shapes stream several query blocks per workgroup (short,
     unmasked key ranges with many query blocks), and that the others keep

@@ -607,22 +607,24 @@ def test_cosmos_full_shape_per_tensor_through_fused_qknorm(gpu: torch.device) ->
     assert C2.Skv % 128 == 0
     q, k, v = attn_inputs(C2, device=gpu, normalize=False)
     out = ops.fp8_flash_attention_qknorm(q, k, v, granularity="tensor", out_dtype=torch.float32)
-    dqq, q8 = ops.rmsnorm_scale_quantize(q, granularity="tensor")
-    dqk, k8 = ops.rmsnorm_scale_quantize(k, granularity="tensor")
+    # the op's own quantizer call: Q/K prologue and V in shared launches
+    dqq, q8, dqk, k8, dqv, vt8 = ops.rmsnorm_scale_quantize_qkv(q, k, v, granularity="tensor")
     torch.cuda.synchronize()
     heads = [0, 13, 31]
     rows = np.sort(np.random.default_rng(2).choice(C2.Sq, size=128, replace=False))
     ora = []
-    for x, dq_dev, c_dev in ((q, dqq, q8), (k, dqk, k8), (v, None, None)):
+    for x, dq_dev, c_dev, norm in ((q, dqq, q8, True), (k, dqk, k8, True), (v, dqv, vt8, False)):
         bits = bf16_bits(x.cpu())
-        if dq_dev is not None:
+        if norm:
             bits = native.rmsnorm_bf16(bits, 1e-6)
         s = float(native.dequant_from_amax(native.amax_bf16(bits)))
         codes = {h: native.quantize_bf16(bits[0, h], s) for h in heads}
-        if dq_dev is not None:
-            assert dq_dev.cpu().numpy()[0] == np.float32(s)
-            for h in heads:
-                assert np.array_equal(codes_np(c_dev[0, h]), codes[h]), h
+        assert dq_dev.cpu().numpy()[0] == np.float32(s)
+        for h in heads:
+            got_c = codes_np(c_dev[0, h])
+            if not norm:   # V^T (D, ldv) -> (Skv, D)
+                got_c = np.ascontiguousarray(got_c[:, :C2.Skv].T)
+            assert np.array_equal(got_c, codes[h]), h
         ora.append((s, codes))
         del bits
     got = out[0, heads][:, torch.from_numpy(rows).to(gpu)].cpu().numpy()
@@ -631,7 +633,7 @@ def test_cosmos_full_shape_per_tensor_through_fused_qknorm(gpu: torch.device) ->
                                      block_n=ops.BLOCK_N) for h in heads])
     _check(got, ref, f"c2 per-tensor heads {heads} rows 128")
     assert torch.isfinite(out).all()
-    del q, k, v, out, q8, k8
+    del q, k, v, out, q8, k8, vt8
     torch.cuda.empty_cache()
 
 

@@ -1,4 +1,5 @@
-"""GPU parity of the fused QK-norm prologue (rp_fp8_rmsnorm_scale_quantize):
+"""GPU parity of the fused QK-norm prologue (rp_fp8_rmsnorm_scale_quantize, and
+rp_fp8_rmsnorm_scale_quantize_qkv with V's quantizer in the same launches):
 scales and codes bit-exact against oracle/prologue.py, which restates the
 normalisation with the kernel's summation order and the reference quantizer.
 """
@@ -66,6 +67,75 @@ def test_prologue_bit_exact(gpu: torch.device, case: tuple) -> None:
     got = codes_np(codes)
     mism = np.flatnonzero(got.reshape(-1) != codes_ref.reshape(-1))
     assert mism.size == 0, f"{name}: {mism.size} codes differ, first at {mism[:5]}"
+
+
+QKV_CASES = [
+    # name, (B, H, Sq, Skv, D), weights, rope, granularity, permuted (B, S, H, D) inputs
+    ("self_d128", (1, 4, 1000, 1000, 128), False, None, "bh", False),
+    ("cross_weights_tensor", (2, 3, 700, 300, 128), True, None, "tensor", True),
+    ("kv_longer_rope_half_d64", (1, 3, 200, 777, 64), True, "half", "bh", False),
+    ("interleaved_tensor_d64", (2, 2, 300, 300, 64), False, "interleaved", "tensor", True),
+    ("rope_half_d128_strided", (1, 2, 513, 640, 128), True, "half", "bh", True),
+    ("tiny", (1, 1, 5, 3, 64), False, None, "bh", False),
+]
+
+
+@pytest.mark.parametrize("case", QKV_CASES, ids=[c[0] for c in QKV_CASES])
+def test_fused_qkv_prologue_bit_exact(gpu: torch.device, case: tuple) -> None:
+    """rp_fp8_rmsnorm_scale_quantize_qkv: Q's and K's scales and codes equal
+    the prologue oracle's (each with its own weight and tables), V's transposed
+    codes equal the plain quantizer oracle's, and all of it -- V^T's zeroed
+    padding columns included -- equals the three single-tensor calls."""
+    from oracle import native
+    from tests._helpers import bf16_bits
+
+    name, (B, H, Sq, Skv, D), use_w, rope, gran, permuted = case
+    seed = sum(map(ord, name))
+
+    def make(S, sd, scale):
+        if permuted:
+            return _x(sd, (B, S, H, D), scale).to(gpu).permute(0, 2, 1, 3)
+        return _x(sd, (B, H, S, D), scale).to(gpu)
+
+    q, k, v = make(Sq, seed, 2.0), make(Skv, seed + 1, 1.0), make(Skv, seed + 2, 0.5)
+    wq = _x(seed + 3, (D,), 0.8) if use_w else None
+    wk = _x(seed + 4, (D,), 1.2) if use_w else None
+    tq, tk = (_tables(Sq, D), _tables(Skv, D)) if rope else ((None, None), (None, None))
+    to_dev = lambda t: None if t[0] is None else tuple(torch.from_numpy(a).to(gpu) for a in t)  # noqa: E731
+    dev_w = lambda w: None if w is None else w.to(gpu)  # noqa: E731
+    qs, q8, ks, k8, vs, vt8 = ops.rmsnorm_scale_quantize_qkv(
+        q, k, v, norm_q_weight=dev_w(wq), norm_k_weight=dev_w(wk), rope_q=to_dev(tq),
+        rope_k=to_dev(tk), rope_layout=rope or "half", granularity=gran)
+    mode = {None: P.ROPE_NONE, "half": P.ROPE_HALF, "interleaved": P.ROPE_INTERLEAVED}[rope]
+    for x, w, t, s, c in ((q, wq, tq, qs, q8), (k, wk, tk, ks, k8)):
+        dq_ref, codes_ref = P.quantize_prologue(x.cpu().contiguous(), 1e-6, w, t[0], t[1], mode,
+                                                gran)
+        assert np.array_equal(s.cpu().numpy().view(np.uint32), dq_ref.view(np.uint32)), name
+        assert np.array_equal(codes_np(c), codes_ref), name
+    n = B * H if gran == "bh" else 1
+    dv_ref, cv_ref = native.quantize_groups(bf16_bits(v.cpu().contiguous()), n)
+    assert np.array_equal(vs.cpu().numpy(), dv_ref), name
+    vt = codes_np(vt8)
+    assert np.array_equal(np.ascontiguousarray(np.swapaxes(vt[..., :Skv], -1, -2)), cv_ref)
+    assert not vt[..., Skv:].any(), "V^T padding columns must be zero"
+    # the single-tensor calls, bit for bit
+    s1, c1 = ops.rmsnorm_scale_quantize(q, dev_w(wq), 1e-6, to_dev(tq), rope or "half", gran)
+    s2, c2 = ops.rmsnorm_scale_quantize(k, dev_w(wk), 1e-6, to_dev(tk), rope or "half", gran)
+    s3, c3 = ops.scale_quantize(v, gran, "bhds")
+    for a, b in ((qs, s1), (ks, s2), (vs, s3)):
+        assert torch.equal(a.view(torch.int32), b.view(torch.int32)), name
+    for a, b in ((q8, c1), (k8, c2), (vt8, c3)):
+        assert a.shape == b.shape and torch.equal(a.view(torch.uint8), b.view(torch.uint8)), name
+
+
+def test_fused_qkv_refuses_rope_for_one_tensor(gpu: torch.device) -> None:
+    """One rotary layout serves Q and K in the fused call: tables for only one
+    of them are refused on the host (fp8_flash_attention_qknorm then runs the
+    single-tensor calls)."""
+    x = torch.zeros(1, 2, 64, 64, dtype=torch.bfloat16, device=gpu)
+    t = tuple(torch.from_numpy(a).to(gpu) for a in _tables(64, 64))
+    with pytest.raises(ValueError, match="both q and k"):
+        ops.rmsnorm_scale_quantize_qkv(x, x, x, rope_q=t)
 
 
 def test_prologue_reads_permuted_bshd_view(gpu: torch.device) -> None:

@@ -380,7 +380,7 @@ def test_gemm_slot_ring_negative_controls() -> None:
 
 
 # ----------------------------- quantizer: the V^T tile's LDS swizzle
-QUANT = (CSRC / "rp_quant.hip").read_text()
+QUANT = (CSRC / "rp_quant_dev.h").read_text()   # the transposed apply body
 VT_W = _fn(_expr(QUANT, r"const int qs = (4 \* \(q \^ \(8 \* \(c & 3\)\)\));"), "q", "c")
 VT_R = _fn(_expr(QUANT, r"const int sch = (ch \^ \(2 \* \(\(dr >> 3\) & 3\)\));"), "ch", "dr")
 
