@@ -247,6 +247,8 @@ def bench_attention(args, cfg) -> dict:
         cfg.B, cfg.H, cfg.Sq, cfg.Skv, cfg.D, mask, ops._stream(q)) > 0)
     attn_launches = ("attn_fwd_kernel + attn_combine_kernel (the merge of the key-split rows)"
                      if merged else "attn_fwd_kernel")
+    if merged and splits == 0:   # the balanced launch clears its item counter first
+        attn_launches = "attn_zero_counter_kernel + " + attn_launches
     qbytes = QUANT_BYTES_PER_ELEM * cfg.quant_elems
     q_gbps = qbytes / (quant_ms * 1e-3) / 1e9
     res = {

@@ -248,8 +248,11 @@ int rp_fp8_attn_fwd_split(const uint8_t* q8, const uint8_t* k8, const uint8_t* v
  * whole one.  For unmasked shapes whose blocks do not fill whole rounds, the
  * largest number of query blocks per head that does runs over the whole key
  * range, and the keys of the remaining blocks are split 2, 4 or 8 ways; both
- * kinds of workgroup run in one launch, the split ones dispatched last, and
- * rp_fp8_attn_fwd_split's merge follows.  E.g. (1, 40, 75600, 75600, 128) on
+ * kinds of workgroup run in one launch, and rp_fp8_attn_fwd_split's merge
+ * follows.  The split items and the last unsplit items of every XCD's share
+ * are handed out through a counter in the workspace (zeroed by the call's
+ * own first kernel), so the XCDs that run faster take more of them; calls
+ * that may overlap must not share a workspace.  E.g. (1, 40, 75600, 75600, 128) on
  * 256 CUs runs 288 blocks per head unsplit and the last 8 split 4 ways.  Rows
  * of the unsplit blocks are rp_fp8_attn_fwd's bit for bit; rows of the split
  * ones are what rp_fp8_attn_fwd_split computes for them.  Shapes with

@@ -54,8 +54,10 @@
 //   workgroups resident on one XCD (dispatch is round-robin over the 8
 //   XCDs) work on the same head and share its K/V through that XCD's L2.
 //   The balanced launch (tail_plan) adds key-split workgroups for the query
-//   blocks past the last whole round, dispatched last on every XCD; short
-//   key ranges run several query blocks per workgroup (multi_block_plan).
+//   blocks past the last whole round; they and the last unsplit items of
+//   every XCD's share are pooled behind a counter, so faster XCDs take more
+//   of them.  Short key ranges run several query blocks per workgroup
+//   (multi_block_plan).
 
 #include "rp_common.h"
 
@@ -103,6 +105,13 @@ struct AttnArgs {
   int qb_begin;
   int ws_rows;
   int n_main;
+  // A mixed launch hands its key-split items out through this counter
+  // (zeroed before the launch) to n_grid - n_main workgroups, more than the
+  // n_work - n_main items: the XCDs that finish their unsplit share first
+  // take more of them, and workgroups that find none left return at once.
+  unsigned* item_counter;
+  int n_grid;
+  int pool_r;   // unsplit items per XCD share that go to the pool
 };
 
 // Output kinds of the attention kernel.
@@ -475,11 +484,39 @@ void attn_fwd_kernel(AttnArgs a) {
   const int xcd = w & 7, k_x = w >> 3;
   // a mixed launch's XCDs each run their share of the unsplit items first,
   // then their share of the key-split ones, which fill the launch's end
-  const int pm = MIXED ? a.n_main >> 3 : 0;
-  const bool part = OUT == kOutSplit || (MIXED && k_x >= pm);
-  const int nw = MIXED && part ? a.n_work - a.n_main : a.n_work;
+  const int pm = MIXED ? a.n_main >> 3 : 0;      // unsplit items per XCD
+  const int ps = MIXED ? pm - a.pool_r : 0;       // of which taken in place
+  bool part = OUT == kOutSplit;
+  const int nw = MIXED ? a.n_work - a.n_main : a.n_work;   // split items
   const int per = nw >> 3, rem = nw & 7;
-  const int L2 = MIXED && !part ? xcd * pm + k_x : xcd * per + min(xcd, rem) + (k_x - pm);
+  int L2 = MIXED ? xcd * pm + k_x : xcd * per + min(xcd, rem) + k_x;
+  if constexpr (MIXED) {
+    if (k_x >= ps) {
+      // the next pooled item, whichever XCD asks: first the last pool_r
+      // unsplit items of every XCD's share, then the key-split items
+      __shared__ int item;
+      if (threadIdx.x == 0) item = (int)atomicAdd(a.item_counter, 1u);
+      __syncthreads();
+      const int it = item;
+      if (it >= 8 * a.pool_r + nw) return;   // every item is taken
+      part = it >= 8 * a.pool_r;
+      // consecutive pooled items share K/V: the unsplit ones share by share
+      // (one head's consecutive query blocks), the split ones by head and key
+      // range.  (Interleaving the shares read 13.4 GB of HBM per C3 launch
+      // against 8.8 GB this way, in the same time.)
+      if (!part) {
+        L2 = (it / a.pool_r) * pm + ps + it % a.pool_r;
+      } else {
+        const int r = it - 8 * a.pool_r;
+        const int nq_s = a.n_qblocks - a.qb_begin;            // split blocks per head
+        const int per_h = nq_s * a.kv_splits * (DV < DK ? 2 : 1);
+        const int hh = r / per_h, rr = r - hh * per_h;
+        const int hv = DV < DK ? rr & 1 : 0, r2 = DV < DK ? rr >> 1 : rr;
+        const int sp = r2 / nq_s, ql = r2 - sp * nq_s;
+        L2 = hh * per_h + ((ql * a.kv_splits + sp) << (DV < DK ? 1 : 0)) + hv;
+      }
+    }
+  }
   // the two halves of a split query block are neighbours: same XCD, same
   // K tiles in its L2
   const int half = DV < DK ? L2 & 1 : 0;
@@ -1010,10 +1047,23 @@ void launch_fwd(const AttnArgs& a, hipStream_t st) {
 
 // The balanced launch: the unsplit query blocks into the output, the rest
 // key-split into the workspace (attn_combine_kernel merges them after).
+// The XCDs of one GPU run the same workgroups at different speeds (measured
+// at C3, per-XCD mean time of an unsplit workgroup: 1.12 to 1.19 ms, the
+// same XCDs slow on every launch of a box), so equal static shares end
+// up to 3 ms apart.  A mixed launch therefore pools the key-split items and
+// the last kPoolPerXcd unsplit items of every XCD's share behind one
+// counter: C3 balanced 54.6 -> 54.0 ms with the split items pooled, 53.4 ms
+// with 32 unsplit items per XCD as well (64: the same), alternating on one
+// box.
+constexpr int kPoolPerXcd = 32;
+
+__global__ void attn_zero_counter_kernel(unsigned* c) { *c = 0u; }
+
 template <int D, int OUT>
 void launch_fwd_mixed(const AttnArgs& a, hipStream_t st) {
   constexpr int DV = kPVWidth<D>;
-  hipLaunchKernelGGL((attn_fwd_kernel<D, DV, OUT, false, false, false, true>), dim3(a.n_work),
+  hipLaunchKernelGGL(attn_zero_counter_kernel, dim3(1), dim3(1), 0, st, a.item_counter);
+  hipLaunchKernelGGL((attn_fwd_kernel<D, DV, OUT, false, false, false, true>), dim3(a.n_grid),
                      dim3(512), 0, st, a);
 }
 
@@ -1070,9 +1120,10 @@ inline void split_plan(int Skv, int kv_splits, int* split_tiles, int* n_splits) 
 // fill the last rounds; attn_combine_kernel merges their partial results.
 // C3 self (40 heads x 296 blocks on 256 CUs): 288 blocks per head in 45
 // rounds, the last 8 split 4 ways in 1.25 round-equivalents, against 47.
-// Both kinds of workgroup run in one launch, the split ones dispatched last
-// on every XCD: they also fill the uneven end of the unsplit rounds, which
-// a second launch would wait for.
+// Both kinds of workgroup run in one launch, the split ones last: they also
+// fill the uneven end of the unsplit rounds, which a second launch would
+// wait for, and they are pooled with the last unsplit items of every XCD's
+// share (kPoolPerXcd).
 struct TailPlan {
   int main_blocks;   // query blocks per head run unsplit
   int splits;        // key splits of the remaining blocks (1: a plain launch)
@@ -1146,11 +1197,22 @@ int launch_attn(const AttnArgs& base, int out_dtype, hipStream_t st) {
   }
   a.n_work = (int)work;
   a.n_main = mixed ? (int)(heads * a.qb_begin) : 0;
-  if (mixed && (a.n_main % 8 != 0 || a.kv_splits < 2 || a.mask != RP_MASK_NONE)) {
-    rp_set_error("attn: mixed launch needs unsplit workgroups in multiples of 8, key splits "
-                 "and no mask");
+  if (mixed && (a.n_main % 8 != 0 || a.kv_splits < 2 || a.mask != RP_MASK_NONE ||
+                a.item_counter == nullptr)) {
+    rp_set_error("attn: mixed launch needs unsplit workgroups in multiples of 8, key splits, "
+                 "no mask and an item counter");
     return RP_ERR_UNSUPPORTED;
   }
+  // pooled items: the last pool_r unsplit items of each XCD's share and the
+  // split items, run by twice as many workgroups, the same number per XCD
+  a.pool_r = mixed ? min(kPoolPerXcd, a.n_main / 8) : 0;
+  const int64_t pooled = 8 * (int64_t)a.pool_r + (work - a.n_main);
+  const int64_t grid = mixed ? a.n_main - 8 * a.pool_r + (2 * pooled + 7) / 8 * 8 : work;
+  if (grid > 0x7fffffff) {
+    rp_set_error("attn: grid too large");
+    return RP_ERR_UNSUPPORTED;
+  }
+  a.n_grid = (int)grid;
   if (a.kv_splits == 1) {
     if (kind == kOutF32)
       launch_fwd<D, kOutF32>(a, st);
@@ -1355,12 +1417,17 @@ extern "C" int rp_fp8_attn_balanced_plan(int B, int H, int Sq, int Skv, int D, i
 }
 
 // Workspace of rp_fp8_attn_fwd_balanced: the key-split partial results of
-// the rows past the unsplit blocks.
-static size_t balanced_ws_bytes(const TailPlan& t, int B, int H, int Sq, int Skv, int D) {
-  if (t.splits <= 1) return 0;
+// the rows past the unsplit blocks, then 256 bytes for the launch's item
+// counter.
+static size_t balanced_partials_bytes(const TailPlan& t, int B, int H, int Sq, int Skv, int D) {
   int split_tiles = 0, n_splits = 1;
   split_plan(Skv, t.splits, &split_tiles, &n_splits);
-  return rp_fp8_attn_workspace_bytes(B, H, Sq - t.main_blocks * kBlockM, D, n_splits);
+  const size_t n = rp_fp8_attn_workspace_bytes(B, H, Sq - t.main_blocks * kBlockM, D, n_splits);
+  return (n + 255) / 256 * 256;
+}
+static size_t balanced_ws_bytes(const TailPlan& t, int B, int H, int Sq, int Skv, int D) {
+  if (t.splits <= 1) return 0;
+  return balanced_partials_bytes(t, B, H, Sq, Skv, D) + 256;
 }
 
 extern "C" size_t rp_fp8_attn_balanced_workspace_bytes(int B, int H, int Sq, int Skv, int D,
@@ -1402,5 +1469,7 @@ extern "C" int rp_fp8_attn_fwd_balanced(const uint8_t* q8, const uint8_t* k8, co
   a.ws_ml = static_cast<float*>(workspace);
   a.ws_acc = reinterpret_cast<float*>(static_cast<char*>(workspace) +
                                       (rows * 2 * sizeof(float) + 255) / 256 * 256);
+  a.item_counter = reinterpret_cast<unsigned*>(static_cast<char*>(workspace) +
+                                               balanced_partials_bytes(t, B, H, Sq, Skv, D));
   return attn_run(a, D, out_dtype, stream);
 }
