@@ -361,6 +361,24 @@ int rp_fp8_linear(const uint8_t* a8, const uint8_t* b8, int b_layout, const void
                   float a_scale, float b_scale, const float* a_scale_dev,
                   const float* b_scale_dev, void* stream);
 
+/* rp_fp8_linear (bias may be NULL: rp_fp8_gemm) with the work balanced
+ * across the GPU's XCDs, which run the same tiles at different speeds (at
+ * C4 the mean 256 x 256 tile took 63-68 us depending on the XCD, so equal
+ * static shares ended 0.25 ms apart).  Every XCD runs its share of tiles
+ * but the last few in place; the tiles so left are handed out, in share
+ * order, through a counter in `workspace` to whichever XCD asks first.  The
+ * outputs equal rp_fp8_linear's bit for bit.  workspace: at least
+ * RP_GEMM_BALANCED_WORKSPACE_BYTES, 256-byte aligned, zeroed by the call's
+ * own first kernel, not shared by calls that may overlap.  No counterpart
+ * in the reference (its GEMM launch takes no workspace); for callers that
+ * can pass one, e.g. the FP8 linear layers. */
+#define RP_GEMM_BALANCED_WORKSPACE_BYTES 256u
+int rp_fp8_linear_balanced(const uint8_t* a8, const uint8_t* b8, int b_layout, const void* bias,
+                           void* c, int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldb,
+                           int64_t ldc, float a_scale, float b_scale, const float* a_scale_dev,
+                           const float* b_scale_dev, void* workspace, size_t workspace_bytes,
+                           void* stream);
+
 /* rp_fp8_gemm with row-wise scales, batched: for each batch z < `batch`,
  *   C_z (M, N) = bf16( fp32(fp32(A8_z . B8_z) * row_scale_z[m]) * col_scale_z[n] )
  * with A8_z = a8 + z*bsa, B8_z = b8 + z*bsb (bytes), C_z = c + z*bsc,

@@ -33,6 +33,7 @@ RP_ROPE_INTERLEAVED = 2
 RP_QKV_NOALLOC_SCRATCH_BYTES = 1 << 20
 RP_B_NK = 0
 RP_B_KN = 1
+RP_GEMM_BALANCED_WORKSPACE_BYTES = 256
 
 #: Every function include/repercep_fp8.h declares.
 EXPORTS = (
@@ -47,7 +48,8 @@ EXPORTS = (
     "rp_fp8_attn_balanced_workspace_bytes", "rp_fp8_attn_fwd_balanced",
     "rp_fp8_rmsnorm_quant_workspace_bytes",
     "rp_fp8_rmsnorm_scale_quantize", "rp_fp8_rmsnorm_quant_qkv_workspace_bytes",
-    "rp_fp8_rmsnorm_scale_quantize_qkv", "rp_fp8_gemm", "rp_fp8_linear", "rp_fp8_transpose",
+    "rp_fp8_rmsnorm_scale_quantize_qkv", "rp_fp8_gemm", "rp_fp8_linear",
+    "rp_fp8_linear_balanced", "rp_fp8_transpose",
     "rp_fp8_gemm_rowwise", "rp_fp8_rowwise_quantize", "rp_transpose16",
     "rp_fp8_softmax_rowwise_quantize",
     "rp_selftest_e4m3", "rp_selftest_scale",
@@ -130,6 +132,8 @@ def _declare(L: ctypes.CDLL) -> None:
     L.rp_fp8_linear.restype = _int
     L.rp_fp8_linear.argtypes = [_vp, _vp, _int, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64,
                                 _f32, _f32, _vp, _vp, _vp]
+    L.rp_fp8_linear_balanced.restype = _int
+    L.rp_fp8_linear_balanced.argtypes = (list(L.rp_fp8_linear.argtypes[:-1]) + [_vp, _sz, _vp])
     L.rp_fp8_gemm_rowwise.restype = _int
     L.rp_fp8_gemm_rowwise.argtypes = ([_vp, _vp, _int, _vp] + [_i64] * 6 + [_vp, _vp]
                                       + [_i64] * 6 + [_vp])

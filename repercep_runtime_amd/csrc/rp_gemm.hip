@@ -56,6 +56,11 @@ struct GemmArgs {
   // batched launches (blockIdx.y = batch): strides of A and B (bytes), C
   // (elements) and the two scale vectors (elements)
   int64_t bsa, bsb, bsc, bsr, bss;
+  // rp_fp8_linear_balanced (one batch): the last pool_r tiles of every
+  // XCD's share of gemm256_kernel's tiles are handed out through this
+  // counter, zeroed before the launch; null: every tile in place
+  unsigned* item_counter;
+  int pool_r;
 };
 
 // The batch a workgroup works on: offsets every operand pointer (one batch
@@ -426,7 +431,27 @@ void gemm256_kernel(GemmArgs g) {
   const int w = blockIdx.x;
   const int per = nwork >> 3, rem = nwork & 7;
   const int xcd = w & 7;
-  const int L = xcd * per + min(xcd, rem) + (w >> 3);
+  int L = xcd * per + min(xcd, rem) + (w >> 3);
+  if (g.item_counter != nullptr) {
+    // XCDs run at different speeds: every XCD runs its share of tiles but
+    // the last pool_r (pool_r + 1 for the first rem shares) in place, and
+    // the tiles so left go, in share order, to whichever XCD asks first
+    const int in_place = per - g.pool_r;
+    if ((w >> 3) >= in_place) {
+      // the operand ring is full: its first bytes pass the item on, read by
+      // every thread before the first loads can land there
+      int* const item = reinterpret_cast<int*>(smem);
+      if (threadIdx.x == 0) *item = (int)atomicAdd(g.item_counter, 1u);
+      __syncthreads();
+      const int p = *item;
+      __syncthreads();
+      if (p >= 8 * g.pool_r + rem) return;   // every tile is taken
+      const int big = rem * (g.pool_r + 1);    // pooled tiles of the larger shares
+      const int x = p < big ? p / (g.pool_r + 1) : rem + (p - big) / g.pool_r;
+      const int j = p < big ? p - x * (g.pool_r + 1) : (p - big) - (x - rem) * g.pool_r;
+      L = x * per + min(x, rem) + in_place + j;
+    }
+  }
   constexpr int kBand = 4;
   const int band_tiles = kBand * g.tiles_n;
   const int band = L / band_tiles;
@@ -735,15 +760,35 @@ void launch_g256(const GemmArgs& g, dim3 grid, hipStream_t st) {
     hipLaunchKernelGGL((gemm256_kernel<KN, kEpiPlain>), grid, dim3(kG2Threads), 0, st, g);
 }
 
+__global__ void gemm_zero_counter_kernel(unsigned* c) { *c = 0u; }
+
+// Tiles per XCD share handed out through the counter of a balanced launch.
+// At C4 (15,984 tiles, ~62 per CU), alternating on one box: static shares
+// 4.04-4.07 ms ((K, N) B) and 3.97-3.99 ms ((N, K)); 32 pooled per share
+// 4.01-4.02 / 3.93; 64 3.98-3.99 / 3.90-3.91; 128 the same as 64.
+constexpr int kGemmPoolPerXcd = 64;
+
 int launch_gemm256(GemmArgs g, int64_t batch, hipStream_t st) {
   g.tiles_m = (int)((g.M + kG2Tile - 1) / kG2Tile);
   g.tiles_n = (int)((g.N + kG2Tile - 1) / kG2Tile);
   const int64_t nwork = (int64_t)g.tiles_m * g.tiles_n;
-  if (nwork > 0x7fffffff) {
+  if (nwork > 0x3fffffff) {
     rp_set_error("gemm: grid too large");
     return RP_ERR_UNSUPPORTED;
   }
-  const dim3 grid((unsigned)nwork, (unsigned)batch);
+  int64_t nwg = nwork;
+  const int64_t per = nwork >> 3;
+  g.pool_r = g.item_counter != nullptr && batch == 1 ? (int)min((int64_t)kGemmPoolPerXcd, per) : 0;
+  if (g.pool_r == 0) {
+    g.item_counter = nullptr;
+  } else {
+    // the tiles left by every share, run by twice as many workgroups, the
+    // same number on every XCD
+    const int64_t pooled = 8 * (int64_t)g.pool_r + (nwork & 7);
+    nwg = 8 * (per - g.pool_r) + (2 * pooled + 7) / 8 * 8;
+    hipLaunchKernelGGL(gemm_zero_counter_kernel, dim3(1), dim3(1), 0, st, g.item_counter);
+  }
+  const dim3 grid((unsigned)nwg, (unsigned)batch);
   if (g.b_kn)
     launch_g256<true>(g, grid, st);
   else
@@ -810,7 +855,8 @@ struct RowwiseBatch {
 static int gemm_run(const uint8_t* a8, const uint8_t* b8, int b_layout, const void* bias,
                     void* c, int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldb,
                     int64_t ldc, float a_scale, float b_scale, const float* a_scale_dev,
-                    const float* b_scale_dev, void* stream, const RowwiseBatch& rb = {}) {
+                    const float* b_scale_dev, void* stream, const RowwiseBatch& rb = {},
+                    unsigned* item_counter = nullptr) {
   if (!a8 || !b8 || !c) {
     rp_set_error("gemm: null pointer");
     return RP_ERR_INVALID_ARGUMENT;
@@ -865,6 +911,7 @@ static int gemm_run(const uint8_t* a8, const uint8_t* b8, int b_layout, const vo
   g.M = M; g.N = N; g.K = K; g.lda = lda; g.ldb = ldb; g.ldc = ldc;
   g.a_scale = a_scale; g.b_scale = b_scale; g.a_dev = a_scale_dev; g.b_dev = b_scale_dev;
   g.b_kn = kn ? 1 : 0;
+  g.item_counter = item_counter;
   // The large-tile kernel reads whole 64-byte K sub-slices and keeps tile
   // offsets in 32 bits; from a (K, N) B it loads whole 16-byte N granules.
   const bool big = K % kG2Sub == 0 && lda * (int64_t)kG2Tile < (int64_t)1 << 32 &&
@@ -889,6 +936,23 @@ extern "C" int rp_fp8_linear(const uint8_t* a8, const uint8_t* b8, int b_layout,
                              const float* b_scale_dev, void* stream) {
   return gemm_run(a8, b8, b_layout, bias, c, M, N, K, lda, ldb, ldc, a_scale, b_scale,
                   a_scale_dev, b_scale_dev, stream);
+}
+
+extern "C" int rp_fp8_linear_balanced(const uint8_t* a8, const uint8_t* b8, int b_layout,
+                                      const void* bias, void* c, int64_t M, int64_t N, int64_t K,
+                                      int64_t lda, int64_t ldb, int64_t ldc, float a_scale,
+                                      float b_scale, const float* a_scale_dev,
+                                      const float* b_scale_dev, void* workspace,
+                                      size_t workspace_bytes, void* stream) {
+  if (workspace == nullptr || workspace_bytes < RP_GEMM_BALANCED_WORKSPACE_BYTES ||
+      reinterpret_cast<uintptr_t>(workspace) % 256 != 0) {
+    rp_set_error("gemm: the balanced launch needs a 256-byte aligned workspace of %u bytes",
+                 (unsigned)RP_GEMM_BALANCED_WORKSPACE_BYTES);
+    return RP_ERR_WORKSPACE;
+  }
+  return gemm_run(a8, b8, b_layout, bias, c, M, N, K, lda, ldb, ldc, a_scale, b_scale,
+                  a_scale_dev, b_scale_dev, stream, RowwiseBatch{},
+                  static_cast<unsigned*>(workspace));
 }
 
 extern "C" int rp_fp8_gemm_rowwise(const uint8_t* a8, const uint8_t* b8, int b_layout, void* c,

@@ -625,17 +625,19 @@ def fp8_gemm(a8: torch.Tensor, b8: torch.Tensor, a_scale: float | torch.Tensor,
             0.0 if b_dev is not None else float(b_scale),
             a_dev.data_ptr() if a_dev is not None else None,
             b_dev.data_ptr() if b_dev is not None else None, _stream(a8))
-    if bias is None:
-        C.check(C.lib().rp_fp8_gemm(a8.data_ptr(), b8.data_ptr(), layout, out.data_ptr(), *args),
-                "rp_fp8_gemm")
-    else:
+    if bias is not None:
         _check_bf16("bias", bias)
         if bias.shape != (N,) or not bias.is_contiguous():
             raise ValueError(f"bias must be a contiguous ({N},) tensor, got {tuple(bias.shape)}")
         if bias.data_ptr() % 8 != 0:          # the epilogue reads 4 bias values at a time
             bias = bias.clone()
-        C.check(C.lib().rp_fp8_linear(a8.data_ptr(), b8.data_ptr(), layout, bias.data_ptr(),
-                                      out.data_ptr(), *args), "rp_fp8_linear")
+    # the balanced launch (tiles pooled across XCDs) needs a small workspace
+    # for its counter; the outputs are rp_fp8_gemm's / rp_fp8_linear's bits
+    ws = torch.empty(C.RP_GEMM_BALANCED_WORKSPACE_BYTES, dtype=torch.uint8, device=a8.device)
+    *sizes, stream = args
+    C.check(C.lib().rp_fp8_linear_balanced(
+        a8.data_ptr(), b8.data_ptr(), layout, bias.data_ptr() if bias is not None else None,
+        out.data_ptr(), *sizes, ws.data_ptr(), ws.numel(), stream), "rp_fp8_linear_balanced")
     return out
 
 

@@ -138,6 +138,22 @@ def test_linear_argument_checks() -> None:
     assert L.rp_fp8_linear(*bad) == 2 and "multiples" in L.rp_last_error().decode()
 
 
+def test_balanced_linear_argument_checks() -> None:
+    """rp_fp8_linear_balanced refuses a missing, short or unaligned workspace
+    before any launch, then runs rp_fp8_linear's checks."""
+    L = _capi.lib()
+    n = _capi.RP_GEMM_BALANCED_WORKSPACE_BYTES
+    ok = (FAKE, FAKE, NK, None, FAKE, 64, 64, 64, 64, 64, 64, 1.0, 1.0, None, None)
+    for ws, nbytes in ((None, n), (FAKE, n - 1), (FAKE + 16, n)):
+        assert L.rp_fp8_linear_balanced(*ok, ws, nbytes, None) == 3
+        assert "workspace" in L.rp_last_error().decode()
+    bad = list(ok); bad[3] = FAKE + 2
+    assert L.rp_fp8_linear_balanced(*bad, FAKE, n, None) == 2
+    assert "bias" in L.rp_last_error().decode()
+    bad = list(ok); bad[6] = 6
+    assert L.rp_fp8_linear_balanced(*bad, FAKE, n, None) == 2
+
+
 def test_quantizer_argument_checks() -> None:
     L = _capi.lib()
     bf16, f16 = _capi.RP_DTYPE_BF16, _capi.RP_DTYPE_F16

@@ -276,3 +276,44 @@ def test_device_reproduces_golden_vectors(gpu: torch.device,
                           torch.tensor([sb], device=gpu), b_transposed=True)
         for c in (c1, c2):
             assert np.array_equal(bf16_bits(c), c_bits), name
+
+
+def _linear_static(a8, b8, layout, bias, out, M, N, K, sa, sb):
+    from repercep_runtime_amd import _capi as C
+    C.check(C.lib().rp_fp8_linear(a8.data_ptr(), b8.data_ptr(), layout,
+                                  bias.data_ptr() if bias is not None else None, out.data_ptr(),
+                                  M, N, K, a8.stride(0), b8.stride(0), out.stride(0), sa, sb,
+                                  None, None, ops._stream(a8)), "rp_fp8_linear")
+
+
+@pytest.mark.parametrize("M,N,K,layout,with_bias", [
+    (300, 272, 128, "kn", False),     # 4 tiles: shares of 0 and 1 tiles, nothing to pool
+    (2148, 1280, 128, "kn", True),    # 45 tiles: shares of 6 and 5, every tile pooled
+    (2560, 2304, 192, "nk", True),    # 90 tiles: shares of 12 and 11, every tile pooled
+    (C4.M, C4.N, 512, "kn", False),   # the C4 grid (15,984 tiles): 64 pooled per share
+    (C4.M, C4.N, 512, "nk", True),
+])
+def test_balanced_gemm_equals_static_tiles(gpu: torch.device, M: int, N: int, K: int,
+                                           layout: str, with_bias: bool) -> None:
+    """rp_fp8_linear_balanced (the op's launch: the last tiles of every XCD's
+    share handed out through a counter) writes rp_fp8_linear's bits, on grids
+    too small to pool, where every tile is pooled and the XCD shares differ by
+    one tile, and on C4's grid; two calls in a row reuse the workspace (the call zeroes its
+    counter itself)."""
+    from repercep_runtime_amd import _capi as C
+    g = torch.Generator(device=gpu).manual_seed(M + N + K)
+    a8 = torch.randint(0, 126, (M, K), generator=g, device=gpu, dtype=torch.uint8)
+    b8 = torch.randint(0, 126, (K, N) if layout == "kn" else (N, K), generator=g, device=gpu,
+                       dtype=torch.uint8)
+    lay = C.RP_B_KN if layout == "kn" else C.RP_B_NK
+    bias = (torch.randn(N, generator=g, device=gpu).to(torch.bfloat16) if with_bias else None)
+    ref = torch.empty((M, N), dtype=torch.bfloat16, device=gpu)
+    _linear_static(a8, b8, lay, bias, ref, M, N, K, 0.01, 0.02)
+    ws = torch.empty(C.RP_GEMM_BALANCED_WORKSPACE_BYTES, dtype=torch.uint8, device=gpu)
+    for _ in range(2):
+        out = torch.full((M, N), float("nan"), dtype=torch.bfloat16, device=gpu)
+        C.check(C.lib().rp_fp8_linear_balanced(
+            a8.data_ptr(), b8.data_ptr(), lay, bias.data_ptr() if bias is not None else None,
+            out.data_ptr(), M, N, K, a8.stride(0), b8.stride(0), out.stride(0), 0.01, 0.02, None,
+            None, ws.data_ptr(), ws.numel(), ops._stream(a8)), "rp_fp8_linear_balanced")
+        assert torch.equal(out.view(torch.int16), ref.view(torch.int16))
