@@ -1,4 +1,4 @@
-"""The FP8 attention path under HIP graph capture (torch.cuda.graph): small
+"""The FP8 attention path (and the GEMM) under HIP graph capture (torch.cuda.graph): small
 calls are bound by host launch work, which a captured graph removes.  Every
 replay, with new inputs copied into the captured buffers and eager work and
 synchronisations between replays, equals an eager call bit for bit."""
@@ -60,3 +60,28 @@ def test_captured_balanced_launch_replays_match_eager(gpu: torch.device) -> None
         want = ops.fp8_flash_attention(sq.clone(), sk.clone(), sv.clone(), kv_splits=0)
         _ = torch.randn(1024, device=gpu).sum().item()
         assert torch.equal(sout, want), f"replay {rep} differs from eager"
+
+
+def test_captured_balanced_gemm_replays_match_eager(gpu: torch.device) -> None:
+    """ops.fp8_gemm's balanced launch (its counter cleared by a kernel of the
+    call, tiles handed out through it) captured with its workspace from the
+    capture's pool: every replay, with new operands, equals an eager call bit
+    for bit."""
+    M, N, K = 2148, 1280, 256    # 45 tiles: every tile goes through the counter
+    g = torch.Generator(device=gpu).manual_seed(13)
+    a8 = torch.randint(0, 126, (M, K), generator=g, device=gpu, dtype=torch.uint8)
+    b8 = torch.randint(0, 126, (K, N), generator=g, device=gpu, dtype=torch.uint8)
+    ops.fp8_gemm(a8, b8, 0.01, 0.02)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        sout = ops.fp8_gemm(a8, b8, 0.01, 0.02)
+    for rep in range(3):
+        if rep:
+            a8.copy_(torch.randint(0, 126, (M, K), generator=g, device=gpu, dtype=torch.uint8))
+            b8.copy_(torch.randint(0, 126, (K, N), generator=g, device=gpu, dtype=torch.uint8))
+        graph.replay()
+        torch.cuda.synchronize()
+        want = ops.fp8_gemm(a8.clone(), b8.clone(), 0.01, 0.02)
+        _ = torch.randn(1024, device=gpu).sum().item()
+        assert torch.equal(sout.view(torch.int16), want.view(torch.int16)), f"replay {rep}"
