@@ -98,8 +98,10 @@ __device__ __forceinline__ void load_norm(const PParams& p, const uint16_t* cons
   for (int u = 0; u < U; ++u)
 #pragma unroll
     for (int m = 0; m < NC; ++m) {
-      const uint4 v = *reinterpret_cast<const uint4*>(xrow[u] + 8 * (c + TPR * m));
-      const uint32_t w4[4] = {v.x, v.y, v.z, v.w};
+      // non-temporal: each pass reads x once (0.625 -> 0.618 ms per C2 Q/K/V call)
+      const u32x4 v = __builtin_nontemporal_load(
+          reinterpret_cast<const u32x4*>(xrow[u] + 8 * (c + TPR * m)));
+      const uint32_t w4[4] = {v[0], v[1], v[2], v[3]};
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         x[u][8 * m + 2 * i] = bf16_to_f32(w4[i] & 0xffffu);
@@ -479,8 +481,8 @@ __global__ __launch_bounds__(kPThreads) void qkv_norm_apply_kernel(NormQKV a) {
 #pragma unroll
     for (int db = 0; db < D / 64; ++db) {
       if (db > 0) __syncthreads();  // every thread has read the previous tile back
-      apply_t_body<kInBf16>(a.vt, a.dequant + 2 * a.ngroups, a.per_bh, a.vt8, a.ldv, sblk, db,
-                            bh, tile);
+      apply_t_body<kInBf16, false>(a.vt, a.dequant + 2 * a.ngroups, a.per_bh, a.vt8, a.ldv,
+                                   sblk, db, bh, tile);
     }
   }
 }

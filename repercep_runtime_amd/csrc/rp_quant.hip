@@ -71,7 +71,8 @@ __global__ __launch_bounds__(kQThreads) void quant_apply_t_kernel(QParams p, con
                                                                   int per_bh, uint8_t* codes,
                                                                   int64_t ld) {
   __shared__ __attribute__((aligned(16))) uint8_t tile[kTileBytes];
-  apply_t_body<DT>(p, dequant, per_bh, codes, ld, blockIdx.x, blockIdx.y, blockIdx.z, tile);
+  apply_t_body<DT, true>(p, dequant, per_bh, codes, ld, blockIdx.x, blockIdx.y, blockIdx.z,
+                         tile);
 }
 
 // Multi-tensor launches (the Q, K and V of one attention call): blockIdx.y
