@@ -410,7 +410,8 @@ __device__ __forceinline__ void prologue_quant_body(const PParams& p, int64_t bl
                        clamp_e4m3(y[u][2] * qm), clamp_e4m3(y[u][3] * qm));
       o.y = pack4_e4m3(clamp_e4m3(y[u][4] * qm), clamp_e4m3(y[u][5] * qm),
                        clamp_e4m3(y[u][6] * qm), clamp_e4m3(y[u][7] * qm));
-      *reinterpret_cast<uint2*>(codes + r[u] * D + 8 * c) = o;
+      __builtin_nontemporal_store(u32x2{o.x, o.y},
+                                  reinterpret_cast<u32x2*>(codes + r[u] * D + 8 * c));
     }
   });
 }

@@ -11,6 +11,9 @@
 namespace rp {
 namespace {
 
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+
 constexpr int kQThreads = 256;
 constexpr int64_t kElemsPerBlock = 16384;  // 32 KiB of bf16 per block per pass
 
@@ -66,7 +69,10 @@ __device__ __forceinline__ void amax_partial_body(int64_t blk_id, QParams p, uin
     RowCursor cur;
     cur.init(g * p.rows_per_group + first + roff, p);
     for (int64_t r = roff; r < nrows; r += step) {
-      const uint4 v = *reinterpret_cast<const uint4*>(p.x + cur.base + cur.s * p.ss + col * 8);
+      // non-temporal (C3 Q/K/V on permuted views 0.979 -> 0.941 ms per call)
+      const u32x4 vv = __builtin_nontemporal_load(
+          reinterpret_cast<const u32x4*>(p.x + cur.base + cur.s * p.ss + col * 8));
+      const uint4 v = make_uint4(vv[0], vv[1], vv[2], vv[3]);
       m = pk_umax16(m, v.x & 0x7fff7fffu);
       m = pk_umax16(m, v.y & 0x7fff7fffu);
       m = pk_umax16(m, v.z & 0x7fff7fffu);
@@ -112,7 +118,6 @@ __device__ __forceinline__ uint32_t quant4(uint32_t lo_pair, uint32_t hi_pair, f
 // group; each thread issues all of its kFlatLoads 16-byte loads before using
 // any of them, so every wave keeps 8 loads in flight.
 constexpr int kFlatLoads = kElemsPerBlock / 8 / kQThreads;  // 16-byte loads per thread
-typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ void amax_flat_body(int64_t blk_id, const uint16_t* x, int64_t gsize,
                                                               int64_t nbg, uint32_t* partial) {
@@ -176,7 +181,10 @@ __device__ __forceinline__ void quant_flat_body(int64_t blk_id, const uint16_t* 
       uint2 o;
       o.x = quant4<DT>(v[i][0], v[i][1], qm);
       o.y = quant4<DT>(v[i][2], v[i][3], qm);
-      dst[idx] = o;
+      // non-temporal, like every code store of the quantizers: the codes are
+      // read once, by the next kernel (C3 Q/K/V call 0.960 -> 0.917 ms with
+      // the three quantizer stores non-temporal, C2 0.618 -> 0.585 ms)
+      __builtin_nontemporal_store(u32x2{o.x, o.y}, reinterpret_cast<u32x2*>(dst + idx));
     }
   }
 }
@@ -204,11 +212,12 @@ __device__ __forceinline__ void quant_apply_body(int64_t blk_id, QParams p, cons
   const float qm = 1.0f / dequant[per_bh ? cur.bh : 0];
   int64_t r = r0;
   for (int64_t k = roff; k < nrows; k += step) {
-    const uint4 v = *reinterpret_cast<const uint4*>(p.x + cur.base + cur.s * p.ss + col * 8);
-    uint2 o;
-    o.x = quant4<DT>(v.x, v.y, qm);
-    o.y = quant4<DT>(v.z, v.w, qm);
-    *reinterpret_cast<uint2*>(codes + r * p.D + col * 8) = o;
+    // non-temporal: x is read for the last time, the codes are read once
+    // (C3 Q/K/V on permuted (B, S, H, D) views 1.026 -> 0.978 ms per call)
+    const u32x4 v = __builtin_nontemporal_load(
+        reinterpret_cast<const u32x4*>(p.x + cur.base + cur.s * p.ss + col * 8));
+    __builtin_nontemporal_store(u32x2{quant4<DT>(v[0], v[1], qm), quant4<DT>(v[2], v[3], qm)},
+                                reinterpret_cast<u32x2*>(codes + r * p.D + col * 8));
     cur.advance(step, p);
     r += step;
   }
@@ -293,7 +302,9 @@ __device__ __forceinline__ void apply_t_store(const QParams& p, const uint32_t (
     // ch ^ 2((dr >> 3) & 3)
     const int sch = ch ^ (2 * ((dr >> 3) & 3));
     const uint4 v = *reinterpret_cast<const uint4*>(&tile[dr * 128 + ch * 16]);
-    *reinterpret_cast<uint4*>(codes + (bh * p.D + d0 + dr) * ld + s0 + sch * 16) = v;
+    __builtin_nontemporal_store(
+        u32x4{v.x, v.y, v.z, v.w},
+        reinterpret_cast<u32x4*>(codes + (bh * p.D + d0 + dr) * ld + s0 + sch * 16));
   }
 }
 
