@@ -122,6 +122,49 @@ __global__ __launch_bounds__(kQThreads) void apply_multi_kernel(QJobs3 jobs) {
     quant_apply_body<DT>(blockIdx.x, jb.p, jb.dequant, jb.per_bh, jb.codes);
 }
 
+// Calls whose groups have at most kFoldMaxPartials amax partials (small
+// tensors: C1, C5): every apply block folds its own group's partials into
+// the scale -- a few hundred bytes from L2, the same max and the same
+// rounding as the finalize kernel -- and the first block of each group
+// writes it, so the scales need no launch of their own, and V^T's tiles
+// (blockIdx.y == 2) run in the same launch: two launches per call instead
+// of four, which is what bounds calls this small.
+constexpr int64_t kFoldMaxPartials = 256;
+
+template <int DT>
+__global__ __launch_bounds__(kQThreads) void apply_fold_multi_kernel(QJobs3 jobs, QParams vt,
+                                                                     int64_t ld,
+                                                                     int64_t vt_stiles,
+                                                                     int64_t vt_dtiles,
+                                                                     uint8_t* vt8) {
+  __shared__ __attribute__((aligned(16))) uint8_t tile[kTileBytes];
+  const QJob& jb = job_of(jobs);
+  const int64_t blk = blockIdx.x;
+  if (blockIdx.y < 2) {
+    if (blk >= jb.nblocks) return;
+    const int64_t g = blk / jb.p.nbg;
+    const float dq =
+        dequant_from_amax<DT>(block_max_u32<kQThreads>(jb.partial + g * jb.p.nbg, jb.p.nbg));
+    if (blk == g * jb.p.nbg && threadIdx.x == 0) jb.dequant[g] = dq;
+    if (jb.flat)
+      quant_flat_core<DT>(blk, jb.p.x, jb.gsize, jb.p.nbg, 1.0f / dq, jb.codes);
+    else
+      quant_apply_core<DT>(blk, jb.p, 1.0f / dq, jb.codes);
+  } else {
+    // V^T tile (s tile sb, d tile db) of head bh
+    if (blk >= vt_stiles * vt_dtiles * vt.B * vt.H) return;
+    const int64_t sb = blk % vt_stiles, rest = blk / vt_stiles;
+    const int64_t db = rest % vt_dtiles, bh = rest / vt_dtiles;
+    const int64_t g = jb.per_bh ? bh : 0;
+    const float dq =
+        dequant_from_amax<DT>(block_max_u32<kQThreads>(jb.partial + g * jb.p.nbg, jb.p.nbg));
+    if (sb == 0 && db == 0 && bh == g && threadIdx.x == 0) jb.dequant[g] = dq;
+    uint32_t w[4][2];
+    apply_t_load<DT, true>(vt, 1.0f / dq, sb, db, bh, w);
+    apply_t_store(vt, w, vt8, ld, sb, db, bh, tile);
+  }
+}
+
 __global__ void selftest_e4m3_kernel(const float* x, uint8_t* out, int64_t n) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= n) return;
@@ -365,6 +408,22 @@ static int qkv_launch(const Plan& pq, const Plan& pk, const Plan& pv, const void
   hipLaunchKernelGGL(amax_multi_kernel, dim3((unsigned)amax_blocks, 3), dim3(kQThreads), 0, st,
                      jobs);
   if ((rc = check_launch("amax_multi"))) return rc;
+  const int64_t vt_stiles = ldv / 128, vt_dtiles = (D + 63) / 64;
+  const int64_t vt_blocks = vt_stiles * vt_dtiles * B * H;
+  if (max(pq.p.nbg, max(pk.p.nbg, pv.p.nbg)) <= kFoldMaxPartials &&
+      max(apply_blocks, vt_blocks) <= 0x7fffffff) {
+    QParams vt{};
+    vt.x = static_cast<const uint16_t*>(v);
+    vt.B = B; vt.H = H; vt.S = Skv; vt.D = D; vt.sb = vsb; vt.sh = vsh; vt.ss = vss;
+    const dim3 grid((unsigned)max(apply_blocks, vt_blocks), 3);
+    if (x_dtype == RP_DTYPE_F16)
+      hipLaunchKernelGGL(apply_fold_multi_kernel<kInF16>, grid, dim3(kQThreads), 0, st, jobs, vt,
+                         ldv, vt_stiles, vt_dtiles, vt8);
+    else
+      hipLaunchKernelGGL(apply_fold_multi_kernel<kInBf16>, grid, dim3(kQThreads), 0, st, jobs,
+                         vt, ldv, vt_stiles, vt_dtiles, vt8);
+    return check_launch("apply_fold_multi");
+  }
   if (x_dtype == RP_DTYPE_F16) {
     hipLaunchKernelGGL(finalize_multi_kernel<kInF16>, dim3((unsigned)ng, 3), dim3(kQThreads), 0,
                        st, jobs);

@@ -157,9 +157,8 @@ __device__ __forceinline__ void amax_flat_body(int64_t blk_id, const uint16_t* x
 
 
 template <int DT>
-__device__ __forceinline__ void quant_flat_body(int64_t blk_id, const uint16_t* x, int64_t gsize,
-                                                               int64_t nbg, const float* dequant,
-                                                               int per_bh, uint8_t* codes) {
+__device__ __forceinline__ void quant_flat_core(int64_t blk_id, const uint16_t* x, int64_t gsize,
+                                                int64_t nbg, float qm, uint8_t* codes) {
   const int64_t blk = blk_id;
   const int64_t g = blk / nbg;
   const int64_t j = blk - g * nbg;
@@ -167,7 +166,6 @@ __device__ __forceinline__ void quant_flat_body(int64_t blk_id, const uint16_t* 
   const int64_t n8 = (min((int64_t)kElemsPerBlock, gsize - j * kElemsPerBlock)) / 8;
   const u32x4* src = reinterpret_cast<const u32x4*>(x + start);
   uint2* dst = reinterpret_cast<uint2*>(codes + start);
-  const float qm = 1.0f / dequant[per_bh ? g : 0];
   u32x4 v[kFlatLoads];
 #pragma unroll
   for (int i = 0; i < kFlatLoads; ++i) {
@@ -189,11 +187,19 @@ __device__ __forceinline__ void quant_flat_body(int64_t blk_id, const uint16_t* 
   }
 }
 
+template <int DT>
+__device__ __forceinline__ void quant_flat_body(int64_t blk_id, const uint16_t* x, int64_t gsize,
+                                                int64_t nbg, const float* dequant, int per_bh,
+                                                uint8_t* codes) {
+  const float qm = 1.0f / dequant[per_bh ? blk_id / nbg : 0];
+  quant_flat_core<DT>(blk_id, x, gsize, nbg, qm, codes);
+}
+
 
 // BHSD output: codes[r*D + d] for global row r = bh*S + s.
 template <int DT>
-__device__ __forceinline__ void quant_apply_body(int64_t blk_id, QParams p, const float* dequant,
-                                                                int per_bh, uint8_t* codes) {
+__device__ __forceinline__ void quant_apply_core(int64_t blk_id, QParams p, float qm,
+                                                 uint8_t* codes) {
   const int64_t blk = blk_id;
   const int64_t g = blk / p.nbg;
   const int64_t j = blk - g * p.nbg;
@@ -208,8 +214,6 @@ __device__ __forceinline__ void quant_apply_body(int64_t blk_id, QParams p, cons
   RowCursor cur;
   const int64_t r0 = g * p.rows_per_group + first + roff;
   cur.init(r0, p);
-  // group of the first row; a block never straddles groups
-  const float qm = 1.0f / dequant[per_bh ? cur.bh : 0];
   int64_t r = r0;
   for (int64_t k = roff; k < nrows; k += step) {
     // non-temporal: x is read for the last time, the codes are read once
@@ -221,6 +225,14 @@ __device__ __forceinline__ void quant_apply_body(int64_t blk_id, QParams p, cons
     cur.advance(step, p);
     r += step;
   }
+}
+
+// (a block never straddles groups; with per-(b, h) groups group g is head g)
+template <int DT>
+__device__ __forceinline__ void quant_apply_body(int64_t blk_id, QParams p, const float* dequant,
+                                                 int per_bh, uint8_t* codes) {
+  const float qm = 1.0f / dequant[per_bh ? blk_id / p.nbg : 0];
+  quant_apply_core<DT>(blk_id, p, qm, codes);
 }
 
 // BHDS output: per head, codes[(bh*D + d)*ld + s]; columns [S, ld) zeroed.

@@ -272,15 +272,19 @@ def test_fp16_zero_scale_group_matches_torch_on_the_gpu(gpu: torch.device) -> No
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("granularity", ["bh", "tensor"])
+@pytest.mark.parametrize("sq,skv", [(300, 700), (40000, 41000)], ids=["small", "large"])
 def test_scale_quantize_qkv_equals_three_calls(gpu: torch.device, dtype: torch.dtype,
-                                               granularity: str) -> None:
+                                               granularity: str, sq: int, skv: int) -> None:
     """One library call for Q, K and V (rp_fp8_scale_quantize_qkv) gives the
     same scales and codes as three rp_fp8_scale_quantize calls; K/V longer
-    than Q, and strided (permuted BSHD) inputs."""
-    g = torch.Generator().manual_seed(31)
-    q = torch.randn(2, 300, 3, 128, generator=g).mul(2).to(dtype).to(gpu).permute(0, 2, 1, 3)
-    k = torch.randn(2, 3, 700, 128, generator=g).to(dtype).to(gpu)
-    v = torch.randn(2, 700, 3, 128, generator=g).mul(0.5).to(dtype).to(gpu).permute(0, 2, 1, 3)
+    than Q, and strided (permuted BSHD) inputs.  The small shapes take the
+    two-launch path (each apply block folds its group's few amax partials
+    itself), the large ones (per tensor: 2,400+ partials) the four-launch
+    path with its own finalize launch."""
+    g = torch.Generator(device=gpu).manual_seed(31)
+    q = torch.randn(2, sq, 3, 128, generator=g, device=gpu).mul(2).to(dtype).permute(0, 2, 1, 3)
+    k = torch.randn(2, 3, skv, 128, generator=g, device=gpu).to(dtype)
+    v = torch.randn(2, skv, 3, 128, generator=g, device=gpu).mul(0.5).to(dtype).permute(0, 2, 1, 3)
     qs, q8, ks, k8, vs, vt8 = ops.scale_quantize_qkv(q, k, v, granularity)
     for (s, c), x, lay in (((qs, q8), q, "bhsd"), ((ks, k8), k, "bhsd"), ((vs, vt8), v, "bhds")):
         s2, c2 = ops.scale_quantize(x, granularity, lay)
