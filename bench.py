@@ -18,7 +18,11 @@ profiles/traffic.json, which the rocprofv3 counter runs wrote, and says so in
 per element).  ``cpu_baseline`` times the reference's own CPU attention path
 (AMXSDPAAttention: one torch SDPA call in bf16 on all host cores) on a
 bounded sample, and ``cpu_oracle`` the C restatement of the reference's FP8
-attention (the test oracle) on another.
+attention (the test oracle) on another.  Beside them, as the reference's
+scripts/bench_fp8.py reports its FP8 op: ``whole_op`` times the op as a caller
+runs it (``FP8HipAttention.__call__``, host work included) and ``sdpa_gpu``
+times torch SDPA in bf16 on the same GPU and inputs.  Step and kernel times
+are medians over the timed calls (HIP events on the launch stream).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config NAME]
 """
@@ -28,6 +32,7 @@ from __future__ import annotations
 import argparse
 import json
 import os
+import statistics
 import sys
 import tempfile
 import time
@@ -205,26 +210,34 @@ def bench_attention(args, cfg) -> dict:
         step()
     torch.cuda.synchronize()
 
-    # whole-step timing
-    t0 = torch.cuda.Event(enable_timing=True)
-    t1 = torch.cuda.Event(enable_timing=True)
+    # whole-step timing: one event between consecutive steps, so the K steps
+    # run back to back and each step's time is one interval; ms_per_step is
+    # their median, the bracketed mean is reported beside it
+    marks = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps + 1)]
     torch.cuda.synchronize()
-    t0.record(st)
-    for _ in range(args.steps):
+    marks[0].record(st)
+    for i in range(args.steps):
         step()
-    t1.record(st)
+        marks[i + 1].record(st)
     torch.cuda.synchronize()
-    ms_per_step = t0.elapsed_time(t1) / args.steps
-    log(f"[bench] {args.steps} steps: {ms_per_step:.3f} ms/step")
+    per_step = [marks[i].elapsed_time(marks[i + 1]) for i in range(args.steps)]
+    ms_per_step = statistics.median(per_step)
+    mean_ms = marks[0].elapsed_time(marks[-1]) / args.steps
+    log(f"[bench] {args.steps} steps: median {ms_per_step:.3f} ms/step (mean {mean_ms:.3f})")
 
     # per-kernel split (same stream, separate pass so the events do not perturb the above)
     evs = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps)]
     for e in evs:
         step(e)
     torch.cuda.synchronize()
-    quant_ms = sum(e[0].elapsed_time(e[1]) for e in evs) / len(evs)
-    attn_ms = sum(e[1].elapsed_time(e[2]) for e in evs) / len(evs)
-    log(f"[bench] split: quantize {quant_ms:.3f} ms, attention kernel {attn_ms:.3f} ms")
+    quant_ms = statistics.median(e[0].elapsed_time(e[1]) for e in evs)
+    attn_ms = statistics.median(e[1].elapsed_time(e[2]) for e in evs)
+    log(f"[bench] split (medians): quantize {quant_ms:.3f} ms, attention kernel {attn_ms:.3f} ms")
+
+    whole = _whole_op_timing(args, cfg, q, k, v, st)
+    sdpa = _sdpa_gpu_timing(args, cfg, q, k, v, st)
+    if whole.get("ms") and sdpa.get("ms"):
+        sdpa["speedup_of_fp8_whole_op"] = round(sdpa["ms"] / whole["ms"], 3)
 
     graph = None
     if args.graph:
@@ -239,18 +252,11 @@ def bench_attention(args, cfg) -> dict:
         torch.cuda.synchronize()
         with torch.cuda.graph(g):
             step()
-        for _ in range(args.warmup):
-            g.replay()
-        torch.cuda.synchronize()
-        t0.record(st)
-        for _ in range(args.steps):
-            g.replay()
-        t1.record(st)
-        torch.cuda.synchronize()
-        g_ms = t0.elapsed_time(t1) / args.steps
+        g_ms, _ = _time_calls(g.replay, args.steps, args.warmup, st)
         graph = {"ms_per_step": round(g_ms, 4),
                  "value": round(cfg.flops / (g_ms * 1e-3) / 1e12, 2),
-                 "note": "the step captured once with torch.cuda.graph, then replayed"}
+                 "note": "the step captured once with torch.cuda.graph, then replayed back "
+                         "to back; median replay interval"}
         log(f"[bench] graph replay: {g_ms:.4f} ms/step")
 
     tflops_step = cfg.flops / (ms_per_step * 1e-3) / 1e12
@@ -274,6 +280,10 @@ def bench_attention(args, cfg) -> dict:
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(ms_per_step, 4),
+        "ms_per_step_mean": round(mean_ms, 4),
+        "timing": ("ms_per_step and every *_ms figure: the median over the timed calls of "
+                   "HIP-event intervals on the launch stream; ms_per_step_mean: the "
+                   "bracketed region / steps"),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -306,10 +316,100 @@ def bench_attention(args, cfg) -> dict:
                      "Q, K, V: one multi-tensor amax pass + finalize + apply (V "
                      "transposed), 5 B/element"),
         },
+        "whole_op": whole,
+        "sdpa_gpu": sdpa,
         **({"graph": graph} if graph else {}),
     }
     del q, k, v, out
     return res
+
+
+def _time_calls(fn, steps: int, warmup: int, st) -> tuple[float, float]:
+    """(median ms per call from HIP events around each call, mean wall ms per
+    call over the same calls, host time included, synchronised at the end --
+    the reference's scripts/bench_fp8.py:47-76 measurement)."""
+    import torch
+
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    marks = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
+    t0 = time.perf_counter()
+    marks[0].record(st)
+    for i in range(steps):
+        fn()
+        marks[i + 1].record(st)
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) / steps * 1e3
+    return statistics.median(marks[i].elapsed_time(marks[i + 1]) for i in range(steps)), wall
+
+
+def _whole_op_timing(args, cfg, q, k, v, st) -> dict:
+    """The op as a caller runs it: ``FP8HipAttention.__call__`` -- quantize,
+    launch-configuration lookup, attention and the output allocation, host
+    work included -- on the config's inputs (QK-normalised ones for a config
+    whose processor normalises Q and K before dispatch).  The shared-prefix
+    config has no AttentionOp form (the Protocol takes no mask): it times
+    ``ops.fp8_flash_attention`` with its prefix arguments."""
+    import torch
+
+    from repercep_runtime_amd import ops
+    from repercep_runtime_amd.attention import FP8HipAttention
+    from repercep_runtime_amd.workloads import rmsnorm_heads
+
+    if cfg.rmsnorm_qk:
+        q, k = rmsnorm_heads(q), rmsnorm_heads(k)
+    if cfg.prefix is not None:
+        what = "ops.fp8_flash_attention(q, k, v, prefix_len, suffix_len)"
+        fn = lambda: ops.fp8_flash_attention(q, k, v, prefix_len=cfg.prefix,  # noqa: E731
+                                             suffix_len=cfg.suffix)
+    else:
+        op = FP8HipAttention()
+        what = "FP8HipAttention()(q, k, v" + (", causal=True)" if cfg.causal else ")")
+        fn = lambda: op(q, k, v, causal=cfg.causal)  # noqa: E731
+    ms, wall = _time_calls(fn, args.steps, args.warmup, st)
+    log(f"[bench] whole op: {ms:.4f} ms (wall {wall:.4f} ms)")
+    return {"call": what, "ms": round(ms, 4), "wall_ms": round(wall, 4),
+            "TFLOPs": round(cfg.flops / (ms * 1e-3) / 1e12, 2),
+            "note": "bf16 in, bf16 out; ms: median of event intervals, wall_ms: mean wall "
+                    "time per call, host work included"}
+
+
+def _sdpa_gpu_timing(args, cfg, q, k, v, st) -> dict:
+    """torch SDPA in bf16 on the same GPU and inputs (the reference's
+    NaiveAttention, which its bench_fp8.py sets beside the FP8 op), restricted
+    to the fused flash and memory-efficient backends: the math backend would
+    materialise the (Sq, Skv) scores of every head."""
+    import torch
+    import torch.nn.functional as F
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+
+    from repercep_runtime_amd.workloads import rmsnorm_heads
+
+    if cfg.rmsnorm_qk:
+        q, k = rmsnorm_heads(q), rmsnorm_heads(k)
+    mask = None
+    if cfg.prefix is not None:
+        # the shared-prefix candidates: query i sees the prefix, and suffix key
+        # j (kv - prefix) of its own candidate when j <= i
+        i = torch.arange(cfg.Sq, device=q.device)[:, None]
+        kv = torch.arange(cfg.Skv, device=q.device)[None, :]
+        j = kv - cfg.prefix
+        mask = (kv < cfg.prefix) | ((j >= 0) & (j // cfg.suffix == i // cfg.suffix) & (j <= i))
+    try:
+        with sdpa_kernel([SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]):
+            fn = lambda: F.scaled_dot_product_attention(  # noqa: E731
+                q, k, v, attn_mask=mask, is_causal=cfg.causal)
+            ms, wall = _time_calls(fn, args.steps, args.warmup, st)
+    except Exception as exc:  # no fused backend for this shape or mask
+        log(f"[bench] sdpa: {type(exc).__name__}: {exc}")
+        return {"ms": None, "error": f"{type(exc).__name__}: {str(exc)[:200]}"}
+    log(f"[bench] sdpa bf16: {ms:.4f} ms (wall {wall:.4f} ms)")
+    return {"call": "torch.nn.functional.scaled_dot_product_attention (bf16, flash or "
+                    "memory-efficient backend)",
+            "ms": round(ms, 4), "wall_ms": round(wall, 4),
+            "TFLOPs": round(cfg.flops / (ms * 1e-3) / 1e12, 2),
+            "torch": torch.__version__}
 
 
 def cpu_gemm_baseline(cfg, budget_s: float) -> dict:
@@ -374,9 +474,9 @@ def bench_gemm(args, cfg) -> dict:
     for e in evs:
         step(e)
     torch.cuda.synchronize()
-    step_ms = sum(e[0].elapsed_time(e[2]) for e in evs) / len(evs)
-    gemm_ms = sum(e[1].elapsed_time(e[2]) for e in evs) / len(evs)
-    quant_ms = sum(e[0].elapsed_time(e[1]) for e in evs) / len(evs)
+    step_ms = statistics.median(e[0].elapsed_time(e[2]) for e in evs)
+    gemm_ms = statistics.median(e[1].elapsed_time(e[2]) for e in evs)
+    quant_ms = statistics.median(e[0].elapsed_time(e[1]) for e in evs)
     tf = cfg.flops / (gemm_ms * 1e-3) / 1e12
     # the other B layout on the same codes: same kernel family, same output bits
     sa, a8 = ops.scale_quantize(a, "tensor", "bhsd")

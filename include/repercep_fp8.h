@@ -141,7 +141,10 @@ int rp_fp8_scale_quantize_qkv(const void* q, const void* k, const void* v, int x
  * 1.4e9-element tensors per tensor-scale, fewer with many small heads).
  * Every call on one GPU shares that GPU's array: calls that may overlap on
  * one GPU (two streams, two host threads) race and must be serialised by
- * the caller; calls in one stream are ordered. */
+ * the caller; calls in one stream are ordered.  The first call on each GPU
+ * looks up the array's device address and must be made outside graph
+ * capture (under capture it returns RP_ERR_INVALID_ARGUMENT); later calls
+ * may be captured and replayed. */
 #define RP_QKV_NOALLOC_SCRATCH_BYTES (1u << 20)
 int rp_fp8_scale_quantize_qkv_noalloc(const void* q, const void* k, const void* v, int x_dtype,
                                       int64_t B, int64_t H, int64_t Sq, int64_t Skv, int64_t D,

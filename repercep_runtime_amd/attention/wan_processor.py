@@ -66,6 +66,9 @@ def _fp8_bound_processor() -> Any | None:
                      type(exc).__name__, exc)
         return None
     processor._attention_backend = backend
+    # the backend's registered name, read by callers that check which
+    # backend a processor is bound to (reference wan_processor.py:73)
+    processor._repercep_attention_backend = diffusers_backend.REPERCEP_FP8_BACKEND_NAME
     return processor
 
 

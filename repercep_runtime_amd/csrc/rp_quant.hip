@@ -480,7 +480,10 @@ std::mutex g_scratch_mu;
 uint8_t* g_scratch_ptr[kMaxDevices];  // device address of `scratch`, per device
 
 // Device address of `scratch` on the device that runs `stream`, looked up on
-// the first call for that device (with that device current).
+// the first call for that device (with that device current).  The lookup may
+// load the code object, which a stream under graph capture must not see:
+// a first call on a device made while `stream` is capturing is refused, so
+// one call outside capture has to come first on every device.
 int scratch_for_stream(hipStream_t st, uint8_t** out) {
   int dev = -1;
   hipError_t e = st != nullptr ? hipStreamGetDevice(st, &dev) : hipGetDevice(&dev);
@@ -491,6 +494,13 @@ int scratch_for_stream(hipStream_t st, uint8_t** out) {
   }
   std::lock_guard<std::mutex> lock(g_scratch_mu);
   if (g_scratch_ptr[dev] == nullptr) {
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    if ((e = hipStreamIsCapturing(st, &cap)) != hipSuccess || cap != hipStreamCaptureStatusNone) {
+      rp_set_error("scale_quantize_qkv_noalloc: the first call on device %d must be made "
+                   "outside graph capture (it looks up the scratch address)%s%s", dev,
+                   e != hipSuccess ? ": " : "", e != hipSuccess ? hipGetErrorString(e) : "");
+      return RP_ERR_INVALID_ARGUMENT;
+    }
     int cur = -1;
     if ((e = hipGetDevice(&cur)) != hipSuccess) {
       rp_set_error("scale_quantize_qkv_noalloc: hipGetDevice: %s", hipGetErrorString(e));
@@ -502,10 +512,18 @@ int scratch_for_stream(hipStream_t st, uint8_t** out) {
     }
     void* ptr = nullptr;
     e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
-    if (cur != dev) (void)hipSetDevice(cur);
+    // give the caller back its current device; a failed restore is an error
+    // even when the lookup worked (the caller's later calls would run on the
+    // wrong device)
+    const hipError_t er = cur != dev ? hipSetDevice(cur) : hipSuccess;
     if (e != hipSuccess || ptr == nullptr) {
       rp_set_error("scale_quantize_qkv_noalloc: hipGetSymbolAddress(scratch) on device %d: %s",
                    dev, hipGetErrorString(e));
+      return RP_ERR_LAUNCH;
+    }
+    if (er != hipSuccess) {
+      rp_set_error("scale_quantize_qkv_noalloc: restoring device %d: %s", cur,
+                   hipGetErrorString(er));
       return RP_ERR_LAUNCH;
     }
     g_scratch_ptr[dev] = static_cast<uint8_t*>(ptr);

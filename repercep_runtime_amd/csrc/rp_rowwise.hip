@@ -219,8 +219,8 @@ __global__ __launch_bounds__(kRThreads) void softmax_rowquant_kernel(const uint1
   float sum = 0.0f;
   for (int64_t i = threadIdx.x; i < npair; i += kRThreads) {
     const uint32_t w = s2[i];
-    sum += __expf(score(w & 0xffffu, scale, 2 * i, lim) - m);
-    sum += __expf(score(w >> 16, scale, 2 * i + 1, lim) - m);
+    sum += expf(score(w & 0xffffu, scale, 2 * i, lim) - m);
+    sum += expf(score(w >> 16, scale, 2 * i + 1, lim) - m);
   }
   sum = block_sum(sum, red);
   // P's row maximum is bf16(1 / sum): its scales, then its codes
@@ -229,8 +229,8 @@ __global__ __launch_bounds__(kRThreads) void softmax_rowquant_kernel(const uint1
   uint8_t* dst = codes + row * ldq;
   for (int64_t i = threadIdx.x; i < npair; i += kRThreads) {
     const uint32_t w = s2[i];
-    const float p0 = bf16_round(__expf(score(w & 0xffffu, scale, 2 * i, lim) - m) / sum);
-    const float p1 = bf16_round(__expf(score(w >> 16, scale, 2 * i + 1, lim) - m) / sum);
+    const float p0 = bf16_round(expf(score(w & 0xffffu, scale, 2 * i, lim) - m) / sum);
+    const float p1 = bf16_round(expf(score(w >> 16, scale, 2 * i + 1, lim) - m) / sum);
     int pk;
     asm("v_cvt_pk_fp8_f32 %0, %1, %2" : "=v"(pk) : "v"(clamp_e4m3(p0 * qm)), "v"(clamp_e4m3(p1 * qm)));
     *reinterpret_cast<uint16_t*>(dst + 2 * i) = (uint16_t)pk;

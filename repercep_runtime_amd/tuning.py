@@ -40,7 +40,26 @@ _DEFAULT_CACHE_PATH = Path.home() / ".cache" / "repercep" / "fp8_hip_autotune.js
 
 BLOCK_M = 256
 BLOCK_N = 128
+#: Compute units of an MI355X; the count used when no GPU is visible (CPU
+#: tests, planning ahead of a launch).  On a GPU the current device's count
+#: is used, the same number the C launch plans read from the stream's device.
 NUM_CUS = 256
+
+_cus_by_device: dict[int, int] = {}
+
+
+def num_cus() -> int:
+    """Compute units of torch's current CUDA device, or ``NUM_CUS`` without one."""
+    try:
+        import torch
+    except ImportError:  # pragma: no cover - torch is a dependency
+        return NUM_CUS
+    if not torch.cuda.is_available():
+        return NUM_CUS
+    dev = torch.cuda.current_device()
+    if dev not in _cus_by_device:
+        _cus_by_device[dev] = int(torch.cuda.get_device_properties(dev).multi_processor_count)
+    return _cus_by_device[dev]
 
 #: Used when autotuning is disabled, and the first candidate of every timed
 #: search.
@@ -128,16 +147,18 @@ def autotune_disabled() -> bool:
     return os.environ.get("REPERCEP_FP8_DISABLE_AUTOTUNE", "") in ("1", "true", "on")
 
 
-def candidate_configs(B: int, H: int, Sq: int, Skv: int) -> list[dict]:
+def candidate_configs(B: int, H: int, Sq: int, Skv: int, cus: int | None = None) -> list[dict]:
     """Configurations worth timing for a shape: split counts that leave every
     range at least one key tile (as the kernel plans them: equal whole-tile
     ranges, so a request is rounded to the count it yields) and keep the grid
     within a few workgroups per compute unit.  A shape whose unsplit grid
     already covers the GPU twice gets the balanced launch alone (the plain
-    launch where its plan splits nothing: a full last round, a mask)."""
+    launch where its plan splits nothing: a full last round, a mask).
+    ``cus`` defaults to the current device's compute units (``num_cus``)."""
+    cus = num_cus() if cus is None else int(cus)
     n_kb = -(-Skv // BLOCK_N)
     work = -(-Sq // BLOCK_M) * B * H
-    if work >= 2 * NUM_CUS:
+    if work >= 2 * cus:
         return [{**FALLBACK_CONFIG, "KV_SPLITS": 0}]
     counts: list[int] = []
     for want in sorted(set(SPLIT_CHOICES) | {n_kb}):
@@ -145,7 +166,7 @@ def candidate_configs(B: int, H: int, Sq: int, Skv: int) -> list[dict]:
             continue
         tiles = -(-n_kb // want)
         s = -(-n_kb // tiles)
-        if s not in counts and (s == 1 or work * s <= 8 * NUM_CUS):
+        if s not in counts and (s == 1 or work * s <= 8 * cus):
             counts.append(s)
     return [{**FALLBACK_CONFIG, "KV_SPLITS": s} for s in counts]
 

@@ -151,24 +151,31 @@ def test_softmax_rowwise_quantize_vs_oracle(gpu: torch.device, causal: bool) -> 
         assert (gc[np.broadcast_to(j > q, gc.shape)] == 0).all()
 
 
-@pytest.mark.parametrize("shape,causal,dtype", [
-    ((1, 4, 512, 128), False, torch.bfloat16),
-    ((1, 4, 512, 128), True, torch.bfloat16),
-    ((2, 3, 256, 64), False, torch.float16),
-    ((1, 2, 384, 256), True, torch.bfloat16),
-    ((1, 2, 128, 96), False, torch.bfloat16),
+@pytest.mark.parametrize("shape,skv,causal,dtype", [
+    ((1, 4, 512, 128), None, False, torch.bfloat16),
+    ((1, 4, 512, 128), None, True, torch.bfloat16),
+    ((2, 3, 256, 64), None, False, torch.float16),
+    ((1, 2, 384, 256), None, True, torch.bfloat16),
+    ((1, 2, 128, 96), None, False, torch.bfloat16),
+    # cross shapes: the causal mask is triu(1) on (Sq, Skv), top-left aligned
+    # (fp8_scaled_mm.py:163-166), and the second GEMM runs over Skv
+    ((1, 2, 256, 128), 384, False, torch.bfloat16),
+    ((1, 2, 256, 128), 384, True, torch.bfloat16),
+    ((1, 3, 384, 64), 256, True, torch.float16),
 ])
-def test_scaled_mm_attention_vs_oracle(gpu: torch.device, shape: tuple, causal: bool,
-                                       dtype: torch.dtype) -> None:
+def test_scaled_mm_attention_vs_oracle(gpu: torch.device, shape: tuple, skv: int | None,
+                                       causal: bool, dtype: torch.dtype) -> None:
     """The whole unfused op against the oracle's restatement of
     FP8ScaledMMAttention.__call__, within BASELINE's tolerance."""
-    g = torch.Generator().manual_seed(sum(shape))
-    q, k, v = (torch.randn(*shape, generator=g).to(dtype) for _ in range(3))
+    g = torch.Generator().manual_seed(sum(shape) + (skv or 0))
+    kshape = shape if skv is None else (*shape[:2], skv, shape[3])
+    q = torch.randn(*shape, generator=g).to(dtype)
+    k, v = (torch.randn(*kshape, generator=g).to(dtype) for _ in range(2))
     out = ops.fp8_scaled_mm_attention(q.to(gpu), k.to(gpu), v.to(gpu), causal=causal)
     assert out.dtype == dtype and out.shape == shape
     ref = rowwise.scaled_mm_attention(q, k, v, causal=causal)
     st = err_stats(out.float().cpu().numpy(), ref.float().numpy())
-    print(shape, causal, dtype, st, flush=True)
+    print(shape, skv, causal, dtype, st, flush=True)
     assert st["max_abs"] <= 2e-2 and st["mean_abs"] <= 2e-3 and st["rel_mean"] <= 1e-2
 
 

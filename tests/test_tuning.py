@@ -117,6 +117,21 @@ def test_candidates_only_split_small_grids() -> None:
     assert [c["KV_SPLITS"] for c in tuning.candidate_configs(1, 1, 256, 100)] == [1]
 
 
+def test_candidates_follow_the_compute_unit_count(monkeypatch: pytest.MonkeyPatch) -> None:
+    # C1's 32 workgroups on 24 CUs: 8 splits would exceed the cap of eight
+    # workgroups per CU; on 16 CUs they are two rounds (the balanced launch)
+    assert [c["KV_SPLITS"] for c in tuning.candidate_configs(1, 8, 1024, 1024, cus=24)] == [1, 2, 4]
+    assert [c["KV_SPLITS"] for c in tuning.candidate_configs(1, 8, 1024, 1024, cus=16)] == [0]
+    # 64 workgroups: two rounds on 32 CUs (the balanced launch), not on 256
+    assert tuning.candidate_configs(1, 16, 1024, 1024, cus=32) == [
+        {**tuning.FALLBACK_CONFIG, "KV_SPLITS": 0}]
+    assert len(tuning.candidate_configs(1, 16, 1024, 1024, cus=256)) > 1
+    # the default is the current device's count
+    monkeypatch.setattr(tuning, "num_cus", lambda: 32)
+    assert tuning.candidate_configs(1, 16, 1024, 1024) == [
+        {**tuning.FALLBACK_CONFIG, "KV_SPLITS": 0}]
+
+
 def test_a_large_grid_resolves_to_the_balanced_launch_without_a_search(cache_file: Path) -> None:
     assert ops.tuned_kv_splits(C3_SELF.B, C3_SELF.H, C3_SELF.Sq, C3_SELF.Skv, C3_SELF.D) == 0
     assert ops.tuned_kv_splits(C1.B, C1.H, C1.Sq, C1.Skv, C1.D) == 1   # searched: 1 on a miss

@@ -68,6 +68,7 @@ def test_installer_sets_the_fp8_backend_on_both_experts(monkeypatch: pytest.Monk
     for t in (pipe.transformer, pipe.transformer_2):
         assert isinstance(t.processor, FakeWanAttnProcessor)
         assert t.processor._attention_backend == "repercep-backend"
+        assert t.processor._repercep_attention_backend == "repercep_fp8"
     # one processor object shared by both experts, as diffusers' setter allows
     assert pipe.transformer.processor is pipe.transformer_2.processor
 

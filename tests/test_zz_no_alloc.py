@@ -113,3 +113,50 @@ def test_noalloc_refuses_shapes_beyond_its_scratch() -> None:
         _capi.RP_SCALE_PER_BH, FAKE, FAKE, FAKE, FAKE, 128, None)
     assert rc == 1  # RP_ERR_INVALID_ARGUMENT
     assert isinstance(L.rp_fp8_scale_quantize_qkv_noalloc, ctypes._CFuncPtr)
+
+
+@pytest.mark.gpu
+def test_noalloc_replays_from_a_captured_graph() -> None:
+    """After one eager call on the device, the entry point can be captured:
+    replays with new inputs copied in between (and the program's own eager
+    work and synchronisations between replays) give the eager results bit
+    for bit every time."""
+    if not torch.cuda.is_available():
+        pytest.fail("GPU test collected on a host without a GPU")
+    dev = torch.device("cuda", 0)
+    L = _capi.lib()
+    B, H, Sq, Skv, D = 1, 3, 777, 640, 128
+    gran = _capi.RP_SCALE_PER_BH
+    q, k, v = _case(7, B, H, Sq, Skv, D, torch.bfloat16, False, dev)
+    ldv = -(-Skv // 128) * 128
+    xq, xk, xv = q.clone(), k.clone(), v.clone()    # the graph's input buffers
+    dq = torch.empty(3 * B * H, dtype=torch.float32, device=dev)
+    q8 = torch.empty(B, H, Sq, D, dtype=torch.uint8, device=dev)
+    k8 = torch.empty(B, H, Skv, D, dtype=torch.uint8, device=dev)
+    vt8 = torch.zeros(B, H, D, ldv, dtype=torch.uint8, device=dev)
+
+    def call() -> None:
+        stream = torch.cuda.current_stream(dev).cuda_stream
+        rc = L.rp_fp8_scale_quantize_qkv_noalloc(
+            xq.data_ptr(), xk.data_ptr(), xv.data_ptr(), _capi.RP_DTYPE_BF16, B, H, Sq, Skv, D,
+            *_bhsd(xq), *_bhsd(xk), *_bhsd(xv), gran, dq.data_ptr(), q8.data_ptr(),
+            k8.data_ptr(), vt8.data_ptr(), ldv, stream)
+        _capi.check(rc, "rp_fp8_scale_quantize_qkv_noalloc")
+
+    call()                       # the eager first call resolves the scratch address
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        call()
+    for seed in (11, 12, 13):
+        nq, nk, nv = _case(seed, B, H, Sq, Skv, D, torch.bfloat16, False, dev)
+        want = _run("rp_fp8_scale_quantize_qkv", nq, nk, nv, gran, workspace=True)
+        xq.copy_(nq)
+        xk.copy_(nk)
+        xv.copy_(nv)
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(dq.view(torch.int32), want[0].view(torch.int32)), seed
+        assert torch.equal(q8, want[1]), seed
+        assert torch.equal(k8, want[2]), seed
+        assert torch.equal(vt8[..., :Skv], want[3][..., :Skv]), seed
