@@ -43,6 +43,7 @@ sys.path.insert(0, str(ROOT))
 
 FP8_PEAK_TFLOPS = 5000.0  # MI355X dense FP8 MFMA, published
 HBM_PEAK_GBPS = 8000.0    # MI355X HBM3E, published
+GRAPH_CALLS = 20          # attention launches per captured graph (--graph)
 TRAFFIC_SOURCE = ("profiles/traffic.json: FETCH_SIZE + WRITE_SIZE per launch from two "
                   "rocprofv3 --pmc runs of this bench, scaled by a plain copy's readings; "
                   "not measured in this run")
@@ -186,9 +187,13 @@ def bench_attention(args, cfg) -> dict:
     else:
         ops.fp8_flash_attention(q, k, v, causal=cfg.causal, prefix_len=prefix,
                                 suffix_len=cfg.suffix, out=out, granularity=gran)
-    splits = ops.tuned_kv_splits(cfg.B, cfg.H, cfg.Sq, cfg.Skv, cfg.D, cfg.causal, prefix,
-                                 cfg.suffix) if args.kv_splits is None else args.kv_splits
-    log(f"[bench] kv_splits {splits}")
+    if args.kv_splits is not None or args.block_m is not None:
+        block_m = args.block_m or ops.BLOCK_M
+        splits = 1 if args.kv_splits is None else args.kv_splits
+    else:
+        block_m, splits = ops.tuned_launch(cfg.B, cfg.H, cfg.Sq, cfg.Skv, cfg.D, cfg.causal,
+                                           prefix, cfg.suffix)
+    log(f"[bench] block_m {block_m} kv_splits {splits}")
 
     def step(ev=None):
         if ev is not None:
@@ -201,7 +206,7 @@ def bench_attention(args, cfg) -> dict:
             ev[1].record(st)
         ops.attention_fp8(q8.view(torch.uint8), k8.view(torch.uint8), vt8.view(torch.uint8),
                           qs, ks, vs, sm, out=out, causal=cfg.causal, prefix_len=prefix,
-                          suffix_len=cfg.suffix, kv_splits=splits)
+                          suffix_len=cfg.suffix, kv_splits=splits, block_m=block_m)
         if ev is not None:
             ev[2].record(st)
 
@@ -253,10 +258,30 @@ def bench_attention(args, cfg) -> dict:
         with torch.cuda.graph(g):
             step()
         g_ms, _ = _time_calls(g.replay, args.steps, args.warmup, st)
+        # the attention launch alone: GRAPH_CALLS calls on the same codes in
+        # one graph, so one replay interval holds GRAPH_CALLS kernel times
+        qs, q8, ks, k8, vs, vt8 = ops.scale_quantize_qkv(q, k, v, gran)
+        attn = lambda: ops.attention_fp8(  # noqa: E731
+            q8.view(torch.uint8), k8.view(torch.uint8), vt8.view(torch.uint8), qs, ks, vs, sm,
+            out=out, causal=cfg.causal, prefix_len=prefix, suffix_len=cfg.suffix,
+            kv_splits=splits, block_m=block_m)
+        with torch.cuda.stream(s2):
+            attn()
+        st.wait_stream(s2)
+        torch.cuda.synchronize()
+        ga = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(ga):
+            for _ in range(GRAPH_CALLS):
+                attn()
+        ga_ms, _ = _time_calls(ga.replay, max(3, args.steps // 4), 2, st)
         graph = {"ms_per_step": round(g_ms, 4),
                  "value": round(cfg.flops / (g_ms * 1e-3) / 1e12, 2),
+                 "attention_ms_per_call": round(ga_ms / GRAPH_CALLS, 5),
                  "note": "the step captured once with torch.cuda.graph, then replayed back "
-                         "to back; median replay interval"}
+                         f"to back (median replay interval); attention_ms_per_call: a graph "
+                         f"of {GRAPH_CALLS} attention launches on the same codes, replayed, "
+                         f"per launch"}
+        log(f"[bench] graph attention: {ga_ms / GRAPH_CALLS * 1e3:.2f} us per call")
         log(f"[bench] graph replay: {g_ms:.4f} ms/step")
 
     tflops_step = cfg.flops / (ms_per_step * 1e-3) / 1e12
@@ -270,6 +295,9 @@ def bench_attention(args, cfg) -> dict:
                      if merged else "attn_fwd_kernel")
     if merged and splits == 0:   # the balanced launch clears its item counter first
         attn_launches = "attn_zero_counter_kernel + " + attn_launches
+    kernel = "attn_fwd_kernel"
+    if block_m != ops.BLOCK_M:   # the short-query launch merges its splits itself
+        kernel = attn_launches = "attn_wsplit_kernel"
     qbytes = QUANT_BYTES_PER_ELEM * cfg.quant_elems
     q_gbps = qbytes / (quant_ms * 1e-3) / 1e9
     res = {
@@ -292,16 +320,16 @@ def bench_attention(args, cfg) -> dict:
         "config": {"workload": cfg.name, "B": cfg.B, "H": cfg.H, "Sq": cfg.Sq, "Skv": cfg.Skv,
                    "D": cfg.D, "causal": cfg.causal,
                    "scale_granularity": "per tensor" if gran == "tensor" else "per (b,h)",
-                   "kv_splits": splits, "flops_per_step": cfg.flops},
+                   "block_m": block_m, "kv_splits": splits, "flops_per_step": cfg.flops},
         "roofline": {
             "bound": "mfma",
             "achieved": round(tflops_attn, 2),
             "peak": FP8_PEAK_TFLOPS,
             "unit": "TFLOP/s",
             "frac": round(tflops_attn / FP8_PEAK_TFLOPS, 4),
-            "traffic": _traffic_from_profiles("attn_fwd_kernel", cfg.name),
+            "traffic": _traffic_from_profiles(kernel, cfg.name),
             "traffic_source": TRAFFIC_SOURCE,
-            "kernel": "attn_fwd_kernel",
+            "kernel": kernel,
             "kernel_ms": round(attn_ms, 4),
             "kernel_ms_covers": attn_launches,
         },
@@ -577,6 +605,9 @@ def main() -> int:
     ap.add_argument("--b-layout", choices=("kn", "nk"), default="kn",
                     help="c4_wan_ffn_up: the weight operand as the reference's fp8_gemm takes B, "
                          "(K, N) row-major (kn), or transposed (nk); the other is timed beside it")
+    ap.add_argument("--block-m", type=int, default=None, choices=(32, 64, 128, 256),
+                    help="attention configs: force the query rows per workgroup (32, 64, 128: "
+                         "the short-query launch with its keys split over the waves)")
     ap.add_argument("--kv-splits", type=int, default=None,
                     help="attention configs: force a launch configuration (1: one key range, "
                          "0: the balanced launch, n > 1: n key splits) instead of the one the "

@@ -213,6 +213,33 @@ int rp_fp8_attn_fwd(const uint8_t* q8, const uint8_t* k8, const uint8_t* vt8, in
                     int B, int H, int Sq, int Skv, int D,
                     int mask, int prefix_len, int suffix_len, void* stream);
 
+/* Short-query variant of rp_fp8_attn_fwd: a workgroup of eight waves takes
+ * block_m (32, 64 or 128) query rows of one head and gives each 32-row group
+ * 256 / block_m waves, each a run of the key tiles
+ * (rp_fp8_attn_wsplit_plan); the workgroup merges the runs of its rows in
+ * LDS and writes the output (one launch, no workspace).  Where the 256-row
+ * blocks of rp_fp8_attn_fwd leave most of the GPU idle (few heads, short
+ * Sq: C1, the shared-prefix decode) it runs up to eight times the
+ * workgroups over a fraction of the keys each.  Numerically it is the
+ * one-range rp_fp8_attn_fwd, not a key split: a wave starts its running
+ * max from the maxima of the tiles before its run (exchanged in LDS), so
+ * every tile's P is quantized against the reference's running max
+ * (fp8_flash_attn.py:334-380); the result differs from rp_fp8_attn_fwd only
+ * by fp32 rounding.  The reference's autotune grid has BLOCK_M 64 and 128
+ * too (fp8_flash_attn.py:177-186).  D in {64, 128} (RP_ERR_UNSUPPORTED
+ * otherwise); other arguments as rp_fp8_attn_fwd. */
+int rp_fp8_attn_fwd_wsplit(const uint8_t* q8, const uint8_t* k8, const uint8_t* vt8, int64_t ldv,
+                           const float* q_scale, const float* k_scale, const float* v_scale,
+                           int scale_stride, float sm_scale, void* out, int out_dtype,
+                           int64_t osb, int64_t osh, int64_t oss,
+                           int B, int H, int Sq, int Skv, int D,
+                           int mask, int prefix_len, int suffix_len, int block_m, void* stream);
+
+/* Key tiles per wave and waves with tiles per 32-row query group that
+ * rp_fp8_attn_fwd_wsplit runs for Skv keys at block_m; exposed for tests.
+ * RP_ERR_INVALID_ARGUMENT for Skv <= 0 or another block_m. */
+int rp_fp8_attn_wsplit_plan(int Skv, int block_m, int* split_tiles, int* n_splits);
+
 /* The launch plan rp_fp8_attn_fwd / rp_fp8_attn_fwd_split use for a shape:
  * the number of consecutive query blocks (256 rows each) one workgroup
  * runs.  Above 1, the kernel streams a workgroup's blocks through one tile

@@ -45,6 +45,7 @@ EXPORTS = (
     "rp_fp8_attn_workspace_bytes",
     "rp_fp8_attn_blocks_per_workgroup",
     "rp_fp8_attn_fwd_split", "rp_fp8_attn_balanced_plan",
+    "rp_fp8_attn_fwd_wsplit", "rp_fp8_attn_wsplit_plan",
     "rp_fp8_attn_balanced_workspace_bytes", "rp_fp8_attn_fwd_balanced",
     "rp_fp8_rmsnorm_quant_workspace_bytes",
     "rp_fp8_rmsnorm_scale_quantize", "rp_fp8_rmsnorm_quant_qkv_workspace_bytes",
@@ -107,6 +108,10 @@ def _declare(L: ctypes.CDLL) -> None:
     L.rp_fp8_attn_fwd_split.restype = _int
     L.rp_fp8_attn_fwd_split.argtypes = (list(L.rp_fp8_attn_fwd.argtypes[:-1])
                                         + [_int, _vp, _sz, _vp])
+    L.rp_fp8_attn_fwd_wsplit.restype = _int
+    L.rp_fp8_attn_fwd_wsplit.argtypes = (list(L.rp_fp8_attn_fwd.argtypes[:-1]) + [_int, _vp])
+    L.rp_fp8_attn_wsplit_plan.restype = _int
+    L.rp_fp8_attn_wsplit_plan.argtypes = [_int, _int, ctypes.POINTER(_int), ctypes.POINTER(_int)]
     L.rp_fp8_attn_balanced_plan.restype = _int
     L.rp_fp8_attn_balanced_plan.argtypes = [_int] * 7 + [ctypes.POINTER(_int)] * 2
     L.rp_fp8_attn_balanced_workspace_bytes.restype = _sz

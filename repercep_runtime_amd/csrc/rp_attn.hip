@@ -1246,6 +1246,390 @@ int launch_attn(const AttnArgs& base, int out_dtype, hipStream_t st) {
   return RP_OK;
 }
 
+// ---------------------------------------------------------------------------
+// Short query ranges: keys split across the waves of one workgroup.
+//
+// A workgroup of eight waves takes QG groups of 32 query rows of one head
+// (BLOCK_M = 32 QG) and gives each group 8 / QG waves, one run of key tiles
+// each: wave s covers the tiles [s * split_tiles, (s + 1) * split_tiles) of
+// the key range (split_plan).  A wave loads its operands straight from
+// global memory into registers (K rows in the permuted S^T order, V^T rows
+// of the transposed V) -- no LDS staging, no barrier in the tile loop -- and
+// runs the per-tile arithmetic of attn_fwd_kernel (S^T = K . Q^T, base-2
+// online softmax, P = e4m3(p * 448), O^T += V^T . P^T).
+//
+// The waves of a query group reproduce the one-range algorithm, not a key
+// split: P of tile t is quantized against the running max of tiles 0..t,
+// as in the reference's loop (fp8_flash_attn.py:334-380).  Each wave first
+// takes the row maxima of its own tiles and leaves them in LDS; after a
+// workgroup barrier it starts its running max from the maximum over the
+// tiles of the waves before it, which is the reference's running max at its
+// first tile.  With one tile per wave the scores stay in registers across
+// the barrier; with more, the wave computes its S^T tiles once for their
+// maxima and again for P.  Wave s then holds tile run s's row sum l_s and
+// unnormalised O^T_s relative to its final running max m_s, and the
+// workgroup merges them in LDS: out = sum_s w_s O_s * v_scale /
+// sum_s w_s l_s with w_s = exp2(m_s - m), m = max_s m_s.  That is the
+// reference's l and acc with the rescale factors of the later tiles
+// multiplied out, up to fp32 rounding.  One launch, no workspace.  Where the
+// 256-row kernel runs a few dozen workgroups through their whole key range
+// one tile after another (C1: 32 workgroups x 8 tiles), this one runs eight
+// times as many, each wave over a fraction of the tiles.
+constexpr int kWsWaves = 8;
+
+template <int D, int QG>
+struct WsGeo {
+  static constexpr int SPLITS = kWsWaves / QG;  // tile runs (waves) per query group
+  static constexpr int KSTEPS = D / 64;
+  static constexpr int ETILES = D / 32;
+  static constexpr int OPITCH = D + 4;          // fp32 per staged O row: an odd granule count
+  static constexpr int ROWS = 32 * QG;          // query rows per workgroup
+  static constexpr int CPT = ROWS * D / 512;    // output columns per merging thread
+  static constexpr int LDS_BYTES = kWsWaves * 32 * (OPITCH * 4 + 12);
+  static_assert(D == 64 || D == 128, "head dim");
+  static_assert(QG == 1 || QG == 2 || QG == 4, "query groups");
+  static_assert(CPT % 4 == 0, "whole float4 columns");
+  static_assert(LDS_BYTES <= 160 * 1024, "LDS");
+};
+
+__device__ __forceinline__ i32x8 gload32(const uint8_t* p) {
+  const i32x4* s = reinterpret_cast<const i32x4*>(p);
+  return cat8(s[0], s[1]);
+}
+
+template <int D, int QG, int OUT>
+__global__ __launch_bounds__(512, 1)
+void attn_wsplit_kernel(AttnArgs a) {
+  using G = WsGeo<D, QG>;
+  __shared__ __attribute__((aligned(16))) float s_o[kWsWaves * 32 * G::OPITCH];
+  __shared__ float2 s_ml[kWsWaves * 32];
+  __shared__ float s_tm[kWsWaves * 32];   // row max of each wave's tiles (exp2 domain)
+
+  // work item: (head, block of ROWS query rows); the XCD-aware remap of
+  // attn_fwd_kernel puts one head's blocks on one XCD (its K/V in one L2)
+  const int w = blockIdx.x;
+  const int xcd = w & 7, k_x = w >> 3;
+  const int per = a.n_work >> 3, rem = a.n_work & 7;
+  const int L = xcd * per + min(xcd, rem) + k_x;
+  const int bh = L / a.n_qblocks, qb = L - bh * a.n_qblocks;
+  const int b = bh / a.H, h = bh - b * a.H;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int qg = wave % QG, sp = wave / QG;   // query group, tile run
+  const int lq = lane & 31, lg = lane >> 5;
+  const int q_wave0 = qb * G::ROWS + qg * 32;
+  const int q = q_wave0 + lq;
+  const int q_last = min(q_wave0 + 31, a.Sq - 1);
+
+  const uint8_t* qh = a.q + (int64_t)bh * a.Sq * D;
+  const uint8_t* kh = a.k + (int64_t)bh * a.Skv * D;
+  const uint8_t* vh = a.vt + (int64_t)bh * D * a.ldv;
+  const float q_scale = a.qs[bh * a.scale_stride];
+  const float k_scale = a.ks[bh * a.scale_stride];
+  const float v_scale = a.vs[bh * a.scale_stride];
+  // the exp2-domain score factor, as in attn_fwd_kernel
+  const float c2_raw = ((a.sm_scale * q_scale) * k_scale) * kLog2e;
+  const float c2 = c2_raw == 0.0f ? 1.17549435e-38f : c2_raw;
+
+  // this wave's tiles; under a mask, the tiles past every key its rows can
+  // see hold nothing visible and are skipped (their scores would all be
+  // -inf: they move neither the running max nor l nor O)
+  const int n_kb = (a.Skv + kBlockN - 1) / kBlockN;
+  const int t_begin = sp * a.split_tiles;
+  int t_end = min(n_kb, t_begin + a.split_tiles);
+  if (a.mask == RP_MASK_CAUSAL) t_end = min(t_end, q_last / kBlockN + 1);
+  if (a.mask == RP_MASK_SHARED_PREFIX)
+    t_end = min(t_end, (a.prefix + q_last) / kBlockN + 1);
+
+  i32x8 qop[G::KSTEPS];
+  {
+    const uint8_t* src = qh + (int64_t)min(q, a.Sq - 1) * D + 32 * lg;
+#pragma unroll
+    for (int ks = 0; ks < G::KSTEPS; ++ks) qop[ks] = gload32(src + 64 * ks);
+  }
+
+  // first key of tile j: the last tile of a ragged key range is shifted back
+  // to end at key Skv - 1, its repeats masked (attn_fwd_kernel's
+  // tile_begin); a range shorter than one tile re-reads key Skv - 1
+  auto tile_begin = [&](int j) {
+    const int kv0 = j * kBlockN;
+    return (kv0 + kBlockN > a.Skv && a.Skv >= kBlockN) ? a.Skv - kBlockN : kv0;
+  };
+  auto load_v = [&](i32x8 (&vop)[G::ETILES][2], int kbeg) __attribute__((always_inline)) {
+#pragma unroll
+    for (int e = 0; e < G::ETILES; ++e)
+#pragma unroll
+      for (int m = 0; m < 2; ++m)
+        vop[e][m] = gload32(vh + (int64_t)(32 * e + lq) * a.ldv + kbeg + 64 * m + 32 * lg);
+  };
+  // S^T of tile j with the mask applied; returns the row max of the raw
+  // dot products over the visible keys (-inf if none), combined over the
+  // lane pair that shares the row.  V^T loads of the tile go out with the K
+  // loads when `vop` is given.
+  auto scores = [&](int j, f32x16 (&s)[4], i32x8 (*vop)[G::ETILES][2])
+      __attribute__((always_inline)) -> float {
+    const int kv0 = j * kBlockN;
+    const int kbeg = tile_begin(j);
+    i32x8 kop[4][G::KSTEPS];
+#pragma unroll
+    for (int hh = 0; hh < 4; ++hh) {
+      const int key = min(kbeg + key_of(hh, lq), a.Skv - 1);
+      const uint8_t* src = kh + (int64_t)key * D + 32 * lg;
+#pragma unroll
+      for (int ks = 0; ks < G::KSTEPS; ++ks) kop[hh][ks] = gload32(src + 64 * ks);
+    }
+    if (vop) load_v(*vop, kbeg);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int ks = 0; ks < G::KSTEPS; ++ks)
+#pragma unroll
+      for (int hh = 0; hh < 4; ++hh)
+        s[hh] = mfma_32x32x64(kop[hh][ks], qop[ks], ks == 0 ? f32x16{} : s[hh]);
+    __builtin_amdgcn_sched_barrier(0);
+    bool masked = kv0 + kBlockN > a.Skv;
+    if (a.mask == RP_MASK_CAUSAL) masked |= kv0 + kBlockN - 1 > q_wave0;
+    if (a.mask == RP_MASK_SHARED_PREFIX) masked |= kv0 + kBlockN > a.prefix;
+    if (masked) {
+      const float ninf = -__builtin_inff();
+      int lo = 0, hi = a.Skv - 1;
+      if (a.mask == RP_MASK_CAUSAL) hi = min(q, hi);
+      if (a.mask == RP_MASK_SHARED_PREFIX) {
+        lo = a.prefix + q - q % a.suffix;
+        hi = min(a.prefix + q, hi);
+      }
+      const int pre_end = a.mask == RP_MASK_SHARED_PREFIX ? min(a.prefix, a.Skv) : 0;
+      const int kvl = kbeg + 32 * lg;
+      const int lo_t = lo - kvl, hi_t = hi - kvl, pe_t = pre_end - kvl, new_t = kv0 - kvl;
+#pragma unroll
+      for (int hh = 0; hh < 4; ++hh)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int o = 64 * (hh >> 1) + 16 * (hh & 1) + r;   // key - kvl
+          const int vis = (o >= new_t) & (((o >= lo_t) & (o <= hi_t)) | (o < pe_t));
+          s[hh][r] = vis ? s[hh][r] : ninf;
+        }
+    }
+    float mt[4];
+#pragma unroll
+    for (int hh = 0; hh < 4; ++hh) {
+      float x = max3f(s[hh][0], s[hh][1], s[hh][2]);
+#pragma unroll
+      for (int r = 3; r < 15; r += 2) x = max3f(x, s[hh][r], s[hh][r + 1]);
+      mt[hh] = max3f(x, s[hh][15], s[hh][15]);
+    }
+    return xhalf_max(max3f(mt[0], mt[1], max3f(mt[2], mt[3], mt[3])));
+  };
+
+  f32x16 acc[G::ETILES];
+  float m_run, l_run = 0.0f;
+  // P of a tile from its scores and raw max, the running max and the rescale
+  // of l and O^T (attn_fwd_kernel's softmax phase and P.V products); FIRST:
+  // O^T and l start here, from the first P.V product
+  auto consume = [&](f32x16 (&s)[4], float mx, const i32x8 (&vop)[G::ETILES][2],
+                     auto first_c) __attribute__((always_inline)) {
+    constexpr bool FIRST = decltype(first_c)::value;
+    const float m_new = max3f(m_run, mx * c2, mx * c2);
+    const float m_use = (m_new == -__builtin_inff()) ? 0.0f : m_new;
+    const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
+    m_run = m_new;
+    const float moff = m_use - kLog2PMax;
+    i32x8 pop[2];
+    float ps[4] = {-0.0f, -0.0f, -0.0f, -0.0f};
+#pragma unroll
+    for (int m = 0; m < 2; ++m) {
+      int pw[8];
+#pragma unroll
+      for (int wd = 0; wd < 8; ++wd) {
+        const int hh = 2 * m + (wd >> 2);
+        const int r = 4 * (wd & 3);
+        const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[hh][r + 0], c2, -moff));
+        const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[hh][r + 1], c2, -moff));
+        const float p2 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[hh][r + 2], c2, -moff));
+        const float p3 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[hh][r + 3], c2, -moff));
+        ps[wd & 3] += (p0 + p1) + (p2 + p3);
+        pw[wd] = (int)pack4_e4m3(p0, p1, p2, p3);
+      }
+      pop[m] = i32x8{pw[0], pw[1], pw[2], pw[3], pw[4], pw[5], pw[6], pw[7]};
+    }
+    const float psum = (ps[0] + ps[1]) + (ps[2] + ps[3]);
+    if constexpr (FIRST) {
+      l_run = psum;
+    } else {
+      l_run = l_run * alpha + psum;
+      if (__any(alpha != 1.0f)) {
+#pragma unroll
+        for (int e = 0; e < G::ETILES; ++e)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) acc[e][r] *= alpha;
+      }
+    }
+#pragma unroll
+    for (int m = 0; m < 2; ++m)
+#pragma unroll
+      for (int e = 0; e < G::ETILES; ++e)
+        acc[e] = mfma_32x32x64(vop[e][m], pop[m], FIRST && m == 0 ? f32x16{} : acc[e]);
+  };
+  // running max at this wave's first tile: the max over the tiles of the
+  // waves before it in its query group
+  auto prefix_max = [&]() {
+    float m = -__builtin_inff();
+    for (int s2 = 0; s2 < sp; ++s2) m = fmaxf(m, s_tm[(s2 * QG + qg) * 32 + lq]);
+    return m;
+  };
+
+  const bool has_tiles = t_begin < t_end;
+  if (a.split_tiles == 1) {
+    // one tile per wave: its scores stay in registers across the barrier
+    f32x16 s[4];
+    i32x8 vop[G::ETILES][2];
+    float mx = -__builtin_inff();
+    if (has_tiles) mx = scores(t_begin, s, &vop);
+    if (lg == 0) s_tm[wave * 32 + lq] = mx * c2;
+    __syncthreads();
+    m_run = prefix_max();
+    if (has_tiles) consume(s, mx, vop, std::true_type{});
+  } else {
+    // several tiles per wave: their maxima first, then P and O^T
+    float wm = -__builtin_inff();
+    for (int j = t_begin; j < t_end; ++j) {
+      f32x16 s[4];
+      wm = fmaxf(wm, scores(j, s, nullptr));
+    }
+    if (lg == 0) s_tm[wave * 32 + lq] = wm * c2;
+    __syncthreads();
+    m_run = prefix_max();
+    if (has_tiles) {
+      f32x16 s[4];
+      i32x8 vop[G::ETILES][2];
+      float mx = scores(t_begin, s, &vop);
+      consume(s, mx, vop, std::true_type{});
+      for (int j = t_begin + 1; j < t_end; ++j) {
+        mx = scores(j, s, nullptr);
+        load_v(vop, tile_begin(j));
+        consume(s, mx, vop, std::false_type{});
+      }
+    }
+  }
+  if (!has_tiles) {
+#pragma unroll
+    for (int e = 0; e < G::ETILES; ++e) acc[e] = f32x16{};
+  }
+
+  // ---- each wave's state into LDS: (m, l) per row, O^T as rows of fp32;
+  // waves past the plan's run count hold no tiles and write nothing
+  if (sp < a.kv_splits) {
+    const float l_split = xhalf_sum(l_run);
+    if (lg == 0) s_ml[wave * 32 + lq] = make_float2(m_run, l_split);
+    float* const o_w = s_o + (wave * 32 + lq) * G::OPITCH;
+#pragma unroll
+    for (int e = 0; e < G::ETILES; ++e)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        *reinterpret_cast<float4*>(o_w + 32 * e + 8 * i + 4 * lg) =
+            make_float4(acc[e][4 * i], acc[e][4 * i + 1], acc[e][4 * i + 2], acc[e][4 * i + 3]);
+  }
+  __syncthreads();
+
+  // ---- merge: out = sum_s w_s O_s * v_scale / sum_s w_s l_s with
+  // w_s = exp2(m_s - max_s m_s) over the waves that saw a key of the row
+  // (attn_combine_kernel's formula, runs in ascending order)
+  constexpr int TPR = D / G::CPT;             // merging threads per row
+  const int r = tid / TPR, c0 = (tid % TPR) * G::CPT;
+  const int rg = r >> 5, rl = r & 31;
+  const int nsp = a.kv_splits;   // <= SPLITS
+  float mmax = -__builtin_inff();
+#pragma unroll
+  for (int s2 = 0; s2 < G::SPLITS; ++s2) {
+    if (s2 >= nsp) break;
+    const float2 v = s_ml[(s2 * QG + rg) * 32 + rl];
+    if (v.y != 0.0f) mmax = fmaxf(mmax, v.x);
+  }
+  float l = 0.0f;
+  float o[G::CPT];
+#pragma unroll
+  for (int c = 0; c < G::CPT; ++c) o[c] = 0.0f;
+#pragma unroll
+  for (int s2 = 0; s2 < G::SPLITS; ++s2) {
+    if (s2 >= nsp) break;
+    const int ws = s2 * QG + rg;
+    const float2 v = s_ml[ws * 32 + rl];
+    const float wgt = v.y != 0.0f ? __builtin_amdgcn_exp2f(v.x - mmax) : 0.0f;
+    l += wgt * v.y;
+    const float* src = s_o + (ws * 32 + rl) * G::OPITCH + c0;
+#pragma unroll
+    for (int c = 0; c < G::CPT; c += 4) {
+      const float4 x = *reinterpret_cast<const float4*>(src + c);
+      o[c] += wgt * x.x; o[c + 1] += wgt * x.y; o[c + 2] += wgt * x.z; o[c + 3] += wgt * x.w;
+    }
+  }
+  const int qrow = qb * G::ROWS + r;
+  if (qrow < a.Sq) {
+    const float inv = v_scale / l;
+    const int64_t obase = (int64_t)b * a.osb + (int64_t)h * a.osh + (int64_t)qrow * a.oss + c0;
+#pragma unroll
+    for (int c = 0; c < G::CPT; c += 4) {
+      const float o0 = o[c] * inv, o1 = o[c + 1] * inv, o2 = o[c + 2] * inv, o3 = o[c + 3] * inv;
+      if constexpr (OUT == kOutF32) {
+        *reinterpret_cast<float4*>(static_cast<float*>(a.out) + obase + c) =
+            make_float4(o0, o1, o2, o3);
+      } else {
+        uint2 pk;
+        if constexpr (OUT == kOutF16) {
+          pk.x = pack_f16x2(o0, o1);
+          pk.y = pack_f16x2(o2, o3);
+        } else {
+          pk.x = pack_bf16x2(o0, o1);
+          pk.y = pack_bf16x2(o2, o3);
+        }
+        *reinterpret_cast<uint2*>(static_cast<uint16_t*>(a.out) + obase + c) = pk;
+      }
+    }
+  }
+}
+
+template <int D, int QG>
+int launch_wsplit(const AttnArgs& base, int out_dtype, hipStream_t st) {
+  using G = WsGeo<D, QG>;
+  AttnArgs a = base;
+  a.D = D;
+  a.n_qblocks = (a.Sq + G::ROWS - 1) / G::ROWS;
+  int split_tiles = 0, n_splits = 1;
+  split_plan(a.Skv, G::SPLITS, &split_tiles, &n_splits);
+  a.split_tiles = split_tiles;
+  a.kv_splits = n_splits;
+  const int64_t work = (int64_t)a.B * a.H * a.n_qblocks;
+  if (work > 0x7fffffff) {
+    rp_set_error("attn: grid too large");
+    return RP_ERR_UNSUPPORTED;
+  }
+  a.n_work = (int)work;
+  const dim3 grid(a.n_work), block(512);
+  const int kind = out_kind(out_dtype);
+  if (kind == kOutF32)
+    hipLaunchKernelGGL((attn_wsplit_kernel<D, QG, kOutF32>), grid, block, 0, st, a);
+  else if (kind == kOutF16)
+    hipLaunchKernelGGL((attn_wsplit_kernel<D, QG, kOutF16>), grid, block, 0, st, a);
+  else
+    hipLaunchKernelGGL((attn_wsplit_kernel<D, QG, kOutBf16>), grid, block, 0, st, a);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) {
+    rp_set_error("attn: launch failed: %s", hipGetErrorString(e));
+    return RP_ERR_LAUNCH;
+  }
+  return RP_OK;
+}
+
+template <int D>
+int launch_wsplit_rows(const AttnArgs& a, int block_m, int out_dtype, hipStream_t st) {
+  switch (block_m) {
+    case 32: return launch_wsplit<D, 1>(a, out_dtype, st);
+    case 64: return launch_wsplit<D, 2>(a, out_dtype, st);
+    default: return launch_wsplit<D, 4>(a, out_dtype, st);
+  }
+}
+
 }  // namespace
 }  // namespace rp
 
@@ -1347,6 +1731,40 @@ extern "C" int rp_fp8_attn_fwd(const uint8_t* q8, const uint8_t* k8, const uint8
                             sm_scale, out, out_dtype, osb, osh, oss, B, H, Sq, Skv, D, mask,
                             prefix_len, suffix_len);
   return rc != RP_OK ? rc : attn_run(a, D, out_dtype, stream);
+}
+
+extern "C" int rp_fp8_attn_fwd_wsplit(const uint8_t* q8, const uint8_t* k8, const uint8_t* vt8,
+                                      int64_t ldv, const float* q_scale, const float* k_scale,
+                                      const float* v_scale, int scale_stride, float sm_scale,
+                                      void* out, int out_dtype, int64_t osb, int64_t osh,
+                                      int64_t oss, int B, int H, int Sq, int Skv, int D, int mask,
+                                      int prefix_len, int suffix_len, int block_m, void* stream) {
+  AttnArgs a;
+  const int rc = attn_setup(a, q8, k8, vt8, ldv, q_scale, k_scale, v_scale, scale_stride,
+                            sm_scale, out, out_dtype, osb, osh, oss, B, H, Sq, Skv, D, mask,
+                            prefix_len, suffix_len);
+  if (rc != RP_OK) return rc;
+  if (block_m != 32 && block_m != 64 && block_m != 128) {
+    rp_set_error("attn wave-split: block_m=%d not in {32, 64, 128}", block_m);
+    return RP_ERR_INVALID_ARGUMENT;
+  }
+  if (D != 64 && D != 128) {
+    rp_set_error("attn wave-split: head dim %d not in {64, 128}", D);
+    return RP_ERR_UNSUPPORTED;
+  }
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  return D == 64 ? launch_wsplit_rows<64>(a, block_m, out_dtype, st)
+                 : launch_wsplit_rows<128>(a, block_m, out_dtype, st);
+}
+
+extern "C" int rp_fp8_attn_wsplit_plan(int Skv, int block_m, int* split_tiles, int* n_splits) {
+  if (!split_tiles || !n_splits || Skv <= 0 ||
+      (block_m != 32 && block_m != 64 && block_m != 128)) {
+    rp_set_error("attn wave-split plan: bad arguments");
+    return RP_ERR_INVALID_ARGUMENT;
+  }
+  split_plan(Skv, kWsWaves * 32 / block_m, split_tiles, n_splits);
+  return RP_OK;
 }
 
 extern "C" int rp_fp8_attn_blocks_per_workgroup(int B, int H, int Sq, int Skv, int D, int mask,

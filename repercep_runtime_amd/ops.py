@@ -38,6 +38,10 @@ SUPPORTED_HEAD_DIMS = frozenset({32, 64, 128, 256})
 BLOCK_N = 128
 #: query rows per block of the attention kernel (one workgroup's rows)
 BLOCK_M = 256
+#: query rows per workgroup of the short-query (wave-split) launch, and the
+#: head dims it is compiled for
+WSPLIT_BLOCK_MS = (32, 64, 128)
+WSPLIT_HEAD_DIMS = frozenset({64, 128})
 #: row padding of the transposed V operand
 V_PAD = 128
 
@@ -379,11 +383,12 @@ def fp8_flash_attention_qknorm(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor
         ks, k8 = rmsnorm_scale_quantize(k, norm_k_weight, eps, rope_k, rope_layout, granularity)
         vs, vt8 = scale_quantize(v, granularity, "bhds")
     Skv = k.shape[2]
+    block_m = BLOCK_M
     if kv_splits is None:
-        kv_splits = tuned_kv_splits(B, H, Sq, Skv, D, causal)
+        block_m, kv_splits = tuned_launch(B, H, Sq, Skv, D, causal)
     return attention_fp8(q8.view(torch.uint8), k8.view(torch.uint8), vt8.view(torch.uint8),
                          qs, ks, vs, scale, out=out, out_dtype=out_dtype or q.dtype,
-                         causal=causal, kv_splits=kv_splits)
+                         causal=causal, kv_splits=kv_splits, block_m=block_m)
 
 
 def _round_up(v: int, m: int) -> int:
@@ -394,7 +399,8 @@ def attention_fp8(q8: torch.Tensor, k8: torch.Tensor, vt8: torch.Tensor, q_scale
                   k_scale: torch.Tensor, v_scale: torch.Tensor, sm_scale: float, *,
                   out: torch.Tensor | None = None, out_dtype: torch.dtype = torch.bfloat16,
                   causal: bool = False, prefix_len: int | None = None,
-                  suffix_len: int | None = None, kv_splits: int = 1) -> torch.Tensor:
+                  suffix_len: int | None = None, kv_splits: int = 1,
+                  block_m: int = BLOCK_M) -> torch.Tensor:
     """FP8 attention on already-quantized operands.
 
     q8 (B, H, Sq, D), k8 (B, H, Skv, D) contiguous codes; vt8 (B, H, D, ldv)
@@ -405,7 +411,10 @@ def attention_fp8(q8: torch.Tensor, k8: torch.Tensor, vt8: torch.Tensor, q_scale
     range in that many parts and merges them (``rp_fp8_attn_fwd_split``);
     0 runs the balanced launch (``rp_fp8_attn_fwd_balanced``): the query
     blocks that fill whole rounds of workgroups over one key range, the rest
-    key-split.
+    key-split.  ``block_m`` 32, 64 or 128 (head dims 64 and 128) runs the
+    short-query launch (``rp_fp8_attn_fwd_wsplit``): that many query rows per
+    workgroup, the keys split over its waves and merged in the same launch;
+    ``kv_splits`` must then be left at 1.
     """
     _check_cuda("q8", q8)
     _on_device_of(q8, k8=k8, vt8=vt8, q_scale=q_scale, k_scale=k_scale, v_scale=v_scale,
@@ -444,7 +453,13 @@ def attention_fp8(q8: torch.Tensor, k8: torch.Tensor, vt8: torch.Tensor, q_scale
             out.stride(1), out.stride(2), B, H, Sq, Skv, D, mask, pre, suf)
     if kv_splits < 0:
         raise ValueError(f"kv_splits={kv_splits} must be >= 0")
-    if kv_splits == 1:
+    if block_m != BLOCK_M:
+        if block_m not in WSPLIT_BLOCK_MS or kv_splits != 1:
+            raise ValueError(f"block_m={block_m} (kv_splits={kv_splits}): the short-query launch "
+                             f"takes block_m in {WSPLIT_BLOCK_MS} and kv_splits=1")
+        C.check(C.lib().rp_fp8_attn_fwd_wsplit(*args, int(block_m), _stream(q8)),
+                "rp_fp8_attn_fwd_wsplit")
+    elif kv_splits == 1:
         C.check(C.lib().rp_fp8_attn_fwd(*args, _stream(q8)), "rp_fp8_attn_fwd")
     elif kv_splits == 0:
         # whole rounds of workgroups over one key range, the query blocks of
@@ -501,16 +516,16 @@ def fp8_flash_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *,
         scale = 1.0 / math.sqrt(D)
     qs, q8, ks, k8, vs, vt8 = scale_quantize_qkv(q, k, v, granularity)
 
-    def run(splits: int) -> torch.Tensor:
+    def run(cfg: dict) -> torch.Tensor:
+        block_m, splits = launch_of(cfg)
         return attention_fp8(q8.view(torch.uint8), k8.view(torch.uint8), vt8.view(torch.uint8),
                              qs, ks, vs, scale, out=out, out_dtype=out_dtype or q.dtype,
                              causal=causal, prefix_len=prefix_len, suffix_len=suffix_len,
-                             kv_splits=splits)
+                             kv_splits=splits, block_m=block_m)
 
-    if kv_splits is None:
-        kv_splits = _resolve_kv_splits(B, H, Sq, k.shape[2], D, causal, prefix_len, suffix_len,
-                                       run)
-    return run(kv_splits)
+    if kv_splits is not None:
+        return run({"KV_SPLITS": int(kv_splits)})
+    return run(_resolve_launch(B, H, Sq, k.shape[2], D, causal, prefix_len, suffix_len, run))
 
 
 def _time_call(fn: Callable[[], object], reps: int = 10, rounds: int = 3) -> float:
@@ -531,33 +546,52 @@ def _time_call(fn: Callable[[], object], reps: int = 10, rounds: int = 3) -> flo
     return best
 
 
-def tuned_kv_splits(B: int, H: int, Sq: int, Skv: int, D: int, causal: bool = False,
-                    prefix_len: int | None = None, suffix_len: int | None = None) -> int:
-    """The split count ``fp8_flash_attention`` uses for a shape without
-    searching: the fallback when autotuning is disabled, else the cached
-    entry; on a miss the one candidate of a shape that needs no search (the
-    balanced launch of a large grid), else 1."""
+def launch_of(cfg: dict) -> tuple[int, int]:
+    """(block_m, kv_splits) ``attention_fp8`` runs for a launch configuration:
+    a ``BLOCK_M`` below 256 selects the short-query launch, whose split
+    count follows from its shape (``KV_SPLITS`` in such an entry only
+    records it)."""
+    block_m = int(cfg.get("BLOCK_M", BLOCK_M))
+    if block_m != BLOCK_M:
+        return block_m, 1
+    return block_m, int(cfg.get("KV_SPLITS", 1))
+
+
+def tuned_launch(B: int, H: int, Sq: int, Skv: int, D: int, causal: bool = False,
+                 prefix_len: int | None = None, suffix_len: int | None = None
+                 ) -> tuple[int, int]:
+    """The (block_m, kv_splits) ``fp8_flash_attention`` uses for a shape
+    without searching: the fallback when autotuning is disabled, else the
+    cached entry; on a miss the one candidate of a shape that needs no search
+    (the balanced launch of a large grid), else the fallback."""
     if tuning.autotune_disabled():
-        return int(tuning.FALLBACK_CONFIG["KV_SPLITS"])
+        return launch_of(tuning.FALLBACK_CONFIG)
     cfg = tuning.resolve_config(B, H, Sq, Skv, D, causal, prefix_len, suffix_len)
     if cfg:
-        return int(cfg.get("KV_SPLITS", 1))
-    cands = tuning.candidate_configs(B, H, Sq, Skv)
-    return int(cands[0]["KV_SPLITS"]) if len(cands) == 1 else 1
+        return launch_of(cfg)
+    cands = tuning.candidate_configs(B, H, Sq, Skv, D=D)
+    return launch_of(cands[0] if len(cands) == 1 else tuning.FALLBACK_CONFIG)
 
 
-def _resolve_kv_splits(B: int, H: int, Sq: int, Skv: int, D: int, causal: bool,
-                       prefix_len: int | None, suffix_len: int | None,
-                       run: Callable[[int], torch.Tensor]) -> int:
-    """Key split count for a shape: fallback, cache, or timed search."""
+def tuned_kv_splits(B: int, H: int, Sq: int, Skv: int, D: int, causal: bool = False,
+                    prefix_len: int | None = None, suffix_len: int | None = None) -> int:
+    """The key split count of ``tuned_launch`` (1 for a short-query launch,
+    whose splits run inside its workgroups)."""
+    return tuned_launch(B, H, Sq, Skv, D, causal, prefix_len, suffix_len)[1]
+
+
+def _resolve_launch(B: int, H: int, Sq: int, Skv: int, D: int, causal: bool,
+                    prefix_len: int | None, suffix_len: int | None,
+                    run: Callable[[dict], torch.Tensor]) -> dict:
+    """Launch configuration for a shape: fallback, cache, or timed search."""
     if tuning.autotune_disabled():
-        return tuning.FALLBACK_CONFIG["KV_SPLITS"]
+        return dict(tuning.FALLBACK_CONFIG)
     cfg = tuning.resolve_config(B, H, Sq, Skv, D, causal, prefix_len, suffix_len)
     if not cfg:
-        cands = tuning.candidate_configs(B, H, Sq, Skv)
-        cfg = tuning.autotune(cands, lambda c: _time_call(lambda: run(c["KV_SPLITS"])))
+        cands = tuning.candidate_configs(B, H, Sq, Skv, D=D)
+        cfg = tuning.autotune(cands, lambda c: _time_call(lambda: run(c)))
         tuning.record_config(B, H, Sq, Skv, D, causal, cfg, prefix_len, suffix_len)
-    return int(cfg.get("KV_SPLITS", 1))
+    return cfg
 
 
 def transpose_fp8(x8: torch.Tensor) -> torch.Tensor:

@@ -22,6 +22,13 @@ faster at the Wan shape).  Like the reference's BLOCK_N, a split moves P's
 quantization grid (each range keeps its own running max) within the FP8
 tolerance.
 
+Entries with ``BLOCK_M`` 32, 64 or 128 (and ``SPLIT_IN_WORKGROUP``) select
+the short-query launch (``rp_fp8_attn_fwd_wsplit``) for head dims 64 and
+128: that many query rows per workgroup of eight waves, each wave a run of
+the key tiles, merged in the workgroup.  Its waves exchange their tiles'
+maxima first, so it computes the one-range result (the reference's running
+max at every tile); the timed search offers it for grids of a few rounds.
+
 Entries carry the reference's four keys with the values this kernel runs,
 so they also validate under the reference's resolver (:463-471); an absent
 ``KV_SPLITS`` means 1, the way absent backend knobs mean "default" there.
@@ -68,6 +75,36 @@ FALLBACK_CONFIG = {"BLOCK_M": BLOCK_M, "BLOCK_N": BLOCK_N, "num_warps": 8, "num_
 
 _REQUIRED = ("BLOCK_M", "BLOCK_N", "num_warps", "num_stages")
 SPLIT_CHOICES = (1, 2, 4, 8, 16, 32)
+
+#: Query rows per workgroup of the short-query launch (rp_fp8_attn_fwd_wsplit:
+#: eight waves, the key tiles of each 32-row group run by 256 / BLOCK_M of
+#: them and merged in the workgroup, numerically the one-range launch) and
+#: the head dims it is built for.
+WSPLIT_BLOCK_MS = (32, 64, 128)
+WSPLIT_HEAD_DIMS = (64, 128)
+#: Its workgroups may cover the GPU this many times over.
+WSPLIT_MAX_ROUNDS = 4
+
+
+def wsplit_plan(Skv: int, block_m: int) -> tuple[int, int]:
+    """(key tiles per wave, waves with tiles) of the short-query launch: at
+    most 256 / block_m equal runs of whole 128-key tiles (rp_attn.hip
+    split_plan)."""
+    n_kb = -(-Skv // BLOCK_N)
+    want = max(1, min(8 * 32 // block_m, n_kb))
+    tiles = -(-n_kb // want)
+    return tiles, -(-n_kb // tiles)
+
+
+def wsplit_config(Skv: int, block_m: int) -> dict:
+    """The cache entry of a short-query launch.  ``num_warps`` is its eight
+    waves; ``num_stages`` keeps the reference grid's value although the
+    kernel stages nothing in LDS; ``KV_SPLITS`` records how many waves of a
+    query group run key tiles (their runs merge inside the workgroup into
+    the one-range result, so unlike a key-split launch this moves no P
+    grid)."""
+    return {"BLOCK_M": block_m, "BLOCK_N": BLOCK_N, "num_warps": 8, "num_stages": 2,
+            "KV_SPLITS": wsplit_plan(Skv, block_m)[1], "SPLIT_IN_WORKGROUP": True}
 
 
 def cache_path() -> Path:
@@ -121,12 +158,19 @@ def cache_key(B: int, H: int, Sq: int, Skv: int, D: int, causal: bool,
 
 def runnable(cfg: object) -> bool:
     """Whether this kernel can launch ``cfg`` (entries written by the
-    reference's Triton autotuner may name other tile shapes)."""
+    reference's Triton autotuner may name other tile shapes).  A short-query
+    entry (``BLOCK_M`` 32, 64 or 128) must carry ``SPLIT_IN_WORKGROUP``: a
+    Triton winner with the same tile numbers describes another kernel."""
     if not isinstance(cfg, dict) or not all(k in cfg for k in _REQUIRED):
         return False
     splits = cfg.get("KV_SPLITS", 1)
-    return (cfg["BLOCK_M"] == BLOCK_M and cfg["BLOCK_N"] == BLOCK_N
-            and isinstance(splits, int) and not isinstance(splits, bool) and splits >= 0)
+    if not (isinstance(splits, int) and not isinstance(splits, bool) and splits >= 0):
+        return False
+    if cfg["BLOCK_N"] != BLOCK_N:
+        return False
+    if cfg["BLOCK_M"] == BLOCK_M:
+        return True
+    return cfg["BLOCK_M"] in WSPLIT_BLOCK_MS and cfg.get("SPLIT_IN_WORKGROUP") is True
 
 
 def resolve_config(B: int, H: int, Sq: int, Skv: int, D: int, causal: bool,
@@ -147,14 +191,18 @@ def autotune_disabled() -> bool:
     return os.environ.get("REPERCEP_FP8_DISABLE_AUTOTUNE", "") in ("1", "true", "on")
 
 
-def candidate_configs(B: int, H: int, Sq: int, Skv: int, cus: int | None = None) -> list[dict]:
+def candidate_configs(B: int, H: int, Sq: int, Skv: int, cus: int | None = None,
+                      D: int | None = None) -> list[dict]:
     """Configurations worth timing for a shape: split counts that leave every
     range at least one key tile (as the kernel plans them: equal whole-tile
     ranges, so a request is rounded to the count it yields) and keep the grid
     within a few workgroups per compute unit.  A shape whose unsplit grid
     already covers the GPU twice gets the balanced launch alone (the plain
     launch where its plan splits nothing: a full last round, a mask).
-    ``cus`` defaults to the current device's compute units (``num_cus``)."""
+    ``cus`` defaults to the current device's compute units (``num_cus``).
+    For head dims the short-query launch is built for (``D`` given), its
+    block heights follow, those whose grid covers the GPU at most
+    ``WSPLIT_MAX_ROUNDS`` times."""
     cus = num_cus() if cus is None else int(cus)
     n_kb = -(-Skv // BLOCK_N)
     work = -(-Sq // BLOCK_M) * B * H
@@ -168,7 +216,12 @@ def candidate_configs(B: int, H: int, Sq: int, Skv: int, cus: int | None = None)
         s = -(-n_kb // tiles)
         if s not in counts and (s == 1 or work * s <= 8 * cus):
             counts.append(s)
-    return [{**FALLBACK_CONFIG, "KV_SPLITS": s} for s in counts]
+    cands = [{**FALLBACK_CONFIG, "KV_SPLITS": s} for s in counts]
+    if D in WSPLIT_HEAD_DIMS:
+        for bm in WSPLIT_BLOCK_MS:
+            if -(-Sq // bm) * B * H <= WSPLIT_MAX_ROUNDS * cus:
+                cands.append(wsplit_config(Skv, bm))
+    return cands
 
 
 #: A later (more split) candidate must beat the best earlier one by this

@@ -435,10 +435,11 @@ def test_autotune_records_and_reuses_a_split_count(gpu: torch.device, tmp_path,
     out = ops.fp8_flash_attention(qg, kg, vg, out_dtype=torch.float32).cpu().numpy()[0]
     cfg = tuning.resolve_config(1, C1.H, C1.Sq, C1.Skv, C1.D, False)
     assert cfg["KV_SPLITS"] in (1, 2, 4, 8), cfg
+    print("autotuned C1 launch:", cfg, flush=True)
     assert "B1_H8_Sq1024_Skv1024_D64_C0" in tuning.cache_load()
     # the winner depends on the box's timings: check it against the oracle of
     # its own key ranges (rp_attn.hip split_plan: equal ranges of whole tiles)
-    n = cfg["KV_SPLITS"]
+    block_m, n = ops.launch_of(cfg)   # a short-query winner computes the one-range result
     n_kb = -(-C1.Skv // 128)
     qs8, ks8, vs8 = (native.quantize_groups(bf16_bits(t), C1.H) for t in (q, k, v))
     for h in range(C1.H):
@@ -450,15 +451,19 @@ def test_autotune_records_and_reuses_a_split_count(gpu: torch.device, tmp_path,
             ref = attention.emulate_key_splits(
                 qs8[1][0, h], ks8[1][0, h], vs8[1][0, h], qs8[0][h], ks8[0][h], vs8[0][h],
                 C1.D ** -0.5, split_keys=-(-n_kb // min(n, n_kb)) * 128)
-        _check(out[h], ref, f"c1 autotuned kv_splits={n} h={h}")
+        _check(out[h], ref, f"c1 autotuned block_m={block_m} kv_splits={n} h={h}")
 
     def no_timing(*_a, **_k):
         raise AssertionError("cache hit must not time candidates")
 
     monkeypatch.setattr(ops, "_time_call", no_timing)
     again = ops.fp8_flash_attention(qg, kg, vg, out_dtype=torch.float32).cpu().numpy()[0]
-    direct = ops.fp8_flash_attention(qg, kg, vg, out_dtype=torch.float32,
-                                     kv_splits=cfg["KV_SPLITS"]).cpu().numpy()[0]
+    # the recorded launch run directly: (block_m, kv_splits) of the entry
+    qs, q8, ks, k8, vs, vt8 = ops.scale_quantize_qkv(qg, kg, vg)
+    direct = ops.attention_fp8(q8.view(torch.uint8), k8.view(torch.uint8),
+                               vt8.view(torch.uint8), qs, ks, vs, C1.D ** -0.5,
+                               out_dtype=torch.float32, kv_splits=n,
+                               block_m=block_m).cpu().numpy()[0]
     assert np.array_equal(again, direct)
 
 
@@ -809,3 +814,103 @@ def test_softmax_extremes_vs_oracle(gpu: torch.device, kind: str) -> None:
     ref, _ = _oracle_rows(q, k, v, list(range(H)), np.arange(S), sm_scale=D ** -0.5)
     # both kinds make peaked rows (one or a few dominant keys): outputs exceed 1
     _check(out, ref, f"{kind} (1, {H}, {S}, {D})", scaled=True)
+
+
+WSPLIT_CASES = [
+    # name, B, H, Sq, Skv, D, mask, prefix, suffix, block_m, in dtype, out dtype, granularity
+    ("c1_bm32", 1, 8, 1024, 1024, 64, 0, 0, 1, 32, torch.bfloat16, torch.bfloat16, "tensor"),
+    ("c1_bm64_f32", 1, 8, 1024, 1024, 64, 0, 0, 1, 64, torch.bfloat16, torch.float32, "bh"),
+    ("c1_bm128", 1, 8, 1024, 1024, 64, 0, 0, 1, 128, torch.bfloat16, torch.float32, "bh"),
+    ("c5_bm32", 1, 32, 128, 640, 128, 2, 512, 8, 32, torch.bfloat16, torch.float32, "tensor"),
+    ("c5_bm64_bf16", 1, 32, 128, 640, 128, 2, 512, 8, 64, torch.bfloat16, torch.bfloat16,
+     "tensor"),
+    # a ragged last tile, shifted back, opening the last split
+    ("causal_ragged", 1, 2, 700, 700, 128, 1, 0, 1, 32, torch.bfloat16, torch.float32, "bh"),
+    # splits wholly past a block's queries: skipped, left out of the merge
+    ("causal_kv_longer", 1, 2, 300, 1000, 64, 1, 0, 1, 64, torch.float16, torch.float16, "bh"),
+    ("cross_ragged", 2, 2, 300, 1000, 128, 0, 0, 1, 64, torch.bfloat16, torch.float32, "bh"),
+    ("short_kv", 1, 1, 100, 100, 64, 0, 0, 1, 32, torch.bfloat16, torch.float32, "bh"),
+    # 18 tiles: six splits of three tiles per wave
+    ("three_tiles_per_wave", 1, 2, 256, 2200, 128, 0, 0, 1, 32, torch.bfloat16, torch.float32,
+     "bh"),
+    ("ragged_sq", 1, 3, 77, 513, 64, 0, 0, 1, 128, torch.bfloat16, torch.float32, "bh"),
+]
+
+
+@pytest.mark.parametrize("case", WSPLIT_CASES, ids=[c[0] for c in WSPLIT_CASES])
+def test_wave_split_launch_vs_oracle(gpu: torch.device, case: tuple) -> None:
+    """rp_fp8_attn_fwd_wsplit against the one-range oracle (the reference's
+    loop over 128-key tiles): each wave starts from the running max of the
+    tiles before its run, so P is quantized on the reference's grid and the
+    usual tolerance holds, not only the key-split one; the run plan is the
+    host's (tuning.wsplit_plan); rows past Sq of a strided output are left
+    untouched."""
+    import ctypes
+
+    from oracle import quant
+    from repercep_runtime_amd import _capi, tuning
+
+    name, B, H, Sq, Skv, D, mask, prefix, suffix, bm, dt, odt, gran = case
+    st, ns = ctypes.c_int(), ctypes.c_int()
+    assert _capi.lib().rp_fp8_attn_wsplit_plan(Skv, bm, ctypes.byref(st), ctypes.byref(ns)) == 0
+    assert (st.value, ns.value) == tuning.wsplit_plan(Skv, bm)
+    g = torch.Generator().manual_seed(sum(map(ord, name)))
+    q = torch.randn(B, H, Sq, D, generator=g).to(dt)
+    k = torch.randn(B, H, Skv, D, generator=g).to(dt)
+    v = torch.randn(B, H, Skv, D, generator=g).to(dt)
+    qs, q8, ks, k8, vs, vt8 = ops.scale_quantize_qkv(q.to(gpu), k.to(gpu), v.to(gpu), gran)
+    big = torch.full((B, H, Sq + 3, D), float("nan"), dtype=odt, device=gpu)
+    out = big[:, :, :Sq]
+    ops.attention_fp8(q8.view(torch.uint8), k8.view(torch.uint8), vt8.view(torch.uint8), qs, ks,
+                      vs, D ** -0.5, out=out, causal=mask == 1,
+                      prefix_len=prefix if mask == 2 else None,
+                      suffix_len=suffix if mask == 2 else None, block_m=bm)
+    torch.cuda.synchronize()
+    assert torch.isnan(big[:, :, Sq:].float()).all(), "rows past Sq were written"
+    got = out.float().cpu().numpy()
+    for b in range(B):
+        sl = slice(b, b + 1)
+        cq, c8q = quant.quantize_codes(q[sl], gran)
+        ck, c8k = quant.quantize_codes(k[sl], gran)
+        cv, c8v = quant.quantize_codes(v[sl], gran)
+        for h in range(H):
+            si = h if gran == "bh" else 0
+            ref = native.attn_rows(c8q[0, h], c8k[0, h], c8v[0, h], cq[si], ck[si], cv[si],
+                                   D ** -0.5, np.arange(Sq), block_n=ops.BLOCK_N, mask=mask,
+                                   prefix=prefix, suffix=suffix)
+            if odt != torch.float32:
+                ref = torch.from_numpy(ref).to(odt).float().numpy()
+            _check(got[b, h], ref, f"{name} b={b} h={h} runs={ns.value}x{st.value}")
+
+
+def test_wave_split_launch_equals_one_range_launch(gpu: torch.device) -> None:
+    """Same tiles, same running maxima: the short-query launch and the
+    256-row one-range launch agree to fp32 rounding of the merge (which
+    multiplies out the rescale factors of later tiles), far inside the FP8
+    tolerance, at every block height."""
+    q, k, v = attn_inputs(C1)
+    qs, q8, ks, k8, vs, vt8 = ops.scale_quantize_qkv(q.to(gpu), k.to(gpu), v.to(gpu), "tensor")
+    args = (q8.view(torch.uint8), k8.view(torch.uint8), vt8.view(torch.uint8), qs, ks, vs,
+            C1.D ** -0.5)
+    one = ops.attention_fp8(*args, out_dtype=torch.float32).cpu().numpy()
+    for bm in ops.WSPLIT_BLOCK_MS:
+        ws = ops.attention_fp8(*args, out_dtype=torch.float32, block_m=bm).cpu().numpy()
+        st = err_stats(ws, one)
+        print(f"block_m={bm} vs the one-range launch: {st}", flush=True)
+        assert st["max_abs"] <= 1e-3 and st["rel_mean"] <= 1e-4, (bm, st)
+
+
+def test_wave_split_launch_refuses_other_shapes(gpu: torch.device) -> None:
+    """Head dims outside {64, 128} and other block heights are refused with
+    the library's message, before any launch."""
+    q8 = torch.zeros(1, 1, 128, 32, dtype=torch.uint8, device=gpu)
+    vt8 = torch.zeros(1, 1, 32, 128, dtype=torch.uint8, device=gpu)
+    one = torch.ones(1, device=gpu)
+    with pytest.raises(RuntimeError, match="head dim 32"):
+        ops.attention_fp8(q8, q8, vt8, one, one, one, 0.125, block_m=32)
+    q8 = torch.zeros(1, 1, 128, 64, dtype=torch.uint8, device=gpu)
+    vt8 = torch.zeros(1, 1, 64, 128, dtype=torch.uint8, device=gpu)
+    with pytest.raises(ValueError, match="block_m"):
+        ops.attention_fp8(q8, q8, vt8, one, one, one, 0.125, block_m=48)
+    with pytest.raises(ValueError, match="block_m"):
+        ops.attention_fp8(q8, q8, vt8, one, one, one, 0.125, block_m=64, kv_splits=2)

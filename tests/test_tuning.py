@@ -193,3 +193,48 @@ def test_cache_is_reread_when_the_file_changes(cache_file: Path) -> None:
     assert ops.tuned_kv_splits(1, 8, 8192, 8192, 128) == 4
     cache_file.unlink()
     assert ops.tuned_kv_splits(1, 8, 8192, 8192, 128) == 1        # gone: a miss
+
+
+def test_short_query_entries(cache_file: Path) -> None:
+    """Short-query launches (BLOCK_M 32/64/128, keys split over the waves):
+    candidates only for head dims 64 and 128 and grids of a few rounds, each
+    carrying the split count of its plan and the SPLIT_IN_WORKGROUP marker;
+    a reference Triton winner with the same tile numbers but no marker is
+    another kernel's entry and reads as a miss."""
+    c1 = tuning.candidate_configs(C1.B, C1.H, C1.Sq, C1.Skv, cus=256, D=C1.D)
+    ws = [c for c in c1 if c["BLOCK_M"] != 256]
+    assert [(c["BLOCK_M"], c["KV_SPLITS"]) for c in ws] == [(32, 8), (64, 4), (128, 2)]
+    assert all(c["SPLIT_IN_WORKGROUP"] is True and c["BLOCK_N"] == 128 for c in ws)
+    assert [c for c in c1 if c["BLOCK_M"] == 256][0] == tuning.FALLBACK_CONFIG
+    assert all(c["BLOCK_M"] == 256 for c in
+               tuning.candidate_configs(C1.B, C1.H, C1.Sq, C1.Skv, cus=256, D=32))
+    c5 = tuning.candidate_configs(1, C5.H, C5.Sq, C5.Skv, cus=256, D=C5.D)
+    assert [(c["BLOCK_M"], c["KV_SPLITS"]) for c in c5 if c["BLOCK_M"] != 256] == \
+        [(32, 5), (64, 3), (128, 2)]
+    # 18 key tiles over eight waves: six splits of three tiles
+    assert tuning.wsplit_plan(18 * 128, 32) == (3, 6)
+    assert tuning.wsplit_plan(100, 32) == (1, 1)
+    key = tuning.cache_key(1, 8, 1024, 1024, 64, False)
+    entry = tuning.wsplit_config(1024, 32)
+    cache_file.write_text(json.dumps({key: entry}))
+    assert tuning.resolve_config(1, 8, 1024, 1024, 64, False) == entry
+    assert ops.tuned_launch(1, 8, 1024, 1024, 64) == (32, 1)
+    assert ops.tuned_kv_splits(1, 8, 1024, 1024, 64) == 1
+    triton_128 = {"BLOCK_M": 128, "BLOCK_N": 128, "num_warps": 8, "num_stages": 2}
+    cache_file.write_text(json.dumps({key: triton_128}))
+    assert tuning.resolve_config(1, 8, 1024, 1024, 64, False) == {}
+    assert ops.launch_of({**tuning.FALLBACK_CONFIG, "KV_SPLITS": 4}) == (256, 4)
+
+
+def test_short_query_plan_matches_the_library() -> None:
+    import ctypes
+
+    L = _capi.lib()
+    for skv in (1, 100, 128, 129, 640, 1024, 1000, 2200, 8192):
+        for bm in (32, 64, 128):
+            st, ns = ctypes.c_int(), ctypes.c_int()
+            assert L.rp_fp8_attn_wsplit_plan(skv, bm, ctypes.byref(st), ctypes.byref(ns)) == 0
+            assert (st.value, ns.value) == tuning.wsplit_plan(skv, bm), (skv, bm)
+    st, ns = ctypes.c_int(), ctypes.c_int()
+    assert L.rp_fp8_attn_wsplit_plan(128, 48, ctypes.byref(st), ctypes.byref(ns)) == 1
+    assert L.rp_fp8_attn_wsplit_plan(0, 32, ctypes.byref(st), ctypes.byref(ns)) == 1
