@@ -61,6 +61,8 @@
 
 #include "rp_common.h"
 
+#include <utility>
+
 namespace rp {
 namespace {
 
@@ -1254,9 +1256,14 @@ int launch_attn(const AttnArgs& base, int out_dtype, hipStream_t st) {
 // each: wave s covers the tiles [s * split_tiles, (s + 1) * split_tiles) of
 // the key range (split_plan).  A wave loads its operands straight from
 // global memory into registers (K rows in the permuted S^T order, V^T rows
-// of the transposed V) -- no LDS staging, no barrier in the tile loop -- and
+// of the transposed V) -- no barrier in the tile loop -- and
 // runs the per-tile arithmetic of attn_fwd_kernel (S^T = K . Q^T, base-2
-// online softmax, P = e4m3(p * 448), O^T += V^T . P^T).
+// online softmax, P = e4m3(p * 448), O^T += V^T . P^T).  Its K tile, then
+// its V^T tile, pass through a region of LDS of its own, filled by
+// direct-to-LDS loads of whole KiB (eight 128-byte rows per instruction) in
+// attn_fwd_kernel's padded operand layout and read back as MFMA operands:
+// loaded straight into the operand registers, every 16-byte piece of a wave
+// instruction lies in another row, and the C5 tile loads took 4 us.
 //
 // The waves of a query group reproduce the one-range algorithm, not a key
 // split: P of tile t is quantized against the running max of tiles 0..t,
@@ -1279,18 +1286,57 @@ constexpr int kWsWaves = 8;
 
 template <int D, int QG>
 struct WsGeo {
+  using T = Geo<D, D, 8>;                       // attn_fwd_kernel's tile layout in LDS
   static constexpr int SPLITS = kWsWaves / QG;  // tile runs (waves) per query group
   static constexpr int KSTEPS = D / 64;
   static constexpr int ETILES = D / 32;
   static constexpr int OPITCH = D + 4;          // fp32 per staged O row: an odd granule count
   static constexpr int ROWS = 32 * QG;          // query rows per workgroup
   static constexpr int CPT = ROWS * D / 512;    // output columns per merging thread
-  static constexpr int LDS_BYTES = kWsWaves * 32 * (OPITCH * 4 + 12);
+  // a wave's LDS region: its K tile, then its V^T tile, then its O^T rows
+  static constexpr int REGION = (T::K_BLKS > T::V_BLKS ? T::K_BLKS : T::V_BLKS) * 1024;
+  static constexpr int LDS_BYTES = kWsWaves * (REGION + 32 * 12);
   static_assert(D == 64 || D == 128, "head dim");
   static_assert(QG == 1 || QG == 2 || QG == 4, "query groups");
   static_assert(CPT % 4 == 0, "whole float4 columns");
+  static_assert(32 * OPITCH * 4 <= REGION, "O^T rows fit the region");
   static_assert(LDS_BYTES <= 160 * 1024, "LDS");
 };
+
+// x, or -inf unless O lies in [i0, i0 + w] (O - i0 <= w, unsigned): one
+// subtract, compare and select per score.  Written as asm so that each
+// compare's lane mask is consumed at once -- as C the compiler computes all
+// 64 compares of a tile first and spills their masks; O, the score's key
+// offset, is an immediate.
+template <int O>
+__device__ __forceinline__ float mask1(float x, int i0, unsigned w, float ninf) {
+  int t;
+  asm("v_sub_u32 %1, %3, %4\n\tv_cmp_le_u32 vcc, %1, %5\n\tv_cndmask_b32 %0, %2, %0, vcc"
+      : "+v"(x), "=&v"(t)
+      : "v"(ninf), "n"(O), "v"(i0), "v"(w)
+      : "vcc");
+  return x;
+}
+// the same for the union of [i0, i0 + w] and [j0, j0 + u]
+template <int O>
+__device__ __forceinline__ float mask2(float x, int i0, unsigned w, int j0, unsigned u,
+                                       float ninf) {
+  int t;
+  uint64_t m;
+  asm("v_sub_u32 %1, %4, %5\n\tv_cmp_le_u32 vcc, %1, %6\n\t"
+      "v_sub_u32 %1, %4, %7\n\tv_cmp_le_u32 %2, %1, %8\n\t"
+      "s_or_b64 vcc, vcc, %2\n\tv_cndmask_b32 %0, %3, %0, vcc"
+      : "+v"(x), "=&v"(t), "=&s"(m)
+      : "v"(ninf), "n"(O), "v"(i0), "v"(w), "v"(j0), "v"(u)
+      : "vcc");
+  return x;
+}
+// f(integral_constant<int, t>) for t = 0 .. 63, the scores of a lane in
+// register order (block t / 16, register t % 16)
+template <typename F, int... T>
+__device__ __forceinline__ void each_score(F&& f, std::integer_sequence<int, T...>) {
+  (f(std::integral_constant<int, T>{}), ...);
+}
 
 __device__ __forceinline__ i32x8 gload32(const uint8_t* p) {
   const i32x4* s = reinterpret_cast<const i32x4*>(p);
@@ -1301,7 +1347,8 @@ template <int D, int QG, int OUT>
 __global__ __launch_bounds__(512, 1)
 void attn_wsplit_kernel(AttnArgs a) {
   using G = WsGeo<D, QG>;
-  __shared__ __attribute__((aligned(16))) float s_o[kWsWaves * 32 * G::OPITCH];
+  using GT = typename G::T;
+  __shared__ __attribute__((aligned(1024))) uint8_t s_stage[kWsWaves * G::REGION];
   __shared__ float2 s_ml[kWsWaves * 32];
   __shared__ float s_tm[kWsWaves * 32];   // row max of each wave's tiles (exp2 domain)
 
@@ -1357,30 +1404,73 @@ void attn_wsplit_kernel(AttnArgs a) {
     const int kv0 = j * kBlockN;
     return (kv0 + kBlockN > a.Skv && a.Skv >= kBlockN) ? a.Skv - kBlockN : kv0;
   };
-  auto load_v = [&](i32x8 (&vop)[G::ETILES][2], int kbeg) __attribute__((always_inline)) {
+  // this wave's LDS region (byte address for the direct-to-LDS loads)
+  uint8_t* const region = s_stage + wave * G::REGION;
+  const uint32_t region_lds = (uint32_t)(uintptr_t)(lds_ptr_t)region;
+  // K tile from key kbeg into the region: LDS row 32 hh + rho holds key
+  // key_of(hh, rho), each row one pad granule longer (the pad re-loads the
+  // row's first granule; rows past Skv re-read key Skv - 1)
+  // (rolled loops: unrolled, the per-lane addresses of all blocks stay live
+  // and spill at D = 128)
+  auto stage_k = [&](int kbeg) __attribute__((always_inline)) {
+#pragma unroll 1
+    for (int b = 0; b < GT::K_BLKS; ++b) {
+      const int p = b * kWave + lane;
+      const int row = p / GT::K_GRAN, slot = p % GT::K_GRAN;
+      const int key = min(kbeg + key_of(row >> 5, row & 31), a.Skv - 1);
+      gload_lds16(kh + (int64_t)key * D + (slot < GT::KVALID ? slot : 0) * 16,
+                  region_lds + (uint32_t)b * 1024u);
+    }
+  };
+  // V^T columns [kbeg, kbeg + 128) into the region: LDS row d holds V^T row
+  // d (rows past D in the last, rounded-up KiB re-load row D - 1)
+  auto stage_v = [&](int kbeg) __attribute__((always_inline)) {
+#pragma unroll 1
+    for (int b = 0; b < GT::V_BLKS; ++b) {
+      const int p = b * kWave + lane;
+      const int d = min(p / GT::V_GRAN, D - 1), slot = p % GT::V_GRAN;
+      gload_lds16(vh + (int64_t)d * a.ldv + kbeg + (slot < kBlockN / 16 ? slot : 0) * 16,
+                  region_lds + (uint32_t)b * 1024u);
+    }
+  };
+  // the staged V^T tile as PV operands (its loads waited for)
+  auto read_v = [&](i32x8 (&vop)[G::ETILES][2]) __attribute__((always_inline)) {
+    const uint32_t vb = region_lds + (uint32_t)(lq * GT::V_PITCH + 32 * lg);
 #pragma unroll
     for (int e = 0; e < G::ETILES; ++e)
 #pragma unroll
-      for (int m = 0; m < 2; ++m)
-        vop[e][m] = gload32(vh + (int64_t)(32 * e + lq) * a.ldv + kbeg + 64 * m + 32 * lg);
+      for (int m = 0; m < 2; ++m) vop[e][m] = lds_op(vb + 32 * e * GT::V_PITCH + 64 * m);
+  };
+  // V^T of tile j into registers, once the K operands have left the region
+  auto fetch_v = [&](i32x8 (&vop)[G::ETILES][2], int kbeg) __attribute__((always_inline)) {
+    __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0): the region's K reads are done
+    stage_v(kbeg);
+    wait_vmem_all();
+    read_v(vop);
   };
   // S^T of tile j with the mask applied; returns the row max of the raw
   // dot products over the visible keys (-inf if none), combined over the
-  // lane pair that shares the row.  V^T loads of the tile go out with the K
-  // loads when `vop` is given.
-  auto scores = [&](int j, f32x16 (&s)[4], i32x8 (*vop)[G::ETILES][2])
+  // lane pair that shares the row.  With `stage_v_too` the tile's V^T loads
+  // go out into the region right after the K operands are read from it.
+  auto scores = [&](int j, f32x16 (&s)[4], bool stage_v_too)
       __attribute__((always_inline)) -> float {
     const int kv0 = j * kBlockN;
     const int kbeg = tile_begin(j);
+    stage_k(kbeg);
+    wait_vmem_all();
     i32x8 kop[4][G::KSTEPS];
+    {
+      const uint32_t kb = region_lds + (uint32_t)(lq * GT::K_PITCH + 32 * lg);
 #pragma unroll
-    for (int hh = 0; hh < 4; ++hh) {
-      const int key = min(kbeg + key_of(hh, lq), a.Skv - 1);
-      const uint8_t* src = kh + (int64_t)key * D + 32 * lg;
+      for (int hh = 0; hh < 4; ++hh)
 #pragma unroll
-      for (int ks = 0; ks < G::KSTEPS; ++ks) kop[hh][ks] = gload32(src + 64 * ks);
+        for (int ks = 0; ks < G::KSTEPS; ++ks)
+          kop[hh][ks] = lds_op(kb + 32 * hh * GT::K_PITCH + 64 * ks);
     }
-    if (vop) load_v(*vop, kbeg);
+    if (stage_v_too) {
+      __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0): K is out of the region
+      stage_v(kbeg);
+    }
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int ks = 0; ks < G::KSTEPS; ++ks)
@@ -1402,14 +1492,31 @@ void attn_wsplit_kernel(AttnArgs a) {
       const int pre_end = a.mask == RP_MASK_SHARED_PREFIX ? min(a.prefix, a.Skv) : 0;
       const int kvl = kbeg + 32 * lg;
       const int lo_t = lo - kvl, hi_t = hi - kvl, pe_t = pre_end - kvl, new_t = kv0 - kvl;
-#pragma unroll
-      for (int hh = 0; hh < 4; ++hh)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int o = 64 * (hh >> 1) + 16 * (hh & 1) + r;   // key - kvl
-          const int vis = (o >= new_t) & (((o >= lo_t) & (o <= hi_t)) | (o < pe_t));
-          s[hh][r] = vis ? s[hh][r] : ninf;
-        }
+      // the visible keys of a lane, o = key - kvl: the window [lo, hi] and
+      // the shared prefix [0, pre_end), both from the tile's first new key
+      // on; each interval [i0, i0 + w] is one unsigned compare per score
+      // (o - i0 <= w), an empty one starts past every o
+      auto interval = [](int i0, int i1, int& start, unsigned& width) {
+        start = i1 >= i0 ? i0 : (1 << 20);
+        width = i1 >= i0 ? (unsigned)(i1 - i0) : 0u;
+      };
+      int w0, p0;
+      unsigned ww, pw;
+      interval(max(lo_t, new_t), hi_t, w0, ww);
+      // score t of the lane: block hh = t / 16, register r = t % 16, key
+      // offset o = 64 (hh / 2) + 16 (hh % 2) + r
+      if (pre_end <= kv0) {   // no prefix key in the tile (wave-uniform)
+        each_score([&](auto tc) __attribute__((always_inline)) {
+          constexpr int t = decltype(tc)::value, hh = t / 16, r = t % 16;
+          s[hh][r] = mask1<64 * (hh >> 1) + 16 * (hh & 1) + r>(s[hh][r], w0, ww, ninf);
+        }, std::make_integer_sequence<int, 64>{});
+      } else {
+        interval(new_t, pe_t - 1, p0, pw);
+        each_score([&](auto tc) __attribute__((always_inline)) {
+          constexpr int t = decltype(tc)::value, hh = t / 16, r = t % 16;
+          s[hh][r] = mask2<64 * (hh >> 1) + 16 * (hh & 1) + r>(s[hh][r], w0, ww, p0, pw, ninf);
+        }, std::make_integer_sequence<int, 64>{});
+      }
     }
     float mt[4];
 #pragma unroll
@@ -1485,17 +1592,21 @@ void attn_wsplit_kernel(AttnArgs a) {
     f32x16 s[4];
     i32x8 vop[G::ETILES][2];
     float mx = -__builtin_inff();
-    if (has_tiles) mx = scores(t_begin, s, &vop);
+    if (has_tiles) mx = scores(t_begin, s, true);
     if (lg == 0) s_tm[wave * 32 + lq] = mx * c2;
     __syncthreads();
     m_run = prefix_max();
-    if (has_tiles) consume(s, mx, vop, std::true_type{});
+    if (has_tiles) {
+      wait_vmem_all();   // the V^T tile staged before the barrier
+      read_v(vop);
+      consume(s, mx, vop, std::true_type{});
+    }
   } else {
     // several tiles per wave: their maxima first, then P and O^T
     float wm = -__builtin_inff();
     for (int j = t_begin; j < t_end; ++j) {
       f32x16 s[4];
-      wm = fmaxf(wm, scores(j, s, nullptr));
+      wm = fmaxf(wm, scores(j, s, false));
     }
     if (lg == 0) s_tm[wave * 32 + lq] = wm * c2;
     __syncthreads();
@@ -1503,11 +1614,12 @@ void attn_wsplit_kernel(AttnArgs a) {
     if (has_tiles) {
       f32x16 s[4];
       i32x8 vop[G::ETILES][2];
-      float mx = scores(t_begin, s, &vop);
+      float mx = scores(t_begin, s, false);
+      fetch_v(vop, tile_begin(t_begin));
       consume(s, mx, vop, std::true_type{});
       for (int j = t_begin + 1; j < t_end; ++j) {
-        mx = scores(j, s, nullptr);
-        load_v(vop, tile_begin(j));
+        mx = scores(j, s, false);
+        fetch_v(vop, tile_begin(j));
         consume(s, mx, vop, std::false_type{});
       }
     }
@@ -1517,12 +1629,13 @@ void attn_wsplit_kernel(AttnArgs a) {
     for (int e = 0; e < G::ETILES; ++e) acc[e] = f32x16{};
   }
 
-  // ---- each wave's state into LDS: (m, l) per row, O^T as rows of fp32;
-  // waves past the plan's run count hold no tiles and write nothing
+  // ---- each wave's state into LDS: (m, l) per row, O^T as rows of fp32 in
+  // its own region (its V^T reads, earlier LDS operations of the same wave,
+  // are done first); waves past the plan's run count write nothing
   if (sp < a.kv_splits) {
     const float l_split = xhalf_sum(l_run);
     if (lg == 0) s_ml[wave * 32 + lq] = make_float2(m_run, l_split);
-    float* const o_w = s_o + (wave * 32 + lq) * G::OPITCH;
+    float* const o_w = reinterpret_cast<float*>(region) + lq * G::OPITCH;
 #pragma unroll
     for (int e = 0; e < G::ETILES; ++e)
 #pragma unroll
@@ -1557,7 +1670,8 @@ void attn_wsplit_kernel(AttnArgs a) {
     const float2 v = s_ml[ws * 32 + rl];
     const float wgt = v.y != 0.0f ? __builtin_amdgcn_exp2f(v.x - mmax) : 0.0f;
     l += wgt * v.y;
-    const float* src = s_o + (ws * 32 + rl) * G::OPITCH + c0;
+    const float* src = reinterpret_cast<const float*>(s_stage + ws * G::REGION) +
+                       rl * G::OPITCH + c0;
 #pragma unroll
     for (int c = 0; c < G::CPT; c += 4) {
       const float4 x = *reinterpret_cast<const float4*>(src + c);
