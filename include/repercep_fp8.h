@@ -249,6 +249,17 @@ int rp_fp8_attn_wsplit_plan(int Skv, int block_m, int* split_tiles, int* n_split
 int rp_fp8_attn_blocks_per_workgroup(int B, int H, int Sq, int Skv, int D, int mask,
                                      int kv_splits);
 
+/* Whether rp_fp8_attn_fwd (and the balanced entry, which then runs it)
+ * runs a shape with the head's whole K and V^T resident in LDS: unmasked,
+ * one key split, head dim 64 or 128, at most 512 (D = 128) or 1024 (D = 64)
+ * keys, and a multi-block plan above 1.  A persistent grid, one workgroup
+ * per CU, takes runs of 32-row query tasks; each wave computes a task's
+ * whole attention against the resident tiles in the reference's tile order
+ * (the same one-range result as the other launches, to fp32 rounding).
+ * No counterpart in the reference; exposed for tests and profiling.  1 or
+ * 0. */
+int rp_fp8_attn_resident_kv(int B, int H, int Sq, int Skv, int D, int mask, int kv_splits);
+
 /* Key-split variant of rp_fp8_attn_fwd: the key range is cut into
  * `kv_splits` contiguous parts of whole 128-key tiles (fewer when Skv has
  * fewer tiles), each run by its own workgroups with its own running max, and

@@ -43,7 +43,7 @@ EXPORTS = (
     "rp_fp8_scale_quantize_qkv_noalloc",
     "rp_fp8_attn_fwd",
     "rp_fp8_attn_workspace_bytes",
-    "rp_fp8_attn_blocks_per_workgroup",
+    "rp_fp8_attn_blocks_per_workgroup", "rp_fp8_attn_resident_kv",
     "rp_fp8_attn_fwd_split", "rp_fp8_attn_balanced_plan",
     "rp_fp8_attn_fwd_wsplit", "rp_fp8_attn_wsplit_plan",
     "rp_fp8_attn_balanced_workspace_bytes", "rp_fp8_attn_fwd_balanced",
@@ -103,6 +103,8 @@ def _declare(L: ctypes.CDLL) -> None:
                                   _int, _vp]
     L.rp_fp8_attn_blocks_per_workgroup.restype = _int
     L.rp_fp8_attn_blocks_per_workgroup.argtypes = [_int] * 7
+    L.rp_fp8_attn_resident_kv.restype = _int
+    L.rp_fp8_attn_resident_kv.argtypes = [_int] * 7
     L.rp_fp8_attn_workspace_bytes.restype = _sz
     L.rp_fp8_attn_workspace_bytes.argtypes = [_int, _int, _int, _int, _int]
     L.rp_fp8_attn_fwd_split.restype = _int

@@ -1177,6 +1177,10 @@ inline int out_kind(int out_dtype) {
   return out_dtype == RP_OUT_F32 ? kOutF32 : out_dtype == RP_OUT_F16 ? kOutF16 : kOutBf16;
 }
 
+inline bool kvres_applies(const AttnArgs& a, int D);
+template <int D>
+int launch_kvres(const AttnArgs& base, int out_dtype, hipStream_t st, int cus);
+
 template <int D>
 int launch_attn(const AttnArgs& base, int out_dtype, hipStream_t st) {
   const int kind = out_kind(out_dtype);
@@ -1186,6 +1190,10 @@ int launch_attn(const AttnArgs& base, int out_dtype, hipStream_t st) {
   a.dv_halves = D / kPVWidth<D>;
   a.qb_per_wg = multi_block_plan(a, D);
   a.wg_per_bh = (a.n_qblocks + a.qb_per_wg - 1) / a.qb_per_wg;
+  // a key range resident in LDS runs the persistent resident-K/V kernel
+  if constexpr (D == 64 || D == 128) {
+    if (kvres_applies(a, D)) return launch_kvres<D>(a, out_dtype, st, stream_cus(st));
+  }
   // a mixed launch: blocks [0, qb_begin) unsplit, the rest key-split
   const bool mixed = a.qb_begin > 0;
   const int64_t heads = (int64_t)a.B * a.H * a.dv_halves;
@@ -1744,6 +1752,322 @@ int launch_wsplit_rows(const AttnArgs& a, int block_m, int out_dtype, hipStream_
   }
 }
 
+
+// ---------------------------------------------------------------------------
+// Short key ranges against many queries (cross-attention: C3's 512 text
+// keys): the head's whole K and V^T resident in LDS.
+//
+// One workgroup per CU, persistent: it takes a contiguous run of the
+// launch's tasks -- 32 query rows of one head each, head-major -- loads the
+// K and V^T of each head it meets into LDS once (K rows in the S^T operand
+// order of attn_fwd_kernel, tile after tile; V^T rows d), and its eight
+// waves then take the head's tasks in turn.  A task is one wave's whole
+// attention for its 32 rows: Q^T into registers, then tile after tile S^T
+// = K . Q^T, the base-2 online softmax, P = e4m3(p * 448) and O^T += V^T .
+// P^T with the operands read from LDS, and the rows' output stored -- the
+// one-range arithmetic of attn_fwd_kernel with the tiles in the reference's
+// order (a ragged last tile masks its keys past Skv).  No barrier runs
+// inside a head's tasks, and each wave pipelines its own steps: the next
+// tile's S^T MFMAs go out between the halves of the current tile's softmax
+// (see the loop).  At C3 cross (40 heads x 75,600 queries x 512 keys) this
+// takes 0.52-0.53 ms against the multi-block launch's 0.58 ms; the same
+// kernel with the main kernel's barrier ping-pong took 0.567 ms, and
+// starting the two waves of a SIMD up to 1,500 cycles apart changed nothing.
+template <int D>
+struct KvGeo {
+  static constexpr int KSTEPS = D / 64;
+  static constexpr int ETILES = D / 32;
+  static constexpr int K_PITCH = D + 16;         // an odd number of 16-byte granules
+  static constexpr int K_GRAN = K_PITCH / 16;
+  static constexpr int MAX_TILES = D == 128 ? 4 : 8;
+  static constexpr int K_BYTES = MAX_TILES * kBlockN * K_PITCH;
+  static constexpr int V_BYTES = D * (MAX_TILES * kBlockN + 16);
+  static_assert(D == 64 || D == 128, "head dim");
+  static_assert(K_BYTES + V_BYTES <= 156 * 1024, "LDS");
+};
+
+// The output rows of one wave's 32 queries from its O^T fragments: row
+// q0 + lq gets acc * inv, written through the output strides.  The lane pair
+// (l, l + 32) holding a row swaps halves of adjacent 8-column chunks so that
+// each 16-bit store writes 16 contiguous bytes (attn_fwd_kernel's store).
+template <int DV, int OUT>
+__device__ __forceinline__ void store_o_rows(const AttnArgs& a, const f32x16 (&acc)[DV / 32],
+                                             float inv, int b, int h, int q, int lg) {
+  const bool ok = q < a.Sq;
+  const int64_t obase = (int64_t)b * a.osb + (int64_t)h * a.osh + (int64_t)q * a.oss;
+  uint2 pend = make_uint2(0u, 0u);
+#pragma unroll
+  for (int e = 0; e < DV / 32; ++e) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int d = 32 * e + 8 * i + 4 * lg;
+      const float o0 = acc[e][4 * i + 0] * inv, o1 = acc[e][4 * i + 1] * inv;
+      const float o2 = acc[e][4 * i + 2] * inv, o3 = acc[e][4 * i + 3] * inv;
+      if constexpr (OUT == kOutF32) {
+        if (ok)
+          *reinterpret_cast<float4*>(static_cast<float*>(a.out) + obase + d) =
+              make_float4(o0, o1, o2, o3);
+      } else {
+        uint2 pk;
+        if constexpr (OUT == kOutF16) {
+          pk.x = pack_f16x2(o0, o1);
+          pk.y = pack_f16x2(o2, o3);
+        } else {
+          pk.x = pack_bf16x2(o0, o1);
+          pk.y = pack_bf16x2(o2, o3);
+        }
+        if (i % 2 == 0) {
+          pend = pk;
+        } else {
+          const auto x = __builtin_amdgcn_permlane32_swap(pend.x, pk.x, false, false);
+          const auto y = __builtin_amdgcn_permlane32_swap(pend.y, pk.y, false, false);
+          const int c = 4 * e + i - 1 + lg;   // the 8-column chunk this lane now holds
+          if (ok)
+            *reinterpret_cast<uint4*>(static_cast<uint16_t*>(a.out) + obase + 8 * c) =
+                make_uint4(x[0], y[0], x[1], y[1]);
+        }
+      }
+    }
+  }
+}
+
+template <int D, int OUT>
+__global__ __launch_bounds__(512, 1)
+void attn_kvres_kernel(AttnArgs a) {
+  using G = KvGeo<D>;
+  __shared__ __attribute__((aligned(16))) uint8_t s_kv[G::K_BYTES + G::V_BYTES];
+  uint8_t* const kl = s_kv;                 // K: tile j row 32 hh + rho = key 128 j + key_of(hh, rho)
+  uint8_t* const vl = s_kv + G::K_BYTES;    // V^T: row d at d * VP
+  const uint32_t kl_lds = (uint32_t)(uintptr_t)(lds_ptr_t)kl;
+  const uint32_t vl_lds = (uint32_t)(uintptr_t)(lds_ptr_t)vl;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lq = lane & 31, lg = lane >> 5;
+  const int n_kb = (a.Skv + kBlockN - 1) / kBlockN;   // <= MAX_TILES (host-checked)
+  const int VP = n_kb * kBlockN + 16;                  // V^T LDS pitch: odd granule count
+  const int VG = VP / 16;
+  const int nq = (a.Sq + 31) / 32;                      // 32-row tasks per head
+  const int64_t ntask = (int64_t)a.B * a.H * nq;
+  const int64_t t0 = ntask * blockIdx.x / gridDim.x;
+  const int64_t t1 = ntask * (blockIdx.x + 1) / gridDim.x;
+  const float ninf = -__builtin_inff();
+
+  for (int64_t seg = t0; seg < t1;) {
+    const int bh = (int)(seg / nq);
+    const int64_t seg_end = min(t1, (int64_t)(bh + 1) * nq);
+    const int b = bh / a.H, h = bh - b * a.H;
+    const uint8_t* qh = a.q + (int64_t)bh * a.Sq * D;
+    const uint8_t* kh = a.k + (int64_t)bh * a.Skv * D;
+    const uint8_t* vh = a.vt + (int64_t)bh * D * a.ldv;
+    // ---- the head's K and V^T into LDS (keys past Skv re-read key Skv - 1,
+    // V^T columns past Skv are the zero tail of the ldv row; pad granules
+    // re-read a row's first granule)
+    const int kg = n_kb * kBlockN * G::K_GRAN;
+    for (int g = tid; g < kg; g += 512) {
+      const int row = g / G::K_GRAN, slot = g - row * G::K_GRAN;
+      const int j = row >> 7, rho = row & 127;
+      const int key = min(j * kBlockN + key_of(rho >> 5, rho & 31), a.Skv - 1);
+      const i32x4 v = *reinterpret_cast<const i32x4*>(kh + (int64_t)key * D +
+                                                      (slot < D / 16 ? slot : 0) * 16);
+      *reinterpret_cast<i32x4*>(kl + row * G::K_PITCH + slot * 16) = v;
+    }
+    for (int g = tid; g < D * VG; g += 512) {
+      const int d = g / VG, slot = g - d * VG;
+      const i32x4 v = *reinterpret_cast<const i32x4*>(vh + (int64_t)d * a.ldv +
+                                                      (slot < VG - 1 ? slot : 0) * 16);
+      *reinterpret_cast<i32x4*>(vl + d * VP + slot * 16) = v;
+    }
+    const float q_scale = a.qs[bh * a.scale_stride];
+    const float k_scale = a.ks[bh * a.scale_stride];
+    const float v_scale = a.vs[bh * a.scale_stride];
+    const float c2_raw = ((a.sm_scale * q_scale) * k_scale) * kLog2e;
+    const float c2 = c2_raw == 0.0f ? 1.17549435e-38f : c2_raw;
+    __syncthreads();
+
+    // ---- the head's tasks, wave by wave, as one stream of (task, tile)
+    // steps.  Step i computes tile j = i % n_kb of the wave's task i / n_kb:
+    // its row max, then P in two halves (score blocks 0-1, then 2-3).  The
+    // S^T MFMAs of step i + 1 go out into the score registers each half has
+    // consumed -- the first pair between the halves, the second after -- so
+    // they run under the second half's VALU work and the P.V MFMAs of step
+    // i; the wave waits on MFMA results only where the next max needs them.
+    // A task's Q^T is loaded one task ahead.
+    auto load_q = [&](i32x8 (&dst)[G::KSTEPS], int64_t task) __attribute__((always_inline)) {
+      const int qr = min((int)(task - (int64_t)bh * nq) * 32 + lq, a.Sq - 1);
+      const uint8_t* src = qh + (int64_t)qr * D + 32 * lg;
+#pragma unroll
+      for (int ks = 0; ks < G::KSTEPS; ++ks) dst[ks] = gload32(src + 64 * ks);
+    };
+    const int64_t first = seg + wave;   // the wave's tasks: first, first + 8, ...
+    const int ntw = first < seg_end ? (int)((seg_end - first + kWsWaves - 1) / kWsWaves) : 0;
+    const int nsteps = ntw * n_kb;
+    const uint32_t kb = kl_lds + (uint32_t)(lq * G::K_PITCH + 32 * lg);
+    const uint32_t vb = vl_lds + (uint32_t)(lq * VP + 32 * lg);
+    f32x16 s[4], acc[G::ETILES];
+    i32x8 qop[G::KSTEPS], qnext[G::KSTEPS];
+    // S^T MFMAs of tile jj, score blocks h0 and h0 + 1, against Q^T qq
+    auto s_pair = [&](int jj, int h0, const i32x8 (&qq)[G::KSTEPS]) __attribute__((always_inline)) {
+      i32x8 kop[2][G::KSTEPS];
+#pragma unroll
+      for (int u = 0; u < 2; ++u)
+#pragma unroll
+        for (int ks = 0; ks < G::KSTEPS; ++ks)
+          kop[u][ks] = lds_op(kb + (uint32_t)((jj * kBlockN + 32 * (h0 + u)) * G::K_PITCH + 64 * ks));
+#pragma unroll
+      for (int ks = 0; ks < G::KSTEPS; ++ks)
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+          s[h0 + u] = mfma_32x32x64(kop[u][ks], qq[ks], ks == 0 ? f32x16{} : s[h0 + u]);
+    };
+    if (nsteps > 0) {
+      load_q(qop, first);
+      // the next task's Q^T; the last task's "next" re-reads its own rows
+      load_q(qnext, ntw > 1 ? first + kWsWaves : first);
+      s_pair(0, 0, qop);
+      s_pair(0, 2, qop);
+    }
+    float m_run = -__builtin_inff(), l_run = 0.0f;
+    for (int i = 0; i < nsteps; ++i) {
+      const int t = i / n_kb, j = i - t * n_kb;
+      const bool ends_task = j == n_kb - 1;
+      const int jn = ends_task ? 0 : j + 1;    // tile of step i + 1
+      if (j == 0) m_run = -__builtin_inff();
+      // keys past Skv in a ragged last tile
+      if (j * kBlockN + kBlockN > a.Skv) {
+        // visible key offsets o = key - (128 j + 32 lg): [0, last]
+        const int last = a.Skv - 1 - j * kBlockN - 32 * lg;
+        const int i0 = last >= 0 ? 0 : (1 << 20);
+        const unsigned wd = last >= 0 ? (unsigned)last : 0u;
+        each_score([&](auto tc) __attribute__((always_inline)) {
+          constexpr int tt = decltype(tc)::value, hh = tt / 16, r = tt % 16;
+          s[hh][r] = mask1<64 * (hh >> 1) + 16 * (hh & 1) + r>(s[hh][r], i0, wd, ninf);
+        }, std::make_integer_sequence<int, 64>{});
+      }
+      float mt[4];
+#pragma unroll
+      for (int hh = 0; hh < 4; ++hh) {
+        float x = max3f(s[hh][0], s[hh][1], s[hh][2]);
+#pragma unroll
+        for (int r = 3; r < 15; r += 2) x = max3f(x, s[hh][r], s[hh][r + 1]);
+        mt[hh] = max3f(x, s[hh][15], s[hh][15]);
+      }
+      const float mx = xhalf_max(max3f(mt[0], mt[1], max3f(mt[2], mt[3], mt[3])));
+      const float m_new = max3f(m_run, mx * c2, mx * c2);
+      const float m_use = (m_new == -__builtin_inff()) ? 0.0f : m_new;
+      const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
+      m_run = m_new;
+      const float moff = m_use - kLog2PMax;
+      i32x8 pop[2];
+      float ps[4] = {-0.0f, -0.0f, -0.0f, -0.0f};
+#pragma unroll
+      for (int m = 0; m < 2; ++m) {
+        int pw[8];
+#pragma unroll
+        for (int wd = 0; wd < 8; ++wd) {
+          const int hh = 2 * m + (wd >> 2);
+          const int r = 4 * (wd & 3);
+          const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[hh][r + 0], c2, -moff));
+          const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[hh][r + 1], c2, -moff));
+          const float p2 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[hh][r + 2], c2, -moff));
+          const float p3 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[hh][r + 3], c2, -moff));
+          ps[wd & 3] += (p0 + p1) + (p2 + p3);
+          pw[wd] = (int)pack4_e4m3(p0, p1, p2, p3);
+        }
+        pop[m] = i32x8{pw[0], pw[1], pw[2], pw[3], pw[4], pw[5], pw[6], pw[7]};
+        // score blocks 2m, 2m + 1 are consumed: step i + 1's S^T into them
+        // (issued after the last step too, on valid operands, and never
+        // read: a conditional issue would keep the consumed scores live).
+        // qop is step i + 1's Q^T: at a task's last tile it takes the next
+        // task's rows before the first pair goes out.
+        if (m == 0 && ends_task) {
+#pragma unroll
+          for (int ks = 0; ks < G::KSTEPS; ++ks) qop[ks] = qnext[ks];
+          load_q(qnext, first + (int64_t)min(t + 2, ntw - 1) * kWsWaves);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        s_pair(jn, 2 * m, qop);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      const float psum = (ps[0] + ps[1]) + (ps[2] + ps[3]);
+      // P.V: V^T operands read through a ring two MFMAs ahead (all eight at
+      // once would hold 64 registers); the first tile of a task starts O^T
+      // from the product, the others rescale it first
+      constexpr int NP = 2 * G::ETILES;
+      auto vaddr = [&](int u) {
+        return vb + (uint32_t)(32 * (u % G::ETILES) * VP + j * kBlockN + 64 * (u / G::ETILES));
+      };
+      auto pv = [&](auto first_c) __attribute__((always_inline)) {
+        constexpr bool FIRST = decltype(first_c)::value;
+        i32x8 ring[3];
+        ring[0] = lds_op(vaddr(0));
+        ring[1] = lds_op(vaddr(1));
+#pragma unroll
+        for (int u = 0; u < NP; ++u) {
+          if (u + 2 < NP) ring[(u + 2) % 3] = lds_op(vaddr(u + 2));
+          const int e = u % G::ETILES, m = u / G::ETILES;
+          acc[e] = mfma_32x32x64(ring[u % 3], pop[m], FIRST && m == 0 ? f32x16{} : acc[e]);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      };
+      if (j == 0) {
+        l_run = psum;
+        pv(std::true_type{});
+      } else {
+        l_run = l_run * alpha + psum;
+        if (__any(alpha != 1.0f)) {
+#pragma unroll
+          for (int e = 0; e < G::ETILES; ++e)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[e][r] *= alpha;
+        }
+        pv(std::false_type{});
+      }
+      if (ends_task) {
+        const int64_t task = first + (int64_t)t * kWsWaves;
+        const int q = (int)(task - (int64_t)bh * nq) * 32 + lq;
+        store_o_rows<D, OUT>(a, acc, v_scale / xhalf_sum(l_run), b, h, q, lg);
+      }
+    }
+    seg = seg_end;
+    __syncthreads();   // every wave is done with this head's K/V^T
+  }
+}
+
+// Whether the plain launch runs attn_kvres_kernel: unmasked, one key range,
+// head dim 64 or 128, the key range resident in LDS, and a shape whose
+// 256-row blocks would otherwise stream through multi-block workgroups.
+inline bool kvres_applies(const AttnArgs& a, int D) {
+  if (a.mask != RP_MASK_NONE || a.kv_splits != 1 || a.qb_begin != 0) return false;
+  if (D != 64 && D != 128) return false;
+  const int n_kb = (a.Skv + kBlockN - 1) / kBlockN;
+  if (n_kb > (D == 128 ? KvGeo<128>::MAX_TILES : KvGeo<64>::MAX_TILES)) return false;
+  return multi_block_plan(a, D) > 1;
+}
+
+template <int D>
+int launch_kvres(const AttnArgs& base, int out_dtype, hipStream_t st, int cus) {
+  AttnArgs a = base;
+  a.D = D;
+  const int64_t ntask = (int64_t)a.B * a.H * ((a.Sq + 31) / 32);
+  const int64_t want = cus > 0 ? cus : kCUs;
+  const int grid = (int)(ntask < want ? ntask : want);
+  const int kind = out_kind(out_dtype);
+  if (kind == kOutF32)
+    hipLaunchKernelGGL((attn_kvres_kernel<D, kOutF32>), dim3(grid), dim3(512), 0, st, a);
+  else if (kind == kOutF16)
+    hipLaunchKernelGGL((attn_kvres_kernel<D, kOutF16>), dim3(grid), dim3(512), 0, st, a);
+  else
+    hipLaunchKernelGGL((attn_kvres_kernel<D, kOutBf16>), dim3(grid), dim3(512), 0, st, a);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) {
+    rp_set_error("attn: launch failed: %s", hipGetErrorString(e));
+    return RP_ERR_LAUNCH;
+  }
+  return RP_OK;
+}
+
 }  // namespace
 }  // namespace rp
 
@@ -1891,6 +2215,18 @@ extern "C" int rp_fp8_attn_blocks_per_workgroup(int B, int H, int Sq, int Skv, i
   a.kv_splits = n_splits;
   a.n_qblocks = (Sq + kBlockM - 1) / kBlockM;
   return multi_block_plan(a, D);
+}
+
+extern "C" int rp_fp8_attn_resident_kv(int B, int H, int Sq, int Skv, int D, int mask,
+                                       int kv_splits) {
+  if (B <= 0 || H <= 0 || Sq <= 0 || Skv <= 0 || kv_splits < 1) return 0;
+  AttnArgs a{};
+  a.B = B; a.H = H; a.Sq = Sq; a.Skv = Skv; a.mask = mask;
+  int split_tiles = 0, n_splits = 1;
+  split_plan(Skv, kv_splits, &split_tiles, &n_splits);
+  a.kv_splits = n_splits;
+  a.n_qblocks = (Sq + kBlockM - 1) / kBlockM;
+  return kvres_applies(a, D) ? 1 : 0;
 }
 
 extern "C" size_t rp_fp8_attn_workspace_bytes(int B, int H, int Sq, int D, int kv_splits) {

@@ -86,10 +86,12 @@ __device__ __forceinline__ float add_quad_xor(float v) {
 // each chunk sums its 8 squares in order, then the chunk sums combine as a
 // butterfly over the D/8 chunks (chunk q with chunk q ^ k, k = D/16 ... 1).
 // The levels k >= TPR pair chunks of one thread; the others pair lanes.
-template <int D, int U, int EPT, bool LOAD, bool STORE>
+// With PMAX, pmax[u] also gets the two 16-bit maxima of |x| over the
+// thread's elements of row u, from the packed input bits.
+template <int D, int U, int EPT, bool LOAD, bool STORE, bool PMAX = false>
 __device__ __forceinline__ void load_norm(const PParams& p, const uint16_t* const (&xrow)[U],
                                           const int64_t (&row)[U], int c, float (&x)[U][EPT],
-                                          float (&r)[U]) {
+                                          float (&r)[U], uint32_t* pmax = nullptr) {
 #pragma clang fp contract(off)
   constexpr int TPR = D / EPT;
   constexpr int NC = EPT / 8;
@@ -106,6 +108,7 @@ __device__ __forceinline__ void load_norm(const PParams& p, const uint16_t* cons
       for (int i = 0; i < 4; ++i) {
         x[u][8 * m + 2 * i] = bf16_to_f32(w4[i] & 0xffffu);
         x[u][8 * m + 2 * i + 1] = bf16_to_f32(w4[i] >> 16);
+        if constexpr (PMAX) pmax[u] = pk_max_u16(m == 0 && i == 0 ? 0u : pmax[u], w4[i] & 0x7fff7fffu);
       }
     }
   if constexpr (LOAD) {
@@ -335,23 +338,34 @@ __device__ __forceinline__ void prologue_amax_body(const PParams& p, int64_t blk
   constexpr int EPT = kAmaxEpt<ROPE>;
   uint32_t m = 0;
   if (ROPE == RP_ROPE_NONE && p.weight == nullptr) {
-    // y = bf16(x * r) is only needed for its maximum: take it from the
-    // packed bf16 pairs, two per packed 16-bit max.  A row past the range
-    // repeats a row of the range (the same maximum), so it needs no mask.
-    uint32_t m2 = 0;
+    // y = bf16(x * r) is only needed for its maximum, and for r >= 0 that is
+    // bf16(max |x| * r): the product and the rounding are monotonic in |x|.
+    // So each thread takes the maximum of its |x| from the packed input bits
+    // (two per packed 16-bit max, no unpacking) and multiplies once per row;
+    // the block's maximum over its threads is then the row's.  The one
+    // exception is r = inf (eps = 0 and every square underflowing to 0),
+    // where 0 * r is NaN while max|x| * r is not: such a row takes the
+    // maximum over its products.  A row past the range repeats a row of the
+    // range (the same maximum), so it needs no mask.
     for_rows<D, U, EPT>(p, blk, [&](const int64_t (&r)[U], const int64_t (&)[U],
                                     const int64_t (&)[U], const uint16_t* const (&xrow)[U],
                                     const bool (&)[U], int c) {
 #pragma clang fp contract(off)
       float x[U][EPT], rn[U];
-      load_norm<D, U, EPT, false, kStoreNorm<ROPE>>(p, xrow, r, c, x, rn);
+      uint32_t pm[U];
+      load_norm<D, U, EPT, false, kStoreNorm<ROPE>, true>(p, xrow, r, c, x, rn, pm);
 #pragma unroll
-      for (int u = 0; u < U; ++u)
+      for (int u = 0; u < U; ++u) {
+        // the bf16 conversion of y in every other path (v_cvt_pk_bf16_f32)
+        auto bits = [](float f) { return (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)f); };
+        const float ax = bf16_to_f32(umax32(pm[u] & 0xffffu, pm[u] >> 16));
+        m = umax32(m, bits(ax * rn[u]) & 0x7fffu);
+        if (rn[u] == __builtin_inff()) {
 #pragma unroll
-        for (int i = 0; i < EPT; i += 2)
-          m2 = pk_max_u16(m2, pk_bf16(x[u][i] * rn[u], x[u][i + 1] * rn[u]) & 0x7fff7fffu);
+          for (int i = 0; i < EPT; ++i) m = umax32(m, bits(x[u][i] * rn[u]) & 0x7fffu);
+        }
+      }
     });
-    m = umax32(m2 & 0xffffu, m2 >> 16);
   } else {
     for_rows<D, U, EPT>(p, blk, [&](const int64_t (&r)[U], const int64_t (&)[U],
                                     const int64_t (&s)[U], const uint16_t* const (&xrow)[U],

@@ -181,19 +181,29 @@ MULTI_CASES = [
     # window the Q buffer they borrow stays idle
     ("d128_wan_cross_like_bf16", 1, 40, 9000, 512, 128, torch.bfloat16, torch.bfloat16),
     ("d128_two_tiles_fp16", 1, 24, 7003, 256, 128, torch.float16, torch.float16),
+    # key ranges past what LDS holds (more than 4 tiles at D = 128, 8 at
+    # D = 64): the multi-block kernel, with its staged stores at D = 128
+    ("d128_six_tiles_bf16", 1, 24, 9000, 700, 128, torch.bfloat16, torch.bfloat16),
+    ("d128_eight_tiles_f32", 1, 16, 9000, 1024, 128, torch.bfloat16, torch.float32),
+    ("d64_nine_tiles", 1, 32, 12000, 1100, 64, torch.bfloat16, torch.bfloat16),
 ]
 
 
 @pytest.mark.parametrize("case", MULTI_CASES, ids=[c[0] for c in MULTI_CASES])
 def test_multi_block_launches_vs_oracle(gpu: torch.device, case: tuple) -> None:
     """Rows at the start, at block boundaries and at the end of workgroups'
-    block streams, against the oracle; the launch takes the multi-block path."""
+    block streams, against the oracle.  The shapes have a multi-block plan;
+    those whose keys fit LDS (head dim 64/128, up to 4 or 8 tiles) run the
+    resident-K/V kernel, the rest the multi-block kernel."""
     from oracle import quant
     from repercep_runtime_amd import _capi
 
     name, B, H, Sq, Skv, D, dtype, out_dtype = case
     per = _capi.lib().rp_fp8_attn_blocks_per_workgroup(B, H, Sq, Skv, D, 0, 1)
-    assert per > 1, f"{name}: not a multi-block launch"
+    assert per > 1, f"{name}: not a multi-block plan"
+    kvres = _capi.lib().rp_fp8_attn_resident_kv(B, H, Sq, Skv, D, 0, 1)
+    fits = D in (64, 128) and -(-Skv // 128) <= (4 if D == 128 else 8)
+    assert kvres == int(fits), name
     g = torch.Generator().manual_seed(sum(map(ord, name)))
     q = torch.randn(B, H, Sq, D, generator=g).to(dtype)
     k = torch.randn(B, H, Skv, D, generator=g).to(dtype)
@@ -511,9 +521,9 @@ def _group_scales_codes(x: torch.Tensor, heads: list[int], granularity: str
 
 
 def _wan_sample(gpu: torch.device, cfg: AttnConfig, heads: list[int], nrows: int,
-                granularity: str) -> None:
+                granularity: str, out_dtype: torch.dtype = torch.float32) -> None:
     q, k, v = attn_inputs(cfg, device=gpu)
-    out = ops.fp8_flash_attention(q, k, v, out_dtype=torch.float32, granularity=granularity)
+    out = ops.fp8_flash_attention(q, k, v, out_dtype=out_dtype, granularity=granularity)
     gq = ops.scale_quantize_qkv(q, k, v, granularity)
     torch.cuda.synchronize()
     rng = np.random.default_rng(0)
@@ -529,11 +539,13 @@ def _wan_sample(gpu: torch.device, cfg: AttnConfig, heads: list[int], nrows: int
             assert dev_s.shape == (1,) and dev_s[0] == np.float32(whole)
         else:
             assert all(dev_s[h] == np.float32(sc[i]) for h, i in zip(heads, idx))
-    got = out[0, heads][:, torch.from_numpy(rows).to(gpu)].cpu().numpy()
+    got = out[0, heads][:, torch.from_numpy(rows).to(gpu)].float().cpu().numpy()
     ref = np.stack([native.attn_rows(ora[0][1][i], ora[1][1][i], ora[2][1][i], ora[0][0][i],
                                      ora[1][0][i], ora[2][0][i], cfg.D ** -0.5, rows,
                                      block_n=ops.BLOCK_N) for i in idx])
-    _check(got, ref, f"{cfg.name} {granularity} heads {heads} rows {nrows}")
+    if out_dtype != torch.float32:   # one rounding of the fp32 result, as the reference casts
+        ref = torch.from_numpy(ref).to(out_dtype).float().numpy()
+    _check(got, ref, f"{cfg.name} {granularity} {out_dtype} heads {heads} rows {nrows}")
     assert torch.isfinite(out).all()
     del q, k, v, out, gq
     torch.cuda.empty_cache()
@@ -546,18 +558,26 @@ def test_wan_self_attention_full_shape_sampled_rows(gpu: torch.device, granulari
     _wan_sample(gpu, C3_SELF, [0, 17, 39], 128, granularity)
 
 
+@pytest.mark.parametrize("out_dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("granularity", ["bh", "tensor"])
-def test_wan_cross_attention_full_shape_sampled_rows(gpu: torch.device, granularity: str) -> None:
-    """C3 cross (Skv = 512): 512 rows x 4 heads vs oracle, both granularities."""
-    _wan_sample(gpu, C3_CROSS, [0, 5, 20, 39], 512, granularity)
+def test_wan_cross_attention_full_shape_sampled_rows(gpu: torch.device, granularity: str,
+                                                     out_dtype: torch.dtype) -> None:
+    """C3 cross (Skv = 512, the resident-K/V launch): 512 rows x 4 heads vs
+    oracle, both granularities, fp32 and the bench's bf16 output."""
+    from repercep_runtime_amd import _capi
+
+    c = C3_CROSS
+    assert _capi.lib().rp_fp8_attn_resident_kv(c.B, c.H, c.Sq, c.Skv, c.D, 0, 1) == 1
+    _wan_sample(gpu, C3_CROSS, [0, 5, 20, 39], 512, granularity, out_dtype)
 
 
-def test_wan_self_balanced_launch_full_shape(gpu: torch.device) -> None:
+@pytest.mark.parametrize("out_dtype", [torch.float32, torch.bfloat16])
+def test_wan_self_balanced_launch_full_shape(gpu: torch.device, out_dtype: torch.dtype) -> None:
     """C3 self through the launch the op resolves for it when autotuning is on
     (kv_splits=0, the balanced launch) with per-tensor scales, as the bench
-    runs it: 64 sampled rows of the unsplit query blocks against the
-    one-range oracle, 64 of the key-split tail against the split emulation
-    with the plan's count."""
+    runs it (bf16 output included): 64 sampled rows of the unsplit query
+    blocks against the one-range oracle, 64 of the key-split tail against
+    the split emulation with the plan's count."""
     import ctypes
 
     from repercep_runtime_amd import _capi
@@ -573,7 +593,7 @@ def test_wan_self_balanced_launch_full_shape(gpu: torch.device) -> None:
     if splits == 1:
         pytest.skip(f"no tail split on {cus} CUs")
     q, k, v = attn_inputs(cfg, device=gpu)
-    out = ops.fp8_flash_attention(q, k, v, out_dtype=torch.float32, granularity="tensor",
+    out = ops.fp8_flash_attention(q, k, v, out_dtype=out_dtype, granularity="tensor",
                                   kv_splits=0)
     torch.cuda.synchronize()
     heads = [0, 21, 39]
@@ -586,14 +606,17 @@ def test_wan_self_balanced_launch_full_shape(gpu: torch.device) -> None:
     split_keys = -(-n_kb // min(splits, n_kb)) * 128
     sm = cfg.D ** -0.5
     for rows, tail in ((rows_main, False), (rows_tail, True)):
-        got = out[0, heads][:, torch.from_numpy(rows).to(gpu)].cpu().numpy()
+        got = out[0, heads][:, torch.from_numpy(rows).to(gpu)].float().cpu().numpy()
         refs = []
         for h in heads:
             args = (ora[0][1][h], ora[1][1][h], ora[2][1][h], ora[0][0][h], ora[1][0][h],
                     ora[2][0][h], sm, rows)
             refs.append(attention.emulate_key_splits(*args, split_keys=split_keys) if tail
                         else native.attn_rows(*args, block_n=ops.BLOCK_N))
-        _check(got, np.stack(refs), f"c3 balanced {'tail' if tail else 'unsplit'} rows")
+        ref = np.stack(refs)
+        if out_dtype != torch.float32:
+            ref = torch.from_numpy(ref).to(out_dtype).float().numpy()
+        _check(got, ref, f"c3 balanced {out_dtype} {'tail' if tail else 'unsplit'} rows")
     assert torch.isfinite(out).all()
     del q, k, v, out
     torch.cuda.empty_cache()
