@@ -296,6 +296,10 @@ def bench_attention(args, cfg) -> dict:
     if merged and splits == 0:   # the balanced launch clears its item counter first
         attn_launches = "attn_zero_counter_kernel + " + attn_launches
     kernel = "attn_fwd_kernel"
+    if not merged and splits in (0, 1) and _capi.lib().rp_fp8_attn_resident_kv(
+            cfg.B, cfg.H, cfg.Sq, cfg.Skv, cfg.D, mask, 1):
+        # a plain launch whose key range fits LDS runs the resident-K/V kernel
+        kernel = attn_launches = "attn_kvres_kernel"
     if block_m != ops.BLOCK_M:   # the short-query launch merges its splits itself
         kernel = attn_launches = "attn_wsplit_kernel"
     qbytes = QUANT_BYTES_PER_ELEM * cfg.quant_elems
@@ -344,6 +348,7 @@ def bench_attention(args, cfg) -> dict:
                      "Q, K, V: one multi-tensor amax pass + finalize + apply (V "
                      "transposed), 5 B/element"),
         },
+        "whole_op_ms": whole.get("ms"),
         "whole_op": whole,
         "sdpa_gpu": sdpa,
         **({"graph": graph} if graph else {}),
