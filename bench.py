@@ -516,19 +516,10 @@ def bench_gemm(args, cfg) -> dict:
     a8 = a8.view(torch.uint8)
     other = torch.empty_like(out)
     run_other = lambda: ops.fp8_gemm(a8, b_other, sa, sw, b_transposed=kn, out=other)
-    for _ in range(args.warmup):
-        run_other()
-    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    t0.record(st)
-    for _ in range(args.steps):
-        run_other()
-    t1.record(st)
-    torch.cuda.synchronize()
-    other_ms = t0.elapsed_time(t1) / args.steps
+    other_ms, _ = _time_calls(run_other, args.steps, args.warmup, st)
     ops.fp8_gemm(a8, b_main, sa, sw, b_transposed=not kn, out=out)
     same = bool(torch.equal(out, other))
-    library = _library_gemm(args, cfg, a, wt8, sw, out) if args.library_gemm else None
+    library = _library_gemm(args, cfg, a, wt8, sw, out, st) if args.library_gemm else None
     return {
         "metric": "FP8 scaled GEMM TFLOP/s (Wan FFN up-projection)",
         "value": round(cfg.flops / (step_ms * 1e-3) / 1e12, 2), "unit": "TFLOP/s",
@@ -555,7 +546,7 @@ def bench_gemm(args, cfg) -> dict:
     }
 
 
-def _library_gemm(args, cfg, a, wt8, sw, out) -> dict:
+def _library_gemm(args, cfg, a, wt8, sw, out, st) -> dict:
     """Time the vendor library's FP8 GEMM (torch._scaled_mm, hipBLASLt on
     ROCm) on the same operands and scales, for comparison only; also report
     how far its bf16 output is from this build's."""
@@ -569,16 +560,11 @@ def _library_gemm(args, cfg, a, wt8, sw, out) -> dict:
     B = wt8.view(torch.float8_e4m3fn).t()
     run = lambda: torch._scaled_mm(A, B, scale_a=sa.reshape(()), scale_b=sw.reshape(()),
                                    out_dtype=torch.bfloat16)
-    for _ in range(args.warmup):
-        ref = run()
-    ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+    # the same timing as this build's kernels: median of the intervals
+    # between events recorded after each back-to-back call
+    ms, _ = _time_calls(run, args.steps, args.warmup, st)
+    ref = run()
     torch.cuda.synchronize()
-    ev[0].record()
-    for _ in range(args.steps):
-        ref = run()
-    ev[1].record()
-    torch.cuda.synchronize()
-    ms = ev[0].elapsed_time(ev[1]) / args.steps
     diff = (ref.float() - out.float()).abs()
     return {"op": "torch._scaled_mm", "ms": round(ms, 4),
             "TFLOPs": round(cfg.flops / (ms * 1e-3) / 1e12, 2),

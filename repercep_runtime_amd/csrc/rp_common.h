@@ -118,12 +118,6 @@ __device__ __forceinline__ uint32_t pk_max_u16(uint32_t a, uint32_t b) {
                                                                 __builtin_bit_cast(u16x2, b)));
 }
 
-// Two fp32 -> packed bf16, round to nearest even (v_cvt_pk_bf16_f32).
-__device__ __forceinline__ uint32_t pk_bf16(float lo, float hi) {
-  const __bf16 a = (__bf16)lo, b = (__bf16)hi;
-  return (uint32_t)__builtin_bit_cast(uint16_t, a) | ((uint32_t)__builtin_bit_cast(uint16_t, b) << 16);
-}
-
 // Max of n uint32 values at v, by one workgroup of NT threads; the result is
 // valid in thread 0.  Each thread keeps eight independent loads in flight
 // (a per-tensor scale reduces ~10^4 block maxima: one load at a time, that is

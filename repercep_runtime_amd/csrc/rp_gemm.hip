@@ -376,8 +376,11 @@ __device__ __forceinline__ i32x8 g2_op(const uint8_t* p, int h0, int h1) {
 
 // two fp32 -> packed bf16 with v_cvt_pk_bf16_f32 (round to nearest even)
 __device__ __forceinline__ uint32_t g2_pack_bf16(float lo, float hi) {
-  const __bf16 a = (__bf16)lo, b = (__bf16)hi;
-  return (uint32_t)__builtin_bit_cast(uint16_t, a) | ((uint32_t)__builtin_bit_cast(uint16_t, b) << 16);
+  // as one vector conversion: value by value, the compiler converts each
+  // alone and packs them with an extra or
+  typedef float f32x2_t __attribute__((ext_vector_type(2)));
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{lo, hi}, bf16x2_t));
 }
 
 struct G2Ops {
