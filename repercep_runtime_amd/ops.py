@@ -193,15 +193,32 @@ def _align(n: int, a: int = 256) -> int:
 
 
 def scale_quantize_qkv(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
-                       granularity: Granularity = "bh"
+                       granularity: Granularity = "bh", *, stream: int | None = None
                        ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor,
                                   torch.Tensor, torch.Tensor]:
     """(q_scale, q8, k_scale, k8, v_scale, vt8) of one attention call from one
     library call (rp_fp8_scale_quantize_qkv: four kernel launches instead of
     nine) into one device allocation: the same scales and codes as three
     ``scale_quantize`` calls (V transposed, "bhds"), with a fraction of the
-    host work, which is what bounds small calls.  (B, H, S, D) inputs, bf16 or fp16, any strides with a contiguous
-    head dim; K and V share their shape."""
+    host work, which is what bounds small calls.  (B, H, S, D) inputs, bf16 or
+    fp16, any strides with a contiguous head dim; K and V share their shape."""
+    arena, (o_k, o_v, o_s), G, ldv = _qkv_arena(q, k, v, granularity, stream)
+    B, H, Sq, D = q.shape
+    Skv = k.shape[2]
+    nq, nk, nv = B * H * Sq * D, B * H * Skv * D, B * H * D * ldv
+    dq = arena[o_s:o_s + 3 * G * 4].view(torch.float32)
+    q8 = arena[:nq].view(B, H, Sq, D).view(torch.float8_e4m3fn)
+    k8 = arena[o_k:o_k + nk].view(B, H, Skv, D).view(torch.float8_e4m3fn)
+    vt8 = arena[o_v:o_v + nv].view(B, H, D, ldv).view(torch.float8_e4m3fn)
+    return dq[:G], q8, dq[G:2 * G], k8, dq[2 * G:], vt8
+
+
+def _qkv_arena(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, granularity: Granularity,
+               stream: int | None) -> tuple[torch.Tensor, tuple[int, int, int], int, int]:
+    """The quantizer call of ``scale_quantize_qkv`` into one uint8 arena:
+    (arena, (byte offsets of k8, vt8 and the 3G fp32 scales; q8 at 0), G =
+    scales per tensor, ldv).  ``fp8_flash_attention`` launches from the
+    arena's pointers without building tensor views."""
     dt = _in_dtype("q", q)
     for name, t in (("k", k), ("v", v)):
         if _in_dtype(name, t) != dt:
@@ -227,12 +244,8 @@ def scale_quantize_qkv(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     C.check(C.lib().rp_fp8_scale_quantize_qkv(
         q.data_ptr(), k.data_ptr(), v.data_ptr(), dt, B, H, Sq, Skv, D, qsb, qsh, qss,
         ksb, ksh, kss, vsb, vsh, vss, g, base + o_s, base, base + o_k, base + o_v, ldv,
-        base + o_w, ws, _stream(q)), "rp_fp8_scale_quantize_qkv")
-    dq = arena[o_s:o_s + 3 * G * 4].view(torch.float32)
-    q8 = arena[:nq].view(B, H, Sq, D).view(torch.float8_e4m3fn)
-    k8 = arena[o_k:o_k + nk].view(B, H, Skv, D).view(torch.float8_e4m3fn)
-    vt8 = arena[o_v:o_v + nv].view(B, H, D, ldv).view(torch.float8_e4m3fn)
-    return dq[:G], q8, dq[G:2 * G], k8, dq[2 * G:], vt8
+        base + o_w, ws, _stream(q) if stream is None else stream), "rp_fp8_scale_quantize_qkv")
+    return arena, (o_k, o_v, o_s), G, ldv
 
 
 _ROPE = {None: C.RP_ROPE_NONE, "half": C.RP_ROPE_HALF, "interleaved": C.RP_ROPE_INTERLEAVED}
@@ -451,30 +464,38 @@ def attention_fp8(q8: torch.Tensor, k8: torch.Tensor, vt8: torch.Tensor, q_scale
     args = (q8.data_ptr(), k8.data_ptr(), vt8.data_ptr(), ldv, qs.data_ptr(), ks.data_ptr(),
             vs.data_ptr(), stride, float(sm_scale), out.data_ptr(), odt, out.stride(0),
             out.stride(1), out.stride(2), B, H, Sq, Skv, D, mask, pre, suf)
+    _launch_attention(args, kv_splits, block_m, q8.device, _stream(q8))
+    return out
+
+
+def _launch_attention(args: tuple, kv_splits: int, block_m: int, device: torch.device,
+                      stream: int) -> None:
+    """The attention launch of ``attention_fp8`` on checked arguments (the
+    common leading arguments of the rp_fp8_attn_fwd* entry points)."""
     if kv_splits < 0:
         raise ValueError(f"kv_splits={kv_splits} must be >= 0")
+    L = C.lib()
     if block_m != BLOCK_M:
         if block_m not in WSPLIT_BLOCK_MS or kv_splits != 1:
             raise ValueError(f"block_m={block_m} (kv_splits={kv_splits}): the short-query launch "
                              f"takes block_m in {WSPLIT_BLOCK_MS} and kv_splits=1")
-        C.check(C.lib().rp_fp8_attn_fwd_wsplit(*args, int(block_m), _stream(q8)),
-                "rp_fp8_attn_fwd_wsplit")
+        C.check(L.rp_fp8_attn_fwd_wsplit(*args, int(block_m), stream), "rp_fp8_attn_fwd_wsplit")
     elif kv_splits == 1:
-        C.check(C.lib().rp_fp8_attn_fwd(*args, _stream(q8)), "rp_fp8_attn_fwd")
+        C.check(L.rp_fp8_attn_fwd(*args, stream), "rp_fp8_attn_fwd")
     elif kv_splits == 0:
         # whole rounds of workgroups over one key range, the query blocks of
         # the last partial round key-split so that they fill the GPU
-        nbytes = C.lib().rp_fp8_attn_balanced_workspace_bytes(B, H, Sq, Skv, D, mask,
-                                                              _stream(q8))
-        ws = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=q8.device)
-        C.check(C.lib().rp_fp8_attn_fwd_balanced(*args, ws.data_ptr(), ws.numel(),
-                                                 _stream(q8)), "rp_fp8_attn_fwd_balanced")
+        B, H, Sq, Skv, D, mask = args[14], args[15], args[16], args[17], args[18], args[19]
+        nbytes = L.rp_fp8_attn_balanced_workspace_bytes(B, H, Sq, Skv, D, mask, stream)
+        ws = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=device)
+        C.check(L.rp_fp8_attn_fwd_balanced(*args, ws.data_ptr(), ws.numel(), stream),
+                "rp_fp8_attn_fwd_balanced")
     else:
-        nbytes = C.lib().rp_fp8_attn_workspace_bytes(B, H, Sq, D, int(kv_splits))
-        ws = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=q8.device)
-        C.check(C.lib().rp_fp8_attn_fwd_split(*args, int(kv_splits), ws.data_ptr(), ws.numel(),
-                                              _stream(q8)), "rp_fp8_attn_fwd_split")
-    return out
+        B, H, Sq, D = args[14], args[15], args[16], args[18]
+        nbytes = L.rp_fp8_attn_workspace_bytes(B, H, Sq, D, int(kv_splits))
+        ws = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=device)
+        C.check(L.rp_fp8_attn_fwd_split(*args, int(kv_splits), ws.data_ptr(), ws.numel(),
+                                         stream), "rp_fp8_attn_fwd_split")
 
 
 def fp8_flash_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *,
@@ -514,14 +535,34 @@ def fp8_flash_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *,
         raise ValueError(f"head_dim {D} not in compiled tile shapes {sorted(SUPPORTED_HEAD_DIMS)}")
     if scale is None:
         scale = 1.0 / math.sqrt(D)
-    qs, q8, ks, k8, vs, vt8 = scale_quantize_qkv(q, k, v, granularity)
+    st = _stream(q)
+    arena, (o_k, o_v, o_s), G, ldv = _qkv_arena(q, k, v, granularity, st)
+    base = arena.data_ptr()
+    if out is None:
+        out = torch.empty((B, H, Sq, D), dtype=out_dtype or q.dtype, device=q.device)
+    else:
+        _on_device_of(q, out=out)
+    if out.shape != (B, H, Sq, D) or out.stride(3) != 1:
+        raise ValueError("out must be (B, H, Sq, D) with a contiguous last dimension")
+    odt = _OUT_DTYPES.get(out.dtype)
+    if odt is None:
+        raise TypeError(f"out dtype {out.dtype} not supported (bfloat16, float16 or float32)")
+    if prefix_len is not None:
+        mask, pre, suf = C.RP_MASK_SHARED_PREFIX, int(prefix_len), int(suffix_len or 0)
+    else:
+        mask, pre, suf = (C.RP_MASK_CAUSAL if causal else C.RP_MASK_NONE), 0, 1
+    # the quantizer's own outputs in the arena: contiguous codes, fp32
+    # scales, one per head or one per tensor
+    stride = 1 if G == B * H and B * H > 1 else 0
+    args = (base, base + o_k, base + o_v, ldv, base + o_s, base + o_s + 4 * G,
+            base + o_s + 8 * G, stride, float(scale), out.data_ptr(), odt,
+            out.stride(0), out.stride(1), out.stride(2), B, H, Sq, k.shape[2], D, mask, pre, suf)
 
     def run(cfg: dict) -> torch.Tensor:
         block_m, splits = launch_of(cfg)
-        return attention_fp8(q8.view(torch.uint8), k8.view(torch.uint8), vt8.view(torch.uint8),
-                             qs, ks, vs, scale, out=out, out_dtype=out_dtype or q.dtype,
-                             causal=causal, prefix_len=prefix_len, suffix_len=suffix_len,
-                             kv_splits=splits, block_m=block_m)
+        # the arena stays referenced while the launches are queued
+        _launch_attention(args, splits, block_m, arena.device, st)
+        return out
 
     if kv_splits is not None:
         return run({"KV_SPLITS": int(kv_splits)})

@@ -44,6 +44,7 @@ from pathlib import Path
 from typing import Callable
 
 _DEFAULT_CACHE_PATH = Path.home() / ".cache" / "repercep" / "fp8_hip_autotune.json"
+_DEFAULT_CACHE_STR = str(_DEFAULT_CACHE_PATH)
 
 BLOCK_M = 256
 BLOCK_N = 128
@@ -119,24 +120,31 @@ def cache_path() -> Path:
 _memo: tuple[tuple[str, int, int], dict] | None = None
 
 
-def cache_load() -> dict:
+def _cache_view() -> dict:
+    """The parsed cache file, shared with the memo (callers must not modify
+    it): one os.stat per call, a JSON parse only when the file changed."""
     global _memo
-    path = cache_path()
+    override = os.environ.get("REPERCEP_FP8_AUTOTUNE_CACHE")
+    path = override if override else _DEFAULT_CACHE_STR
     try:
-        st = path.stat()
+        st = os.stat(path)
     except OSError:
         return {}
-    stamp = (str(path), st.st_mtime_ns, st.st_size)
+    stamp = (path, st.st_mtime_ns, st.st_size)
     if _memo is not None and _memo[0] == stamp:
-        return dict(_memo[1])
+        return _memo[1]
     try:
-        with path.open("r") as fh:
+        with open(path, "r") as fh:
             data = json.load(fh)
     except (OSError, ValueError):
         return {}
     data = data if isinstance(data, dict) else {}
     _memo = (stamp, data)
-    return dict(data)
+    return data
+
+
+def cache_load() -> dict:
+    return dict(_cache_view())
 
 
 def cache_save(cache: dict) -> None:
@@ -176,7 +184,7 @@ def runnable(cfg: object) -> bool:
 def resolve_config(B: int, H: int, Sq: int, Skv: int, D: int, causal: bool,
                    prefix_len: int | None = None, suffix_len: int | None = None) -> dict:
     """The cached configuration for this shape, or {} on a miss."""
-    cfg = cache_load().get(cache_key(B, H, Sq, Skv, D, causal, prefix_len, suffix_len))
+    cfg = _cache_view().get(cache_key(B, H, Sq, Skv, D, causal, prefix_len, suffix_len))
     return dict(cfg) if runnable(cfg) else {}
 
 
