@@ -132,7 +132,9 @@ def test_softmax_rowwise_quantize_vs_oracle(gpu: torch.device, causal: bool) -> 
     """P = softmax(bf16(raw * scale)) in bf16 and its row-wise codes: the sum
     of exponentials runs in another order than torch's, so a P value may sit
     one bf16 step away and its code one e4m3 step; the scales agree within
-    one bf16 step and almost every code is identical."""
+    one bf16 step and almost every code is identical (every one of these
+    seeds' codes with the accurate expf; the bound leaves room for a rare
+    P value on the other side of a rounding boundary)."""
     g = torch.Generator().manual_seed(5 + causal)
     raw = (torch.randn(3, 96, 384, generator=g) * 4).to(torch.bfloat16)
     scale = 0.125
@@ -144,7 +146,9 @@ def test_softmax_rowwise_quantize_vs_oracle(gpu: torch.device, causal: bool) -> 
     gc = codes.view(torch.uint8).cpu().numpy().astype(np.int32)
     rc = ref_codes.numpy().astype(np.int32)
     assert np.all(np.abs(gc - rc) <= 1)
-    assert (gc == rc).mean() > 0.995
+    same = (gc == rc).mean()
+    print(f"softmax codes identical: {same:.6f} (causal={causal})", flush=True)
+    assert same > 0.9999
     if causal:      # masked entries quantize to code 0
         q = np.arange(96)[None, :, None]
         j = np.arange(384)[None, None, :]
