@@ -5,7 +5,10 @@ Default workload: BASELINE config 3, Wan-2.2 self-attention
 One step = the whole hot path on one batch: amax scale + e4m3fn quantization
 of Q, K and V (V written transposed) followed by the FP8 flash-attention
 forward writing bf16 output -- the work of the reference's
-``fp8_flash_attention`` call.  Scales are per tensor by default, as BASELINE
+``fp8_flash_attention`` call.  As ``fp8_flash_attention`` does for a
+256-row launch, the step hands the attention Q as it lies with its scale and
+the kernel quantizes Q's rows itself (the same codes) on resident-K/V
+launches (``--codes-q`` runs the two-step form there too).  Scales are per tensor by default, as BASELINE
 configs 2-5 state them (``--granularity bh`` runs the reference's per-(B,H)
 scales; the attention kernel's work is the same either way).
 
@@ -193,20 +196,34 @@ def bench_attention(args, cfg) -> dict:
     else:
         block_m, splits = ops.tuned_launch(cfg.B, cfg.H, cfg.Sq, cfg.Skv, cfg.D, cfg.causal,
                                            prefix, cfg.suffix)
-    log(f"[bench] block_m {block_m} kv_splits {splits}")
+    # what fp8_flash_attention runs for a resident-K/V launch: the quantizer
+    # writes K's and V^T's codes and every scale, the attention quantizes its
+    # own Q rows (the same codes, the same output)
+    mask = 1 if cfg.causal else (2 if prefix is not None else 0)
+    q16 = (not fused_norm and block_m == ops.BLOCK_M and not args.codes_q
+           and ops.q16_pays(cfg.B, cfg.H, cfg.Sq, cfg.Skv, cfg.D, mask, splits,
+                            ops._stream(q)))
+    log(f"[bench] block_m {block_m} kv_splits {splits} q_in_attention {q16}")
 
     def step(ev=None):
         if ev is not None:
             ev[0].record(st)
         if fused_norm:
             qs, q8, ks, k8, vs, vt8 = ops.rmsnorm_scale_quantize_qkv(q, k, v, granularity=gran)
-        else:   # what fp8_flash_attention runs: one library call for Q, K, V
+        elif q16:
+            qs, ks, k8, vs, vt8 = ops.scale_quantize_kv(q, k, v, gran)
+        else:   # one library call for Q, K, V
             qs, q8, ks, k8, vs, vt8 = ops.scale_quantize_qkv(q, k, v, gran)
         if ev is not None:
             ev[1].record(st)
-        ops.attention_fp8(q8.view(torch.uint8), k8.view(torch.uint8), vt8.view(torch.uint8),
-                          qs, ks, vs, sm, out=out, causal=cfg.causal, prefix_len=prefix,
-                          suffix_len=cfg.suffix, kv_splits=splits, block_m=block_m)
+        if q16:
+            ops.attention_fp8_q16(q, k8.view(torch.uint8), vt8.view(torch.uint8), qs, ks, vs, sm,
+                                  out=out, causal=cfg.causal, prefix_len=prefix,
+                                  suffix_len=cfg.suffix, kv_splits=splits)
+        else:
+            ops.attention_fp8(q8.view(torch.uint8), k8.view(torch.uint8), vt8.view(torch.uint8),
+                              qs, ks, vs, sm, out=out, causal=cfg.causal, prefix_len=prefix,
+                              suffix_len=cfg.suffix, kv_splits=splits, block_m=block_m)
         if ev is not None:
             ev[2].record(st)
 
@@ -300,9 +317,13 @@ def bench_attention(args, cfg) -> dict:
             cfg.B, cfg.H, cfg.Sq, cfg.Skv, cfg.D, mask, 1):
         # a plain launch whose key range fits LDS runs the resident-K/V kernel
         kernel = attn_launches = "attn_kvres_kernel"
+        if q16:
+            attn_launches += " (quantizing Q's rows from the bf16 input as it reads them)"
     if block_m != ops.BLOCK_M:   # the short-query launch merges its splits itself
         kernel = attn_launches = "attn_wsplit_kernel"
     qbytes = QUANT_BYTES_PER_ELEM * cfg.quant_elems
+    if q16:   # Q is read once by the quantizer (its amax), its codes never stored
+        qbytes -= (QUANT_BYTES_PER_ELEM - 2) * cfg.B * cfg.H * cfg.Sq * cfg.D
     q_gbps = qbytes / (quant_ms * 1e-3) / 1e9
     res = {
         "metric": "FP8 attn TFLOP/s + % FP8-MFMA peak (Wan-2.2 S=75600); quantize GB/s",
@@ -345,6 +366,10 @@ def bench_attention(args, cfg) -> dict:
             "bytes": qbytes,
             "note": ("Q, K with RMSNorm fused, V plain: one multi-tensor amax pass + "
                      "finalize + apply (V transposed); 5 B/element" if fused_norm else
+                     "Q's scale and K, V codes: one multi-tensor amax pass + finalize + "
+                     "apply of K and V (V transposed); Q read once (2 B/element), K and V "
+                     "5 B/element; the attention kernel quantizes Q's rows as it reads "
+                     "them" if q16 else
                      "Q, K, V: one multi-tensor amax pass + finalize + apply (V "
                      "transposed), 5 B/element"),
         },
@@ -599,6 +624,9 @@ def main() -> int:
     ap.add_argument("--block-m", type=int, default=None, choices=(32, 64, 128, 256),
                     help="attention configs: force the query rows per workgroup (32, 64, 128: "
                          "the short-query launch with its keys split over the waves)")
+    ap.add_argument("--codes-q", action="store_true",
+                    help="write Q's codes in the quantizer and read them in the attention "
+                         "launch, instead of the attention quantizing Q's rows itself")
     ap.add_argument("--kv-splits", type=int, default=None,
                     help="attention configs: force a launch configuration (1: one key range, "
                          "0: the balanced launch, n > 1: n key splits) instead of the one the "

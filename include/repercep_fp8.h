@@ -118,7 +118,9 @@ int rp_fp8_scale_quantize(const void* x, int x_dtype, int64_t B, int64_t H, int6
  * calls.  dequant_out: float[3 * G], G = B*H (RP_SCALE_PER_BH) or 1, in the
  * order q, k, v.  workspace: rp_fp8_quant_qkv_workspace_bytes, 256-byte
  * aligned.  Replaces the three _per_bh_scale + _quantize pairs at
- * kernels/triton_kernels/fp8_flash_attn.py:522-528 with one host call. */
+ * kernels/triton_kernels/fp8_flash_attn.py:522-528 with one host call.
+ * q8 may be NULL: Q's scale is computed and no Q codes are written, for an
+ * attention launch that quantizes Q itself (rp_fp8_attn_fwd_q16). */
 size_t rp_fp8_quant_qkv_workspace_bytes(int64_t B, int64_t H, int64_t Sq, int64_t Skv,
                                         int64_t D, int granularity);
 int rp_fp8_scale_quantize_qkv(const void* q, const void* k, const void* v, int x_dtype,
@@ -259,6 +261,30 @@ int rp_fp8_attn_blocks_per_workgroup(int B, int H, int Sq, int Skv, int D, int m
  * No counterpart in the reference; exposed for tests and profiling.  1 or
  * 0. */
 int rp_fp8_attn_resident_kv(int B, int H, int Sq, int Skv, int D, int mask, int kv_splits);
+
+/* rp_fp8_attn_fwd_balanced (kv_splits 0) or rp_fp8_attn_fwd_split
+ * (kv_splits >= 1) with Q as its 16-bit input instead of codes: q is the
+ * bf16 or fp16 (q_dtype RP_DTYPE_*) tensor (B, H, Sq, D) with element strides
+ * qsb, qsh, qss (16-byte aligned, unit stride on D), q_scale its dequant
+ * scale(s) as rp_fp8_scale_quantize_qkv computes them (there with q8 =
+ * NULL), and each workgroup quantizes the Q rows it reads with the
+ * quantizer's arithmetic -- the codes, and so the output, are those of the
+ * separate quantizer and rp_fp8_attn_fwd*, bit for bit.  No counterpart in
+ * the reference, whose wrapper writes Q's codes and reads them back
+ * (fp8_flash_attn.py:526-528, 604-644): this saves 3 of Q's 6 bytes per
+ * element of HBM traffic.  Head dims 64, 128 and 256; the multi-block launch
+ * of short key ranges that do not fit LDS takes codes only
+ * (RP_ERR_UNSUPPORTED; rp_fp8_attn_q16_supported tells beforehand).
+ * Workspace as the entry point kv_splits selects. */
+int rp_fp8_attn_q16_supported(int B, int H, int Sq, int Skv, int D, int mask, int kv_splits,
+                              void* stream);
+int rp_fp8_attn_fwd_q16(const void* q, int q_dtype, int64_t qsb, int64_t qsh, int64_t qss,
+                        const uint8_t* k8, const uint8_t* vt8, int64_t ldv,
+                        const float* q_scale, const float* k_scale, const float* v_scale,
+                        int scale_stride, float sm_scale, void* out, int out_dtype,
+                        int64_t osb, int64_t osh, int64_t oss, int B, int H, int Sq, int Skv,
+                        int D, int mask, int prefix_len, int suffix_len, int kv_splits,
+                        void* workspace, size_t workspace_bytes, void* stream);
 
 /* Key-split variant of rp_fp8_attn_fwd: the key range is cut into
  * `kv_splits` contiguous parts of whole 128-key tiles (fewer when Skv has

@@ -47,6 +47,7 @@ EXPORTS = (
     "rp_fp8_attn_fwd_split", "rp_fp8_attn_balanced_plan",
     "rp_fp8_attn_fwd_wsplit", "rp_fp8_attn_wsplit_plan",
     "rp_fp8_attn_balanced_workspace_bytes", "rp_fp8_attn_fwd_balanced",
+    "rp_fp8_attn_q16_supported", "rp_fp8_attn_fwd_q16",
     "rp_fp8_rmsnorm_quant_workspace_bytes",
     "rp_fp8_rmsnorm_scale_quantize", "rp_fp8_rmsnorm_quant_qkv_workspace_bytes",
     "rp_fp8_rmsnorm_scale_quantize_qkv", "rp_fp8_gemm", "rp_fp8_linear",
@@ -121,6 +122,12 @@ def _declare(L: ctypes.CDLL) -> None:
     L.rp_fp8_attn_fwd_balanced.restype = _int
     L.rp_fp8_attn_fwd_balanced.argtypes = (list(L.rp_fp8_attn_fwd.argtypes[:-1])
                                            + [_vp, _sz, _vp])
+    L.rp_fp8_attn_q16_supported.restype = _int
+    L.rp_fp8_attn_q16_supported.argtypes = [_int] * 7 + [_vp]
+    L.rp_fp8_attn_fwd_q16.restype = _int
+    L.rp_fp8_attn_fwd_q16.argtypes = ([_vp, _int, _i64, _i64, _i64]
+                                      + list(L.rp_fp8_attn_fwd.argtypes[1:-1])
+                                      + [_int, _vp, _sz, _vp])
     L.rp_fp8_rmsnorm_quant_workspace_bytes.restype = _sz
     L.rp_fp8_rmsnorm_quant_workspace_bytes.argtypes = [_i64, _i64, _i64, _i64, _int]
     L.rp_fp8_rmsnorm_scale_quantize.restype = _int

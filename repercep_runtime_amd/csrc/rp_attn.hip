@@ -73,6 +73,13 @@ constexpr float kLog2PMax = 8.807354922057604f;  // log2(448)
 
 struct AttnArgs {
   const uint8_t* q;
+  // Q as its bf16 or fp16 input (q_dt: kInBf16 / kInF16), (B, H, Sq, D) with
+  // element strides qsb, qsh, qss, instead of codes in q: the kernel
+  // quantizes its own Q rows with the quantizer's arithmetic (quant4, qm =
+  // 1 / q scale), so the codes are the quantizer's.  Null when q holds codes.
+  const uint16_t* q16;
+  int64_t qsb, qsh, qss;
+  int q_dt;
   const uint8_t* k;
   const uint8_t* vt;
   const float* qs;
@@ -333,6 +340,33 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
   typedef float f32x2_t __attribute__((ext_vector_type(2)));
   typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{lo, hi}, bf16x2_t));
+}
+
+// 32 consecutive 16-bit Q elements (64 bytes at p, 16-byte aligned) in four
+// loads, and their e4m3 codes (element 0 in the low byte, as the quantizer
+// stores them)
+struct QRaw32 {
+  i32x4 w[4];
+};
+__device__ __forceinline__ QRaw32 qraw_load(const uint16_t* p) {
+  const i32x4* s = reinterpret_cast<const i32x4*>(p);
+  return QRaw32{{s[0], s[1], s[2], s[3]}};
+}
+__device__ __forceinline__ i32x8 qraw_codes(const QRaw32& r, float qm, int dt) {
+  i32x8 c;
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    const uint32_t x = (uint32_t)r.w[m][0], y = (uint32_t)r.w[m][1];
+    const uint32_t z = (uint32_t)r.w[m][2], t = (uint32_t)r.w[m][3];
+    if (dt == kInF16) {
+      c[2 * m] = (int)quant4<kInF16>(x, y, qm);
+      c[2 * m + 1] = (int)quant4<kInF16>(z, t, qm);
+    } else {
+      c[2 * m] = (int)quant4<kInBf16>(x, y, qm);
+      c[2 * m + 1] = (int)quant4<kInBf16>(z, t, qm);
+    }
+  }
+  return c;
 }
 
 // Two LDS reads (32 bytes per lane) of one MFMA operand.
@@ -629,6 +663,21 @@ void attn_fwd_kernel(AttnArgs a) {
 
   // ---- Q^T operand (B operand of S^T), resident for the whole kernel
   auto load_q = [&](i32x8 (&dst)[G::KSTEPS], int qrow) {
+    if constexpr (!MULTI && DK >= 64) {
+      if (a.q16 != nullptr) {
+        // Q from its 16-bit input: this lane's 32-element runs 32 lg + 64 ks
+        // of row qrow, quantized here
+        const uint16_t* src = a.q16 + (int64_t)b * a.qsb + (int64_t)h * a.qsh +
+                              (int64_t)min(qrow, a.Sq - 1) * a.qss + 32 * lg;
+        const float qm = 1.0f / q_scale;
+        QRaw32 raw[G::KSTEPS];
+#pragma unroll
+        for (int ks = 0; ks < G::KSTEPS; ++ks) raw[ks] = qraw_load(src + 64 * ks);
+#pragma unroll
+        for (int ks = 0; ks < G::KSTEPS; ++ks) dst[ks] = qraw_codes(raw[ks], qm, a.q_dt);
+        return;
+      }
+    }
     if constexpr (DK < 64) {
       // one 64-deep step over a 32-byte row: k-slot group 1 is zero padding
       const i32x4* src = reinterpret_cast<const i32x4*>(qh + (int64_t)min(qrow, a.Sq - 1) * D);
@@ -1106,7 +1155,6 @@ inline int multi_block_plan(const AttnArgs& a, int D) {
   return best;
 }
 
-
 // Key tiles per split and the number of non-empty splits for a request of
 // `kv_splits`.
 inline void split_plan(int Skv, int kv_splits, int* split_tiles, int* n_splits) {
@@ -1197,6 +1245,10 @@ int launch_attn(const AttnArgs& base, int out_dtype, hipStream_t st) {
   // a key range resident in LDS runs the persistent resident-K/V kernel
   if constexpr (D == 64 || D == 128) {
     if (kvres_applies(a, D)) return launch_kvres<D>(a, out_dtype, st, stream_cus(st));
+  }
+  if (a.q16 != nullptr && a.qb_per_wg > 1) {
+    rp_set_error("attn: the multi-block launch of this shape takes Q as codes only");
+    return RP_ERR_UNSUPPORTED;
   }
   // a mixed launch: blocks [0, qb_begin) unsplit, the rest key-split
   const bool mixed = a.qb_begin > 0;
@@ -1354,6 +1406,7 @@ __device__ __forceinline__ i32x8 gload32(const uint8_t* p) {
   const i32x4* s = reinterpret_cast<const i32x4*>(p);
   return cat8(s[0], s[1]);
 }
+
 
 template <int D, int QG, int OUT>
 __global__ __launch_bounds__(512, 1)
@@ -1756,7 +1809,6 @@ int launch_wsplit_rows(const AttnArgs& a, int block_m, int out_dtype, hipStream_
   }
 }
 
-
 // ---------------------------------------------------------------------------
 // Short key ranges against many queries (cross-attention: C3's 512 text
 // keys): the head's whole K and V^T resident in LDS.
@@ -1835,7 +1887,7 @@ __device__ __forceinline__ void store_o_rows(const AttnArgs& a, const f32x16 (&a
   }
 }
 
-template <int D, int OUT>
+template <int D, int OUT, bool Q16>
 __global__ __launch_bounds__(512, 1)
 void attn_kvres_kernel(AttnArgs a) {
   using G = KvGeo<D>;
@@ -1904,6 +1956,22 @@ void attn_kvres_kernel(AttnArgs a) {
 #pragma unroll
       for (int ks = 0; ks < G::KSTEPS; ++ks) dst[ks] = gload32(src + 64 * ks);
     };
+    // Q16: a task's Q rows from their 16-bit input, loaded one task ahead
+    // as they lie and quantized (quant4, the quantizer's arithmetic) when
+    // the task starts
+    const float qm = 1.0f / q_scale;
+    auto load_qraw = [&](QRaw32 (&dst)[G::KSTEPS], int64_t task) __attribute__((always_inline)) {
+      const int qr = min((int)(task - (int64_t)bh * nq) * 32 + lq, a.Sq - 1);
+      const uint16_t* src = a.q16 + (int64_t)b * a.qsb + (int64_t)h * a.qsh +
+                            (int64_t)qr * a.qss + 32 * lg;
+#pragma unroll
+      for (int ks = 0; ks < G::KSTEPS; ++ks) dst[ks] = qraw_load(src + 64 * ks);
+    };
+    auto qcodes = [&](i32x8 (&dst)[G::KSTEPS], const QRaw32 (&raw)[G::KSTEPS])
+        __attribute__((always_inline)) {
+#pragma unroll
+      for (int ks = 0; ks < G::KSTEPS; ++ks) dst[ks] = qraw_codes(raw[ks], qm, a.q_dt);
+    };
     const int64_t first = seg + wave;   // the wave's tasks: first, first + 8, ...
     const int ntw = first < seg_end ? (int)((seg_end - first + kWsWaves - 1) / kWsWaves) : 0;
     const int nsteps = ntw * n_kb;
@@ -1911,6 +1979,7 @@ void attn_kvres_kernel(AttnArgs a) {
     const uint32_t vb = vl_lds + (uint32_t)(lq * VP + 32 * lg);
     f32x16 s[4], acc[G::ETILES];
     i32x8 qop[G::KSTEPS], qnext[G::KSTEPS];
+    QRaw32 qnraw[Q16 ? G::KSTEPS : 1];
     // S^T MFMAs of tile jj, score blocks h0 and h0 + 1, against Q^T qq
     auto s_pair = [&](int jj, int h0, const i32x8 (&qq)[G::KSTEPS]) __attribute__((always_inline)) {
       i32x8 kop[2][G::KSTEPS];
@@ -1926,9 +1995,15 @@ void attn_kvres_kernel(AttnArgs a) {
           s[h0 + u] = mfma_32x32x64(kop[u][ks], qq[ks], ks == 0 ? f32x16{} : s[h0 + u]);
     };
     if (nsteps > 0) {
-      load_q(qop, first);
       // the next task's Q^T; the last task's "next" re-reads its own rows
-      load_q(qnext, ntw > 1 ? first + kWsWaves : first);
+      if constexpr (Q16) {
+        load_qraw(qnraw, first);
+        qcodes(qop, qnraw);
+        load_qraw(qnraw, ntw > 1 ? first + kWsWaves : first);
+      } else {
+        load_q(qop, first);
+        load_q(qnext, ntw > 1 ? first + kWsWaves : first);
+      }
       s_pair(0, 0, qop);
       s_pair(0, 2, qop);
     }
@@ -1986,9 +2061,14 @@ void attn_kvres_kernel(AttnArgs a) {
         // qop is step i + 1's Q^T: at a task's last tile it takes the next
         // task's rows before the first pair goes out.
         if (m == 0 && ends_task) {
+          if constexpr (Q16) {
+            qcodes(qop, qnraw);
+            load_qraw(qnraw, first + (int64_t)min(t + 2, ntw - 1) * kWsWaves);
+          } else {
 #pragma unroll
-          for (int ks = 0; ks < G::KSTEPS; ++ks) qop[ks] = qnext[ks];
-          load_q(qnext, first + (int64_t)min(t + 2, ntw - 1) * kWsWaves);
+            for (int ks = 0; ks < G::KSTEPS; ++ks) qop[ks] = qnext[ks];
+            load_q(qnext, first + (int64_t)min(t + 2, ntw - 1) * kWsWaves);
+          }
         }
         __builtin_amdgcn_sched_barrier(0);
         s_pair(jn, 2 * m, qop);
@@ -2058,12 +2138,20 @@ int launch_kvres(const AttnArgs& base, int out_dtype, hipStream_t st, int cus) {
   const int64_t want = cus > 0 ? cus : kCUs;
   const int grid = (int)(ntask < want ? ntask : want);
   const int kind = out_kind(out_dtype);
-  if (kind == kOutF32)
-    hipLaunchKernelGGL((attn_kvres_kernel<D, kOutF32>), dim3(grid), dim3(512), 0, st, a);
-  else if (kind == kOutF16)
-    hipLaunchKernelGGL((attn_kvres_kernel<D, kOutF16>), dim3(grid), dim3(512), 0, st, a);
-  else
-    hipLaunchKernelGGL((attn_kvres_kernel<D, kOutBf16>), dim3(grid), dim3(512), 0, st, a);
+  if (a.q16 != nullptr) {
+    if (kind == kOutF32)
+      hipLaunchKernelGGL((attn_kvres_kernel<D, kOutF32, true>), dim3(grid), dim3(512), 0, st, a);
+    else if (kind == kOutF16)
+      hipLaunchKernelGGL((attn_kvres_kernel<D, kOutF16, true>), dim3(grid), dim3(512), 0, st, a);
+    else
+      hipLaunchKernelGGL((attn_kvres_kernel<D, kOutBf16, true>), dim3(grid), dim3(512), 0, st, a);
+  } else if (kind == kOutF32) {
+    hipLaunchKernelGGL((attn_kvres_kernel<D, kOutF32, false>), dim3(grid), dim3(512), 0, st, a);
+  } else if (kind == kOutF16) {
+    hipLaunchKernelGGL((attn_kvres_kernel<D, kOutF16, false>), dim3(grid), dim3(512), 0, st, a);
+  } else {
+    hipLaunchKernelGGL((attn_kvres_kernel<D, kOutBf16, false>), dim3(grid), dim3(512), 0, st, a);
+  }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) {
     rp_set_error("attn: launch failed: %s", hipGetErrorString(e));
@@ -2240,18 +2328,9 @@ extern "C" size_t rp_fp8_attn_workspace_bytes(int B, int H, int Sq, int D, int k
   return ml + rows * (size_t)D * sizeof(float);
 }
 
-extern "C" int rp_fp8_attn_fwd_split(const uint8_t* q8, const uint8_t* k8, const uint8_t* vt8,
-                                     int64_t ldv, const float* q_scale, const float* k_scale,
-                                     const float* v_scale, int scale_stride, float sm_scale,
-                                     void* out, int out_dtype, int64_t osb, int64_t osh,
-                                     int64_t oss, int B, int H, int Sq, int Skv, int D, int mask,
-                                     int prefix_len, int suffix_len, int kv_splits,
-                                     void* workspace, size_t workspace_bytes, void* stream) {
-  AttnArgs a;
-  int rc = attn_setup(a, q8, k8, vt8, ldv, q_scale, k_scale, v_scale, scale_stride, sm_scale,
-                      out, out_dtype, osb, osh, oss, B, H, Sq, Skv, D, mask, prefix_len,
-                      suffix_len);
-  if (rc != RP_OK) return rc;
+// The key-split launch on set-up arguments (rp_fp8_attn_fwd_split).
+static int run_split(AttnArgs& a, int B, int H, int Sq, int Skv, int D, int out_dtype,
+                     int kv_splits, void* workspace, size_t workspace_bytes, void* stream) {
   if (kv_splits < 1) {
     rp_set_error("attn: kv_splits=%d must be >= 1", kv_splits);
     return RP_ERR_INVALID_ARGUMENT;
@@ -2274,6 +2353,21 @@ extern "C" int rp_fp8_attn_fwd_split(const uint8_t* q8, const uint8_t* k8, const
                                         (rows * 2 * sizeof(float) + 255) / 256 * 256);
   }
   return attn_run(a, D, out_dtype, stream);
+}
+
+extern "C" int rp_fp8_attn_fwd_split(const uint8_t* q8, const uint8_t* k8, const uint8_t* vt8,
+                                     int64_t ldv, const float* q_scale, const float* k_scale,
+                                     const float* v_scale, int scale_stride, float sm_scale,
+                                     void* out, int out_dtype, int64_t osb, int64_t osh,
+                                     int64_t oss, int B, int H, int Sq, int Skv, int D, int mask,
+                                     int prefix_len, int suffix_len, int kv_splits,
+                                     void* workspace, size_t workspace_bytes, void* stream) {
+  AttnArgs a;
+  int rc = attn_setup(a, q8, k8, vt8, ldv, q_scale, k_scale, v_scale, scale_stride, sm_scale,
+                      out, out_dtype, osb, osh, oss, B, H, Sq, Skv, D, mask, prefix_len,
+                      suffix_len);
+  if (rc != RP_OK) return rc;
+  return run_split(a, B, H, Sq, Skv, D, out_dtype, kv_splits, workspace, workspace_bytes, stream);
 }
 
 extern "C" int rp_fp8_attn_balanced_plan(int B, int H, int Sq, int Skv, int D, int mask, int cus,
@@ -2309,18 +2403,9 @@ extern "C" size_t rp_fp8_attn_balanced_workspace_bytes(int B, int H, int Sq, int
                            D);
 }
 
-extern "C" int rp_fp8_attn_fwd_balanced(const uint8_t* q8, const uint8_t* k8, const uint8_t* vt8,
-                                        int64_t ldv, const float* q_scale, const float* k_scale,
-                                        const float* v_scale, int scale_stride, float sm_scale,
-                                        void* out, int out_dtype, int64_t osb, int64_t osh,
-                                        int64_t oss, int B, int H, int Sq, int Skv, int D,
-                                        int mask, int prefix_len, int suffix_len, void* workspace,
-                                        size_t workspace_bytes, void* stream) {
-  AttnArgs a;
-  int rc = attn_setup(a, q8, k8, vt8, ldv, q_scale, k_scale, v_scale, scale_stride, sm_scale,
-                      out, out_dtype, osb, osh, oss, B, H, Sq, Skv, D, mask, prefix_len,
-                      suffix_len);
-  if (rc != RP_OK) return rc;
+// The balanced launch on set-up arguments (rp_fp8_attn_fwd_balanced).
+static int run_balanced(AttnArgs& a, int B, int H, int Sq, int Skv, int D, int mask,
+                        int out_dtype, void* workspace, size_t workspace_bytes, void* stream) {
   const TailPlan t = tail_plan(B, H, Sq, Skv, D, mask, stream_cus(stream));
   if (t.splits <= 1) return attn_run(a, D, out_dtype, stream);
   const size_t need = balanced_ws_bytes(t, B, H, Sq, Skv, D);
@@ -2344,4 +2429,89 @@ extern "C" int rp_fp8_attn_fwd_balanced(const uint8_t* q8, const uint8_t* k8, co
   a.item_counter = reinterpret_cast<unsigned*>(static_cast<char*>(workspace) +
                                                balanced_partials_bytes(t, B, H, Sq, Skv, D));
   return attn_run(a, D, out_dtype, stream);
+}
+
+extern "C" int rp_fp8_attn_fwd_balanced(const uint8_t* q8, const uint8_t* k8, const uint8_t* vt8,
+                                        int64_t ldv, const float* q_scale, const float* k_scale,
+                                        const float* v_scale, int scale_stride, float sm_scale,
+                                        void* out, int out_dtype, int64_t osb, int64_t osh,
+                                        int64_t oss, int B, int H, int Sq, int Skv, int D,
+                                        int mask, int prefix_len, int suffix_len, void* workspace,
+                                        size_t workspace_bytes, void* stream) {
+  AttnArgs a;
+  int rc = attn_setup(a, q8, k8, vt8, ldv, q_scale, k_scale, v_scale, scale_stride, sm_scale,
+                      out, out_dtype, osb, osh, oss, B, H, Sq, Skv, D, mask, prefix_len,
+                      suffix_len);
+  if (rc != RP_OK) return rc;
+  return run_balanced(a, B, H, Sq, Skv, D, mask, out_dtype, workspace, workspace_bytes, stream);
+}
+
+// Whether the launch a shape resolves to (kv_splits 0: the balanced launch;
+// 1: one key range; more: key splits) quantizes Q itself: every launch but
+// the multi-block one (short key ranges that are not resident in LDS) and
+// the head dim 32 layout.
+static bool q16_launch_ok(int B, int H, int Sq, int Skv, int D, int mask, int kv_splits,
+                          int cus) {
+  if (B <= 0 || H <= 0 || Sq <= 0 || Skv <= 0 || kv_splits < 0) return false;
+  if (D != 64 && D != 128 && D != 256) return false;
+  int splits = kv_splits;
+  if (kv_splits == 0) {
+    const TailPlan t = tail_plan(B, H, Sq, Skv, D, mask, cus);
+    if (t.splits > 1) return true;    // the mixed launch: one query block per workgroup
+    splits = 1;
+  }
+  AttnArgs a{};
+  a.B = B; a.H = H; a.Sq = Sq; a.Skv = Skv; a.mask = mask;
+  int split_tiles = 0, n_splits = 1;
+  split_plan(Skv, splits, &split_tiles, &n_splits);
+  a.kv_splits = n_splits;
+  a.n_qblocks = (Sq + kBlockM - 1) / kBlockM;
+  if (kvres_applies(a, D)) return true;
+  return multi_block_plan(a, D) <= 1;
+}
+
+extern "C" int rp_fp8_attn_q16_supported(int B, int H, int Sq, int Skv, int D, int mask,
+                                         int kv_splits, void* stream) {
+  return q16_launch_ok(B, H, Sq, Skv, D, mask, kv_splits, stream_cus(stream)) ? 1 : 0;
+}
+
+extern "C" int rp_fp8_attn_fwd_q16(const void* q, int q_dtype, int64_t qsb, int64_t qsh,
+                                   int64_t qss, const uint8_t* k8, const uint8_t* vt8,
+                                   int64_t ldv, const float* q_scale, const float* k_scale,
+                                   const float* v_scale, int scale_stride, float sm_scale,
+                                   void* out, int out_dtype, int64_t osb, int64_t osh,
+                                   int64_t oss, int B, int H, int Sq, int Skv, int D, int mask,
+                                   int prefix_len, int suffix_len, int kv_splits,
+                                   void* workspace, size_t workspace_bytes, void* stream) {
+  if (q == nullptr) {
+    rp_set_error("attn: null pointer");
+    return RP_ERR_INVALID_ARGUMENT;
+  }
+  if (q_dtype != RP_DTYPE_BF16 && q_dtype != RP_DTYPE_F16) {
+    rp_set_error("attn: unknown q_dtype %d", q_dtype);
+    return RP_ERR_INVALID_ARGUMENT;
+  }
+  if ((reinterpret_cast<uintptr_t>(q) % 16) != 0 || qsb % 8 != 0 || qsh % 8 != 0 ||
+      qss % 8 != 0) {
+    rp_set_error("attn: q and its strides must be 16-byte aligned");
+    return RP_ERR_UNSUPPORTED;
+  }
+  AttnArgs a;
+  // q passes the null and alignment checks in place of the codes
+  int rc = attn_setup(a, static_cast<const uint8_t*>(q), k8, vt8, ldv, q_scale, k_scale,
+                      v_scale, scale_stride, sm_scale, out, out_dtype, osb, osh, oss, B, H, Sq,
+                      Skv, D, mask, prefix_len, suffix_len);
+  if (rc != RP_OK) return rc;
+  if (!q16_launch_ok(B, H, Sq, Skv, D, mask, kv_splits, stream_cus(stream))) {
+    rp_set_error("attn: this shape's launch takes Q as codes only "
+                 "(rp_fp8_attn_q16_supported)");
+    return RP_ERR_UNSUPPORTED;
+  }
+  a.q = nullptr;
+  a.q16 = static_cast<const uint16_t*>(q);
+  a.qsb = qsb; a.qsh = qsh; a.qss = qss;
+  a.q_dt = q_dtype == RP_DTYPE_F16 ? kInF16 : kInBf16;
+  if (kv_splits == 0)
+    return run_balanced(a, B, H, Sq, Skv, D, mask, out_dtype, workspace, workspace_bytes, stream);
+  return run_split(a, B, H, Sq, Skv, D, out_dtype, kv_splits, workspace, workspace_bytes, stream);
 }

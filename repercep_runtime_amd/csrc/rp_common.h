@@ -90,6 +90,20 @@ __device__ __forceinline__ float clamp_e4m3(float v) {
   return (v != v) ? v : c;
 }
 
+// Four 16-bit inputs (two packed pairs, element 0 in the low half of
+// lo_pair) -> one dword of e4m3fn codes: the quantizer's
+// clamp(x * qm, +-448) cast (qm = fp32 1 / dequant).  Shared by the
+// quantizer and the attention kernels that quantize their own Q rows, so
+// both produce the same codes.
+template <int DT>
+__device__ __forceinline__ uint32_t quant4(uint32_t lo_pair, uint32_t hi_pair, float qm) {
+  const float a = clamp_e4m3(in_to_f32<DT>(lo_pair & 0xffffu) * qm);
+  const float b = clamp_e4m3(in_to_f32<DT>(lo_pair >> 16) * qm);
+  const float c = clamp_e4m3(in_to_f32<DT>(hi_pair & 0xffffu) * qm);
+  const float d = clamp_e4m3(in_to_f32<DT>(hi_pair >> 16) * qm);
+  return pack4_e4m3(a, b, c, d);
+}
+
 // ---------------------------------------------------------- reductions
 template <typename T>
 __device__ __forceinline__ T shfl_xor(T v, int mask) {

@@ -351,7 +351,9 @@ static int qkv_plan(const void* q, const void* k, const void* v, int x_dtype, in
                     int64_t vss, int granularity, const float* dequant_out, const uint8_t* q8,
                     const uint8_t* k8, const uint8_t* vt8, int64_t ldv, Plan* pq, Plan* pk,
                     Plan* pv, size_t* off_k, size_t* off_v, size_t* need) {
-  if (q == nullptr || k == nullptr || v == nullptr || dequant_out == nullptr || q8 == nullptr ||
+  // q8 may be null: Q's scale only (an attention launch that quantizes its
+  // own Q rows from the input, rp_fp8_attn_fwd_q16)
+  if (q == nullptr || k == nullptr || v == nullptr || dequant_out == nullptr ||
       k8 == nullptr || vt8 == nullptr) {
     rp_set_error("scale_quantize_qkv: null pointer");
     return RP_ERR_INVALID_ARGUMENT;
@@ -410,7 +412,9 @@ static int qkv_launch(const Plan& pq, const Plan& pk, const Plan& pv, const void
   if ((rc = check_launch("amax_multi"))) return rc;
   const int64_t vt_stiles = ldv / 128, vt_dtiles = (D + 63) / 64;
   const int64_t vt_blocks = vt_stiles * vt_dtiles * B * H;
-  if (max(pq.p.nbg, max(pk.p.nbg, pv.p.nbg)) <= kFoldMaxPartials &&
+  // (Q's scale alone needs the finalize launch: in the folded apply, Q's
+  // own apply blocks write it)
+  if (q8 != nullptr && max(pq.p.nbg, max(pk.p.nbg, pv.p.nbg)) <= kFoldMaxPartials &&
       max(apply_blocks, vt_blocks) <= 0x7fffffff) {
     QParams vt{};
     vt.x = static_cast<const uint16_t*>(v);
@@ -424,16 +428,26 @@ static int qkv_launch(const Plan& pq, const Plan& pk, const Plan& pv, const void
                          vt, ldv, vt_stiles, vt_dtiles, vt8);
     return check_launch("apply_fold_multi");
   }
+  // the Q and K codes (blockIdx.y 0 and 1), or K's alone (as job 0) when q8
+  // is null
+  QJobs3 apply_jobs = jobs;
+  int n_apply = 2;
+  int64_t blocks = apply_blocks;
+  if (q8 == nullptr) {
+    apply_jobs.j0 = jobs.j1;
+    n_apply = 1;
+    blocks = jobs.j1.nblocks;
+  }
   if (x_dtype == RP_DTYPE_F16) {
     hipLaunchKernelGGL(finalize_multi_kernel<kInF16>, dim3((unsigned)ng, 3), dim3(kQThreads), 0,
                        st, jobs);
-    hipLaunchKernelGGL(apply_multi_kernel<kInF16>, dim3((unsigned)apply_blocks, 2),
-                       dim3(kQThreads), 0, st, jobs);
+    hipLaunchKernelGGL(apply_multi_kernel<kInF16>, dim3((unsigned)blocks, n_apply),
+                       dim3(kQThreads), 0, st, apply_jobs);
   } else {
     hipLaunchKernelGGL(finalize_multi_kernel<kInBf16>, dim3((unsigned)ng, 3), dim3(kQThreads), 0,
                        st, jobs);
-    hipLaunchKernelGGL(apply_multi_kernel<kInBf16>, dim3((unsigned)apply_blocks, 2),
-                       dim3(kQThreads), 0, st, jobs);
+    hipLaunchKernelGGL(apply_multi_kernel<kInBf16>, dim3((unsigned)blocks, n_apply),
+                       dim3(kQThreads), 0, st, apply_jobs);
   }
   if ((rc = check_launch("apply_multi"))) return rc;
   // V^T: its own grid shape

@@ -103,15 +103,6 @@ __device__ __forceinline__ void scale_finalize_body(int64_t blk_id, const uint32
 }
 
 
-template <int DT>
-__device__ __forceinline__ uint32_t quant4(uint32_t lo_pair, uint32_t hi_pair, float qm) {
-  const float a = clamp_e4m3(in_to_f32<DT>(lo_pair & 0xffffu) * qm);
-  const float b = clamp_e4m3(in_to_f32<DT>(lo_pair >> 16) * qm);
-  const float c = clamp_e4m3(in_to_f32<DT>(hi_pair & 0xffffu) * qm);
-  const float d = clamp_e4m3(in_to_f32<DT>(hi_pair >> 16) * qm);
-  return pack4_e4m3(a, b, c, d);
-}
-
 
 // Contiguous (B, H, S, D) input: group g is the flat element range
 // [g*gsize, (g+1)*gsize).  Each block takes kElemsPerBlock elements of one

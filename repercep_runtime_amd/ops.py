@@ -214,11 +214,14 @@ def scale_quantize_qkv(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
 
 
 def _qkv_arena(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, granularity: Granularity,
-               stream: int | None) -> tuple[torch.Tensor, tuple[int, int, int], int, int]:
+               stream: int | None, q_codes: bool = True
+               ) -> tuple[torch.Tensor, tuple[int, int, int], int, int]:
     """The quantizer call of ``scale_quantize_qkv`` into one uint8 arena:
     (arena, (byte offsets of k8, vt8 and the 3G fp32 scales; q8 at 0), G =
     scales per tensor, ldv).  ``fp8_flash_attention`` launches from the
-    arena's pointers without building tensor views."""
+    arena's pointers without building tensor views.  ``q_codes=False``
+    computes Q's scale without its codes (the arena then starts with k8),
+    for the attention launch that quantizes Q itself."""
     dt = _in_dtype("q", q)
     for name, t in (("k", k), ("v", v)):
         if _in_dtype(name, t) != dt:
@@ -235,7 +238,7 @@ def _qkv_arena(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, granularity: G
     ldv = _round_up(Skv, V_PAD)
     nq, nk, nv = B * H * Sq * D, B * H * Skv * D, B * H * D * ldv
     ws = _qkv_ws_bytes(B, H, Sq, Skv, D, g)
-    o_k = _align(nq)
+    o_k = _align(nq) if q_codes else 0
     o_v = o_k + _align(nk)
     o_s = o_v + _align(nv)
     o_w = o_s + _align(3 * G * 4)
@@ -243,8 +246,9 @@ def _qkv_arena(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, granularity: G
     base = arena.data_ptr()
     C.check(C.lib().rp_fp8_scale_quantize_qkv(
         q.data_ptr(), k.data_ptr(), v.data_ptr(), dt, B, H, Sq, Skv, D, qsb, qsh, qss,
-        ksb, ksh, kss, vsb, vsh, vss, g, base + o_s, base, base + o_k, base + o_v, ldv,
-        base + o_w, ws, _stream(q) if stream is None else stream), "rp_fp8_scale_quantize_qkv")
+        ksb, ksh, kss, vsb, vsh, vss, g, base + o_s, base if q_codes else None, base + o_k,
+        base + o_v, ldv, base + o_w, ws, _stream(q) if stream is None else stream),
+        "rp_fp8_scale_quantize_qkv")
     return arena, (o_k, o_v, o_s), G, ldv
 
 
@@ -536,8 +540,7 @@ def fp8_flash_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *,
     if scale is None:
         scale = 1.0 / math.sqrt(D)
     st = _stream(q)
-    arena, (o_k, o_v, o_s), G, ldv = _qkv_arena(q, k, v, granularity, st)
-    base = arena.data_ptr()
+    Skv = k.shape[2]
     if out is None:
         out = torch.empty((B, H, Sq, D), dtype=out_dtype or q.dtype, device=q.device)
     else:
@@ -551,12 +554,28 @@ def fp8_flash_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *,
         mask, pre, suf = C.RP_MASK_SHARED_PREFIX, int(prefix_len), int(suffix_len or 0)
     else:
         mask, pre, suf = (C.RP_MASK_CAUSAL if causal else C.RP_MASK_NONE), 0, 1
+    # a resident-K/V launch known without a timed search quantizes Q itself:
+    # Q is read as it lies instead of written as codes and read back
+    if kv_splits is not None:
+        known = {"KV_SPLITS": int(kv_splits)}
+    else:
+        known = _known_launch(B, H, Sq, Skv, D, causal, prefix_len, suffix_len)
+    if known is not None:
+        block_m, splits = launch_of(known)
+        if (block_m == BLOCK_M and q.data_ptr() % 16 == 0
+                and all(x % 8 == 0 for x in q.stride()[:3]) and q.stride(3) == 1
+                and q16_pays(B, H, Sq, Skv, D, mask, splits, st)):
+            _qkv_q16_attention(q, k, v, granularity, st, out, odt, float(scale), mask, pre, suf,
+                               splits)
+            return out
+    arena, (o_k, o_v, o_s), G, ldv = _qkv_arena(q, k, v, granularity, st)
+    base = arena.data_ptr()
     # the quantizer's own outputs in the arena: contiguous codes, fp32
     # scales, one per head or one per tensor
     stride = 1 if G == B * H and B * H > 1 else 0
     args = (base, base + o_k, base + o_v, ldv, base + o_s, base + o_s + 4 * G,
             base + o_s + 8 * G, stride, float(scale), out.data_ptr(), odt,
-            out.stride(0), out.stride(1), out.stride(2), B, H, Sq, k.shape[2], D, mask, pre, suf)
+            out.stride(0), out.stride(1), out.stride(2), B, H, Sq, Skv, D, mask, pre, suf)
 
     def run(cfg: dict) -> torch.Tensor:
         block_m, splits = launch_of(cfg)
@@ -564,9 +583,144 @@ def fp8_flash_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *,
         _launch_attention(args, splits, block_m, arena.device, st)
         return out
 
-    if kv_splits is not None:
-        return run({"KV_SPLITS": int(kv_splits)})
-    return run(_resolve_launch(B, H, Sq, k.shape[2], D, causal, prefix_len, suffix_len, run))
+    if known is not None:
+        return run(known)
+    return run(_resolve_launch(B, H, Sq, Skv, D, causal, prefix_len, suffix_len, run))
+
+
+def _known_launch(B: int, H: int, Sq: int, Skv: int, D: int, causal: bool,
+                  prefix_len: int | None, suffix_len: int | None) -> dict | None:
+    """The launch configuration ``_resolve_launch`` returns for a shape when
+    it needs no timed search (autotuning off, or a cached entry), else None."""
+    if tuning.autotune_disabled():
+        return dict(tuning.FALLBACK_CONFIG)
+    cfg = tuning.resolve_config(B, H, Sq, Skv, D, causal, prefix_len, suffix_len)
+    return cfg or None
+
+
+def scale_quantize_kv(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                      granularity: Granularity = "bh"
+                      ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor,
+                                 torch.Tensor]:
+    """(q_scale, k_scale, k8, v_scale, vt8): ``scale_quantize_qkv`` without
+    Q's codes (rp_fp8_scale_quantize_qkv with q8 = NULL), for
+    ``attention_fp8_q16``, which quantizes Q's rows itself."""
+    arena, (o_k, o_v, o_s), G, ldv = _qkv_arena(q, k, v, granularity, None, q_codes=False)
+    B, H, _, D = q.shape
+    Skv = k.shape[2]
+    nk, nv = B * H * Skv * D, B * H * D * ldv
+    dq = arena[o_s:o_s + 3 * G * 4].view(torch.float32)
+    k8 = arena[o_k:o_k + nk].view(B, H, Skv, D).view(torch.float8_e4m3fn)
+    vt8 = arena[o_v:o_v + nv].view(B, H, D, ldv).view(torch.float8_e4m3fn)
+    return dq[:G], dq[G:2 * G], k8, dq[2 * G:], vt8
+
+
+def q16_pays(B: int, H: int, Sq: int, Skv: int, D: int, mask: int, kv_splits: int,
+             stream: int) -> bool:
+    """Whether ``fp8_flash_attention`` hands this launch Q as it lies: the
+    resident-K/V launch (one key range).  Its step (Q's amax, K/V codes,
+    attention) measured 0.94-0.95 -> 0.86 ms at C3 cross, the attention kernel
+    0.54 -> 0.63 ms with Q's quantization inside it; the self-attention
+    launches are VALU-bound through many more key tiles per Q row and gained
+    nothing (C3 self: quantize 0.92 -> 0.73 ms, attention +0.15-0.25 ms)."""
+    if kv_splits not in (0, 1):
+        return False
+    L = C.lib()
+    return bool(L.rp_fp8_attn_resident_kv(B, H, Sq, Skv, D, mask, 1)
+                and L.rp_fp8_attn_q16_supported(B, H, Sq, Skv, D, mask, kv_splits, stream))
+
+
+def attention_q16_supported(B: int, H: int, Sq: int, Skv: int, D: int, causal: bool = False,
+                            prefix_len: int | None = None, kv_splits: int = 1) -> bool:
+    """Whether ``attention_fp8_q16`` runs this shape with ``kv_splits``
+    (rp_fp8_attn_q16_supported: every launch but the multi-block one)."""
+    mask = (C.RP_MASK_SHARED_PREFIX if prefix_len is not None
+            else C.RP_MASK_CAUSAL if causal else C.RP_MASK_NONE)
+    return bool(C.lib().rp_fp8_attn_q16_supported(B, H, Sq, Skv, D, mask, int(kv_splits),
+                                                    torch.cuda.current_stream().cuda_stream))
+
+
+def attention_fp8_q16(q: torch.Tensor, k8: torch.Tensor, vt8: torch.Tensor,
+                      q_scale: torch.Tensor, k_scale: torch.Tensor, v_scale: torch.Tensor,
+                      sm_scale: float, *, out: torch.Tensor | None = None,
+                      out_dtype: torch.dtype | None = None, causal: bool = False,
+                      prefix_len: int | None = None, suffix_len: int | None = None,
+                      kv_splits: int = 1) -> torch.Tensor:
+    """``attention_fp8`` with Q as its bf16/fp16 (B, H, Sq, D) input
+    (any 16-byte aligned strides, contiguous head dim) and its scale(s):
+    each workgroup quantizes the Q rows it reads with the quantizer's
+    arithmetic (rp_fp8_attn_fwd_q16), so the output equals
+    ``attention_fp8`` on ``scale_quantize_qkv``'s codes bit for bit.
+    ``kv_splits`` 0 (balanced), 1 or more; no short-query launch."""
+    qdt = _in_dtype("q", q)
+    _on_device_of(q, k8=k8, vt8=vt8, q_scale=q_scale, k_scale=k_scale, v_scale=v_scale,
+                  out=out)
+    B, H, Sq, D, qsb, qsh, qss = _bhsd_view(q)
+    for name, t in (("k8", k8), ("vt8", vt8)):
+        if t.dtype not in (torch.float8_e4m3fn, torch.uint8) or not t.is_contiguous():
+            raise ValueError(f"{name} must hold contiguous e4m3fn codes")
+    Skv = k8.shape[2]
+    if k8.shape != (B, H, Skv, D) or vt8.shape[:3] != (B, H, D):
+        raise ValueError(f"operand shapes disagree: q {tuple(q.shape)}, k8 {tuple(k8.shape)}, "
+                         f"vt8 {tuple(vt8.shape)}")
+    n = q_scale.numel()
+    if not (n == k_scale.numel() == v_scale.numel()) or n not in (1, B * H):
+        raise ValueError("scales must all have B*H or 1 elements")
+    if kv_splits < 0:
+        raise ValueError(f"kv_splits={kv_splits} must be >= 0")
+    stride = 1 if n == B * H and B * H > 1 else 0
+    if out is None:
+        out = torch.empty((B, H, Sq, D), dtype=out_dtype or q.dtype, device=q.device)
+    if out.shape != (B, H, Sq, D) or out.stride(3) != 1:
+        raise ValueError("out must be (B, H, Sq, D) with a contiguous last dimension")
+    odt = _OUT_DTYPES.get(out.dtype)
+    if odt is None:
+        raise TypeError(f"out dtype {out.dtype} not supported (bfloat16, float16 or float32)")
+    if prefix_len is not None:
+        mask, pre, suf = C.RP_MASK_SHARED_PREFIX, int(prefix_len), int(suffix_len or 0)
+    else:
+        mask, pre, suf = (C.RP_MASK_CAUSAL if causal else C.RP_MASK_NONE), 0, 1
+    qs = q_scale.to(torch.float32).contiguous()
+    ks = k_scale.to(torch.float32).contiguous()
+    vs = v_scale.to(torch.float32).contiguous()
+    st = _stream(q)
+    L = C.lib()
+    if kv_splits == 0:
+        nbytes = L.rp_fp8_attn_balanced_workspace_bytes(B, H, Sq, Skv, D, mask, st)
+    else:
+        nbytes = L.rp_fp8_attn_workspace_bytes(B, H, Sq, D, kv_splits) if kv_splits > 1 else 0
+    ws = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=q.device)
+    C.check(L.rp_fp8_attn_fwd_q16(
+        q.data_ptr(), qdt, qsb, qsh, qss, k8.data_ptr(), vt8.data_ptr(), vt8.shape[3],
+        qs.data_ptr(), ks.data_ptr(), vs.data_ptr(), stride, float(sm_scale), out.data_ptr(),
+        odt, out.stride(0), out.stride(1), out.stride(2), B, H, Sq, Skv, D, mask, pre, suf,
+        int(kv_splits), ws.data_ptr(), ws.numel(), st), "rp_fp8_attn_fwd_q16")
+    return out
+
+
+def _qkv_q16_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                       granularity: Granularity, st: int, out: torch.Tensor, odt: int,
+                       scale: float, mask: int, pre: int, suf: int, kv_splits: int) -> None:
+    """Scales of Q, K and V with K's and V^T's codes (rp_fp8_scale_quantize_qkv
+    with no Q codes), then the attention that quantizes Q's rows itself
+    (rp_fp8_attn_fwd_q16): the same codes and output as the two-step path."""
+    B, H, Sq, D = q.shape
+    Skv = k.shape[2]
+    arena, (o_k, o_v, o_s), G, ldv = _qkv_arena(q, k, v, granularity, st, q_codes=False)
+    base = arena.data_ptr()
+    stride = 1 if G == B * H and B * H > 1 else 0
+    L = C.lib()
+    if kv_splits == 0:
+        nbytes = L.rp_fp8_attn_balanced_workspace_bytes(B, H, Sq, Skv, D, mask, st)
+    else:
+        nbytes = L.rp_fp8_attn_workspace_bytes(B, H, Sq, D, kv_splits) if kv_splits > 1 else 0
+    ws = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=q.device)
+    qsb, qsh, qss, _ = q.stride()
+    C.check(L.rp_fp8_attn_fwd_q16(
+        q.data_ptr(), _IN_DTYPES[q.dtype], qsb, qsh, qss, base + o_k, base + o_v, ldv,
+        base + o_s, base + o_s + 4 * G, base + o_s + 8 * G, stride, scale, out.data_ptr(), odt,
+        out.stride(0), out.stride(1), out.stride(2), B, H, Sq, Skv, D, mask, pre, suf,
+        kv_splits, ws.data_ptr(), ws.numel(), st), "rp_fp8_attn_fwd_q16")
 
 
 def _time_call(fn: Callable[[], object], reps: int = 10, rounds: int = 3) -> float:
