@@ -84,10 +84,13 @@ __device__ __forceinline__ uint32_t pack4_e4m3(float a, float b, float c, float 
   return (uint32_t)r;
 }
 
-// Reference clamp: Tensor.clamp(-448, 448) propagates NaN.
+// Reference clamp: Tensor.clamp(-448, 448) propagates NaN.  The IEEE
+// 754-2019 minimum and maximum (v_minimum3_f32, v_maximum3_f32 on gfx950)
+// propagate it themselves: two instructions instead of a min, a max, a
+// compare and a select (the NaN's sign and payload may change; its e4m3
+// code is a NaN code either way).
 __device__ __forceinline__ float clamp_e4m3(float v) {
-  float c = fminf(fmaxf(v, -kE4m3Max), kE4m3Max);
-  return (v != v) ? v : c;
+  return __builtin_elementwise_maximum(__builtin_elementwise_minimum(v, kE4m3Max), -kE4m3Max);
 }
 
 // Four 16-bit inputs (two packed pairs, element 0 in the low half of
