@@ -1944,12 +1944,15 @@ void attn_kvres_kernel(AttnArgs a) {
 
     // ---- the head's tasks, wave by wave, as one stream of (task, tile)
     // steps.  Step i computes tile j = i % n_kb of the wave's task i / n_kb:
-    // its row max, then P in two halves (score blocks 0-1, then 2-3).  The
-    // S^T MFMAs of step i + 1 go out into the score registers each half has
-    // consumed -- the first pair between the halves, the second after -- so
-    // they run under the second half's VALU work and the P.V MFMAs of step
-    // i; the wave waits on MFMA results only where the next max needs them.
-    // A task's Q^T is loaded one task ahead.
+    // its row max, then P in two halves (score blocks 0-1, then 2-3), then
+    // one block of MFMAs: step i + 1's S^T into the consumed score
+    // registers, then step i's P.V.  The wave waits on MFMA results only
+    // where the next max needs them.  The block runs at raised wave priority,
+    // so that its MFMAs go out ahead of the other wave's softmax on the SIMD
+    // and run under it.  (Step i + 1's first S^T pair issued between the
+    // halves, into the registers the first half had consumed, measured 2.5%
+    // slower at C3 cross: the waves' MFMA and VALU stretches overlapped
+    // less.)  A task's Q^T is loaded one task ahead.
     auto load_q = [&](i32x8 (&dst)[G::KSTEPS], int64_t task) __attribute__((always_inline)) {
       const int qr = min((int)(task - (int64_t)bh * nq) * 32 + lq, a.Sq - 1);
       const uint8_t* src = qh + (int64_t)qr * D + 32 * lg;
@@ -2055,11 +2058,8 @@ void attn_kvres_kernel(AttnArgs a) {
           pw[wd] = (int)pack4_e4m3(p0, p1, p2, p3);
         }
         pop[m] = i32x8{pw[0], pw[1], pw[2], pw[3], pw[4], pw[5], pw[6], pw[7]};
-        // score blocks 2m, 2m + 1 are consumed: step i + 1's S^T into them
-        // (issued after the last step too, on valid operands, and never
-        // read: a conditional issue would keep the consumed scores live).
         // qop is step i + 1's Q^T: at a task's last tile it takes the next
-        // task's rows before the first pair goes out.
+        // task's rows before step i + 1's S^T goes out
         if (m == 0 && ends_task) {
           if constexpr (Q16) {
             qcodes(qop, qnraw);
@@ -2071,10 +2071,15 @@ void attn_kvres_kernel(AttnArgs a) {
           }
         }
         __builtin_amdgcn_sched_barrier(0);
-        s_pair(jn, 2 * m, qop);
-        __builtin_amdgcn_sched_barrier(0);
       }
       const float psum = (ps[0] + ps[1]) + (ps[2] + ps[3]);
+      // the scores are consumed: step i + 1's S^T into them (issued after
+      // the last step too, on valid operands, and never read: a conditional
+      // issue would keep the consumed scores live)
+      __builtin_amdgcn_s_setprio(1);
+      s_pair(jn, 0, qop);
+      s_pair(jn, 2, qop);
+      __builtin_amdgcn_sched_barrier(0);
       // P.V: V^T operands read through a ring two MFMAs ahead (all eight at
       // once would hold 64 registers); the first tile of a task starts O^T
       // from the product, the others rescale it first
@@ -2108,6 +2113,7 @@ void attn_kvres_kernel(AttnArgs a) {
         }
         pv(std::false_type{});
       }
+      __builtin_amdgcn_s_setprio(0);
       if (ends_task) {
         const int64_t task = first + (int64_t)t * kWsWaves;
         const int q = (int)(task - (int64_t)bh * nq) * 32 + lq;
