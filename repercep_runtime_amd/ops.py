@@ -52,7 +52,14 @@ _OUT_DTYPES = {torch.bfloat16: C.RP_OUT_BF16, torch.float16: C.RP_OUT_F16,
                torch.float32: C.RP_OUT_F32}
 
 
+# torch's accessor of the current stream's raw handle (what its own kernels
+# launch on), without building a Stream object on every call
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def _stream(t: torch.Tensor) -> int:
+    if _raw_stream is not None:
+        return _raw_stream(t.get_device())
     return torch.cuda.current_stream(t.device).cuda_stream
 
 
@@ -214,18 +221,23 @@ def scale_quantize_qkv(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
 
 
 def _qkv_arena(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, granularity: Granularity,
-               stream: int | None, q_codes: bool = True
+               stream: int | None, q_codes: bool = True, dtype_code: int | None = None
                ) -> tuple[torch.Tensor, tuple[int, int, int], int, int]:
     """The quantizer call of ``scale_quantize_qkv`` into one uint8 arena:
     (arena, (byte offsets of k8, vt8 and the 3G fp32 scales; q8 at 0), G =
     scales per tensor, ldv).  ``fp8_flash_attention`` launches from the
     arena's pointers without building tensor views.  ``q_codes=False``
     computes Q's scale without its codes (the arena then starts with k8),
-    for the attention launch that quantizes Q itself."""
-    dt = _in_dtype("q", q)
-    for name, t in (("k", k), ("v", v)):
-        if _in_dtype(name, t) != dt:
-            raise TypeError(f"q, k, v dtypes differ ({q.dtype}, {k.dtype}, {v.dtype})")
+    for the attention launch that quantizes Q itself.
+    (``dtype_code``: the caller has checked q, k and v for one supported
+    dtype, this RP_DTYPE_* code.)"""
+    if dtype_code is None:
+        dt = _in_dtype("q", q)
+        for name, t in (("k", k), ("v", v)):
+            if _in_dtype(name, t) != dt:
+                raise TypeError(f"q, k, v dtypes differ ({q.dtype}, {k.dtype}, {v.dtype})")
+    else:
+        dt = dtype_code
     B, H, Sq, D, qsb, qsh, qss = _bhsd_view(q)
     _, _, Skv, _, ksb, ksh, kss = _bhsd_view(k)
     _, _, _, _, vsb, vsh, vss = _bhsd_view(v)
@@ -525,8 +537,9 @@ def fp8_flash_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *,
     the shape; else a timed search over ``tuning.candidate_configs`` whose
     winner is recorded (see ``repercep_runtime_amd.tuning``).
     """
-    for name, t in (("q", q), ("k", k), ("v", v)):
-        _in_dtype(name, t)
+    dt = _in_dtype("q", q)
+    _in_dtype("k", k)
+    _in_dtype("v", v)
     if not (q.dtype == k.dtype == v.dtype):
         raise TypeError(f"q, k, v dtypes differ ({q.dtype}, {k.dtype}, {v.dtype})")
     if q.dim() != 4 or k.dim() != 4 or v.dim() != 4:
@@ -568,7 +581,7 @@ def fp8_flash_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *,
             _qkv_q16_attention(q, k, v, granularity, st, out, odt, float(scale), mask, pre, suf,
                                splits)
             return out
-    arena, (o_k, o_v, o_s), G, ldv = _qkv_arena(q, k, v, granularity, st)
+    arena, (o_k, o_v, o_s), G, ldv = _qkv_arena(q, k, v, granularity, st, dtype_code=dt)
     base = arena.data_ptr()
     # the quantizer's own outputs in the arena: contiguous codes, fp32
     # scales, one per head or one per tensor
