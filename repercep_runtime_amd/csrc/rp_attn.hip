@@ -352,6 +352,21 @@ __device__ __forceinline__ QRaw32 qraw_load(const uint16_t* p) {
   const i32x4* s = reinterpret_cast<const i32x4*>(p);
   return QRaw32{{s[0], s[1], s[2], s[3]}};
 }
+//
+// bf16 rows skip the quantizer's clamp to +-448.  The attention launches
+// take Q's scale as the quantizer computed it from Q itself, bf16(max(amax,
+// 1e-6) / 425.6), and for every finite bf16 amax fl(amax * qm) <= 426.67
+// (the largest, at amax = 1.043e-6), so |x * qm| never reaches 448 and the
+// clamp never binds: the codes are the quantizer's.  A NaN or infinite
+// element makes the scale non-finite and every code of the group NaN or 0
+// either way.  This saves two of the 4.5 instructions per element.  fp16
+// scales can round to subnormals or 0 (977 fp16 amax values give
+// |amax * qm| > 448), so fp16 rows keep the clamp.
+__device__ __forceinline__ uint32_t quant4_bf16_own_scale(uint32_t lo_pair, uint32_t hi_pair,
+                                                          float qm) {
+  return pack4_e4m3(bf16_to_f32(lo_pair & 0xffffu) * qm, bf16_to_f32(lo_pair >> 16) * qm,
+                    bf16_to_f32(hi_pair & 0xffffu) * qm, bf16_to_f32(hi_pair >> 16) * qm);
+}
 __device__ __forceinline__ i32x8 qraw_codes(const QRaw32& r, float qm, int dt) {
   i32x8 c;
 #pragma unroll
@@ -362,8 +377,8 @@ __device__ __forceinline__ i32x8 qraw_codes(const QRaw32& r, float qm, int dt) {
       c[2 * m] = (int)quant4<kInF16>(x, y, qm);
       c[2 * m + 1] = (int)quant4<kInF16>(z, t, qm);
     } else {
-      c[2 * m] = (int)quant4<kInBf16>(x, y, qm);
-      c[2 * m + 1] = (int)quant4<kInBf16>(z, t, qm);
+      c[2 * m] = (int)quant4_bf16_own_scale(x, y, qm);
+      c[2 * m + 1] = (int)quant4_bf16_own_scale(z, t, qm);
     }
   }
   return c;

@@ -163,3 +163,52 @@ def test_op_runs_the_q16_launch_with_the_code_path_bits(gpu: torch.device,
                                  out_dtype=torch.bfloat16)
         torch.cuda.synchronize()
         assert torch.equal(got.view(torch.uint8), want.view(torch.uint8)), name
+
+
+@pytest.mark.parametrize("Sq,Skv", [(1000, 1000), (9000, 512)], ids=["one_range", "resident_kv"])
+def test_q16_codes_at_the_extreme_scales(gpu: torch.device, Sq: int, Skv: int) -> None:
+    """bf16 rows are quantized without the clamp (Q's own scale keeps every
+    |x * qm| <= 426.67).  Heads whose maxima sit at that worst case
+    (amax 1.043e-6), at 1e-6 and below (the scale's floor), and at large
+    magnitudes: the raw-Q launch equals the code launch bit for bit."""
+    B, H, D = 1, (40 if Skv == 512 else 4), 128
+    if Skv == 512:
+        assert _capi.lib().rp_fp8_attn_resident_kv(B, H, Sq, Skv, D, 0, 1) == 1
+    q, k, v = _inputs(f"ext{Sq}", B, H, Sq, Skv, D, torch.bfloat16, "bhsd", gpu)
+    worst = torch.tensor(1.043081283569336e-06).to(torch.bfloat16).float().item()
+    for h, amax in enumerate((worst, 1e-6, 3e-7, 3.0e4)):
+        qh = q[0, h].float()
+        qh = qh / qh.abs().max() * amax
+        q[0, h] = qh.to(torch.bfloat16)
+        q[0, h, 7, 5] = torch.tensor(amax).to(torch.bfloat16)     # the maximum itself
+    for gran in ("bh", "tensor"):
+        qs, q8, ks, k8, vs, vt8 = ops.scale_quantize_qkv(q, k, v, gran)
+        want = ops.attention_fp8(q8.view(torch.uint8), k8.view(torch.uint8),
+                                 vt8.view(torch.uint8), qs, ks, vs, D ** -0.5,
+                                 out_dtype=torch.float32, kv_splits=1)
+        got = torch.empty_like(want)
+        print(f"extreme scales Sq={Sq} Skv={Skv} {gran}", flush=True)
+        rc = _q16_call(q, k8.view(torch.uint8), vt8.view(torch.uint8), qs, ks, vs, got,
+                       D ** -0.5, 0, 1)
+        assert rc == 0, _capi.lib().rp_last_error()
+        assert torch.equal(got, want), gran
+
+
+def test_q16_non_finite_head(gpu: torch.device) -> None:
+    """A NaN in one head's Q makes that head's scale NaN: both launches give
+    that head NaN everywhere and every other head the same bits."""
+    B, H, Sq, Skv, D = 1, 40, 9000, 512, 128
+    assert _capi.lib().rp_fp8_attn_resident_kv(B, H, Sq, Skv, D, 0, 1) == 1
+    q, k, v = _inputs("nanq", B, H, Sq, Skv, D, torch.bfloat16, "bhsd", gpu)
+    q[0, 2, 100, 3] = float("nan")
+    qs, q8, ks, k8, vs, vt8 = ops.scale_quantize_qkv(q, k, v, "bh")
+    keep = [h for h in range(H) if h != 2]
+    assert torch.isnan(qs[2]) and torch.isfinite(qs[keep]).all()
+    want = ops.attention_fp8(q8.view(torch.uint8), k8.view(torch.uint8), vt8.view(torch.uint8),
+                             qs, ks, vs, D ** -0.5, out_dtype=torch.float32, kv_splits=1)
+    got = torch.empty_like(want)
+    rc = _q16_call(q, k8.view(torch.uint8), vt8.view(torch.uint8), qs, ks, vs, got, D ** -0.5,
+                   0, 1)
+    assert rc == 0, _capi.lib().rp_last_error()
+    assert torch.isnan(got[0, 2]).all() and torch.isnan(want[0, 2]).all()
+    assert torch.equal(got[0, keep], want[0, keep])

@@ -180,6 +180,31 @@ def test_fp16_scale_every_amax() -> None:
     assert np.isinf(want[n - 2]) and np.isnan(want[n - 1])     # inf and NaN maxima propagate
 
 
+def test_own_scale_keeps_bf16_rows_inside_the_clamp() -> None:
+    """The attention launches that quantize Q's bf16 rows themselves
+    (rp_fp8_attn_fwd_q16) leave out the clamp to +-448: with the group's own
+    scale, |x| <= amax gives |fl(x * qm)| <= fl(amax * qm), and over every
+    finite bf16 amax that product stays <= 426.67, so the clamp never binds.
+    For fp16 the scale can round to a subnormal or to 0, the product passes
+    448 on 977 amax values, and those rows keep the clamp."""
+    vals = _all_bf16()
+    amax = vals.to(torch.float32).abs()
+    fin = torch.isfinite(amax)
+    amax_b = vals[fin].abs()
+    dq = quant.per_group_dequant(amax_b.reshape(1, -1, 1, 1)).numpy()
+    qm = (np.float32(1.0) / dq).astype(np.float32)
+    prod = (amax_b.to(torch.float32).numpy() * qm).astype(np.float32)
+    assert np.isfinite(prod).all()
+    assert prod.max() <= 448.0 and abs(float(prod.max()) - 426.6667) < 1e-3
+    worst = float(amax_b[int(prod.argmax())].to(torch.float32))
+    assert abs(worst - 1.043081e-6) < 1e-12
+    f16 = _all_f16()[:-2]                     # every finite non-negative fp16 value
+    dq16 = quant.per_group_dequant(f16.reshape(1, -1, 1, 1)).numpy()
+    with np.errstate(divide="ignore", invalid="ignore"):
+        p16 = (f16.to(torch.float32).numpy() * (np.float32(1.0) / dq16)).astype(np.float32)
+    assert int((p16 > 448.0).sum()) == 977
+
+
 def _bf16_rne(x: np.float32) -> np.float32:
     u = np.array([x], dtype=np.float32).view(np.uint32)[0]
     u = (u + 0x7FFF + ((u >> 16) & 1)) & 0xFFFF0000
