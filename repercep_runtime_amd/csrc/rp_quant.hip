@@ -128,7 +128,11 @@ __global__ __launch_bounds__(kQThreads) void apply_multi_kernel(QJobs3 jobs) {
 // rounding as the finalize kernel -- and the first block of each group
 // writes it, so the scales need no launch of their own, and V^T's tiles
 // (blockIdx.y == 2) run in the same launch: two launches per call instead
-// of four, which is what bounds calls this small.
+// of four, which is what bounds calls this small.  Without Q's codes (an
+// attention launch that quantizes Q itself) only K and V need to be small:
+// job 0 has no codes, and its first ngroups blocks fold Q's partials into
+// Q's scales, however many there are (the finalize kernel's work, one block
+// per group).
 constexpr int64_t kFoldMaxPartials = 256;
 
 template <int DT>
@@ -141,6 +145,13 @@ __global__ __launch_bounds__(kQThreads) void apply_fold_multi_kernel(QJobs3 jobs
   const QJob& jb = job_of(jobs);
   const int64_t blk = blockIdx.x;
   if (blockIdx.y < 2) {
+    if (jb.codes == nullptr) {   // Q's scales only
+      if (blk >= jb.p.ngroups) return;
+      const float dq = dequant_from_amax<DT>(
+          block_max_u32<kQThreads>(jb.partial + blk * jb.p.nbg, jb.p.nbg));
+      if (threadIdx.x == 0) jb.dequant[blk] = dq;
+      return;
+    }
     if (blk >= jb.nblocks) return;
     const int64_t g = blk / jb.p.nbg;
     const float dq =
@@ -412,14 +423,16 @@ static int qkv_launch(const Plan& pq, const Plan& pk, const Plan& pv, const void
   if ((rc = check_launch("amax_multi"))) return rc;
   const int64_t vt_stiles = ldv / 128, vt_dtiles = (D + 63) / 64;
   const int64_t vt_blocks = vt_stiles * vt_dtiles * B * H;
-  // (Q's scale alone needs the finalize launch: in the folded apply, Q's
-  // own apply blocks write it)
-  if (q8 != nullptr && max(pq.p.nbg, max(pk.p.nbg, pv.p.nbg)) <= kFoldMaxPartials &&
-      max(apply_blocks, vt_blocks) <= 0x7fffffff) {
+  // (with Q's codes, Q's own apply blocks write its scale; without them,
+  // job 0's first blocks do, from any number of partials)
+  const int64_t fold_blocks =
+      max(q8 != nullptr ? apply_blocks : max(jobs.j1.nblocks, ng), vt_blocks);
+  if ((q8 == nullptr || pq.p.nbg <= kFoldMaxPartials) &&
+      max(pk.p.nbg, pv.p.nbg) <= kFoldMaxPartials && fold_blocks <= 0x7fffffff) {
     QParams vt{};
     vt.x = static_cast<const uint16_t*>(v);
     vt.B = B; vt.H = H; vt.S = Skv; vt.D = D; vt.sb = vsb; vt.sh = vsh; vt.ss = vss;
-    const dim3 grid((unsigned)max(apply_blocks, vt_blocks), 3);
+    const dim3 grid((unsigned)fold_blocks, 3);
     if (x_dtype == RP_DTYPE_F16)
       hipLaunchKernelGGL(apply_fold_multi_kernel<kInF16>, grid, dim3(kQThreads), 0, st, jobs, vt,
                          ldv, vt_stiles, vt_dtiles, vt8);
