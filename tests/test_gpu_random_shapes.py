@@ -17,7 +17,11 @@ every launch, all bit-identical to each other), a relative mean error of
 (the kernel and the oracle differ only by fp32 rounding and the rare P code
 it flips), 5e-2 for launches that split the keys (each range quantizes P
 against its own running max; the reference runs one range,
-kernels/triton_kernels/fp8_flash_attn.py:334-391).  GEMM shapes: every
+kernels/triton_kernels/fp8_flash_attn.py:334-391).  A second set calls
+fp8_flash_attention as a caller does, over two batches, fp16 input,
+(B, S, H, D) views, causal and shared-prefix masks and a caller's softmax
+scale, against the oracle's torch restatement of the quantizer (rows whose
+mask leaves them fewer than 256 keys take the few-key bound).  GEMM shapes: every
 output a bf16 rounding of a value near the exact sum, as in
 tests/test_gpu_gemm.py, with B in the reference's (K, N) layout or
 transposed.
@@ -113,6 +117,91 @@ def test_random_attention_shape_vs_oracle(gpu: torch.device, case: tuple,
         assert np.isfinite(got).all(), f"{name} h={h}: non-finite output"
         assert st["max_abs"] <= max_tol and st["mean_abs"] <= mean_tol, (name, h, st)
         assert st["rel_mean"] <= rel_tol, (name, h, st)
+
+
+def _op_cases() -> list[tuple]:
+    rng = random.Random(4417)
+    cases = []
+    for i in range(20):
+        D = rng.choice([32, 64, 128, 128, 256])
+        B = rng.choice([1, 2])
+        H = rng.randint(1, 6)
+        mask = rng.choice(["none", "none", "causal", "prefix"])
+        if mask == "prefix":
+            suffix = rng.choice([1, 4, 8, 16])
+            Sq = suffix * rng.randint(1, 40)
+            prefix = rng.randint(1, 900)
+            Skv = prefix + Sq
+        else:
+            suffix = prefix = None
+            Sq, Skv = rng.randint(1, 2000), rng.randint(1, 2600)
+        scale = rng.choice([None, None, round(rng.uniform(0.03, 0.3), 4)])
+        dtype = rng.choice([torch.bfloat16, torch.float16])
+        layout = rng.choice(["bhsd", "bshd"])
+        gran = rng.choice(["bh", "tensor"])
+        odt = rng.choice([None, torch.float32])
+        cases.append((f"o{i}_{mask}", B, H, Sq, Skv, D, mask, prefix, suffix, scale, dtype,
+                      layout, gran, odt))
+    return cases
+
+
+OP_CASES = _op_cases()
+
+
+@pytest.mark.parametrize("case", OP_CASES, ids=[c[0] for c in OP_CASES])
+def test_random_op_call_vs_oracle(gpu: torch.device, case: tuple,
+                                  monkeypatch: pytest.MonkeyPatch) -> None:
+    """fp8_flash_attention as a caller runs it on seeded inputs the cases
+    above leave out: two batches, fp16 input, (B, S, H, D) memory viewed as
+    (B, H, S, D), causal and shared-prefix masks, a caller's softmax scale;
+    the oracle quantizes with the reference's torch expressions (fp16 scale
+    included) and replays one key range."""
+    from oracle import quant
+    (name, B, H, Sq, Skv, D, mask, prefix, suffix, scale, dtype, layout, gran,
+     odt) = case
+    monkeypatch.setenv("REPERCEP_FP8_DISABLE_AUTOTUNE", "1")
+    g = torch.Generator().manual_seed(sum(map(ord, name)) + 7)
+
+    def make(S: int) -> torch.Tensor:
+        if layout == "bshd":
+            return torch.randn(B, S, H, D, generator=g).to(dtype).permute(0, 2, 1, 3)
+        return torch.randn(B, H, S, D, generator=g).to(dtype)
+
+    q, k, v = make(Sq), make(Skv), make(Skv)
+    print(f"{name}: B={B} H={H} Sq={Sq} Skv={Skv} D={D} mask={mask} prefix={prefix} "
+          f"suffix={suffix} scale={scale} {dtype} {layout} scales per {gran} out={odt}",
+          flush=True)
+    kw = {"prefix_len": prefix, "suffix_len": suffix} if mask == "prefix" else {}
+    out = ops.fp8_flash_attention(q.to(gpu), k.to(gpu), v.to(gpu), causal=mask == "causal",
+                                  scale=scale, granularity=gran, out_dtype=odt, **kw)
+    torch.cuda.synchronize()
+    assert out.dtype == (odt or dtype) and out.shape == (B, H, Sq, D)
+    out = out.float().cpu().numpy()
+    sm = scale if scale is not None else 1.0 / math.sqrt(D)
+    qs, q8 = quant.quantize_codes(q.contiguous(), gran)
+    ks, k8 = quant.quantize_codes(k.contiguous(), gran)
+    vs, v8 = quant.quantize_codes(v.contiguous(), gran)
+    mcode = {"none": 0, "causal": 1, "prefix": 2}[mask]
+    rng = np.random.default_rng(len(name) + Sq)
+    rows = np.unique(np.concatenate([[0, Sq - 1], rng.integers(0, Sq, 32)]))
+    for b in range(B):
+        for h in sorted({0, H - 1}):
+            si = b * H + h if gran == "bh" else 0
+            ref = native.attn_rows(q8[b, h], k8[b, h], v8[b, h], qs[si], ks[si], vs[si], sm,
+                                   rows, block_n=ops.BLOCK_N, mask=mcode, prefix=prefix or 0,
+                                   suffix=suffix or 1)
+            if (odt or dtype) != torch.float32:
+                ref = torch.from_numpy(ref).to(odt or dtype).float().numpy()
+            got = out[b, h][rows]
+            st = err_stats(got, ref)
+            max_tol, mean_tol = baseline_tolerance(ref)
+            if Skv < 256 or mask != "none":   # rows that see fewer than 256 keys
+                max_tol = max(max_tol, 6e-2 * max(1.0, float(np.abs(ref).max())))
+            print(f"  b={b} h={h}: {st} (tol max {max_tol:.3g}, mean {mean_tol:.3g})",
+                  flush=True)
+            assert np.isfinite(got).all(), f"{name} b={b} h={h}: non-finite output"
+            assert st["max_abs"] <= max_tol and st["mean_abs"] <= mean_tol, (name, b, h, st)
+            assert st["rel_mean"] <= 1e-2, (name, b, h, st)
 
 
 def _gemm_cases() -> list[tuple]:
