@@ -271,8 +271,8 @@ int rp_fp8_attn_resident_kv(int B, int H, int Sq, int Skv, int D, int mask, int 
  * quantizer's arithmetic -- the codes, and so the output, are those of the
  * separate quantizer and rp_fp8_attn_fwd*, bit for bit.  bf16 rows skip the
  * clamp to +-448, which Q's own scale never reaches (|x / scale| <= 426.67);
- * with a smaller scale, elements past 464 * scale become NaN codes.  No counterpart in
- * the reference, whose wrapper writes Q's codes and reads them back
+ * with a smaller scale, elements past 464 * scale become NaN codes.  No
+ * counterpart in the reference, whose wrapper writes Q's codes and reads them back
  * (fp8_flash_attn.py:526-528, 604-644): this saves 3 of Q's 6 bytes per
  * element of HBM traffic.  Head dims 64, 128 and 256; the multi-block launch
  * of short key ranges that do not fit LDS takes codes only
