@@ -24,7 +24,8 @@ scale, against the oracle's torch restatement of the quantizer (rows whose
 mask leaves them fewer than 256 keys take the few-key bound).  GEMM shapes: every
 output a bf16 rounding of a value near the exact sum, as in
 tests/test_gpu_gemm.py, with B in the reference's (K, N) layout or
-transposed.
+transposed, and the bias and row-scaled epilogues on their own seeded
+shapes.
 """
 
 from __future__ import annotations
@@ -230,3 +231,67 @@ def test_random_gemm_shape_is_one_rounding_of_the_exact_sum(gpu: torch.device,
     _assert_one_rounding_apart(c.float().cpu().numpy(), None, a8.numpy(), bt8.numpy(),
                                float(np.float32(sa) * np.float32(sb)))
     assert _capi.lib() is not None
+
+
+def _epilogue_cases() -> list[tuple]:
+    rng = random.Random(911)
+    cases = []
+    for i in range(12):
+        kind = "bias" if i % 2 == 0 else "rowwise"
+        Z = 1 if kind == "bias" else rng.randint(1, 3)
+        M = rng.randint(1, 1300)
+        N = 16 * rng.randint(1, 90) if kind == "bias" else 4 * rng.randint(1, 300)
+        K = rng.choice([64 * rng.randint(1, 20), 16 * rng.randint(1, 40)])
+        kn = rng.random() < 0.5 and kind == "bias"   # the row-scaled op takes B^T only
+        cases.append((f"e{i}_{kind}", kind, Z, M, N, K, kn))
+    return cases
+
+
+EPI_CASES = _epilogue_cases()
+
+
+@pytest.mark.parametrize("case", EPI_CASES, ids=[c[0] for c in EPI_CASES])
+def test_random_gemm_epilogues(gpu: torch.device, case: tuple) -> None:
+    """The bias epilogue (bf16(fp32(fp32(acc * s) + bias)), as a bf16
+    nn.Linear rounds) and the row-scaled one (bf16((acc * s_m) * s_n), the
+    unfused attention's grouped GEMM) on seeded shapes, both tile kernels
+    (K % 64 picks the large tiles): every output one rounding of a value
+    within the MFMA's sum error plus the epilogue's fp32 roundings of the
+    exact result."""
+    from oracle.quant import DECODE
+    name, kind, Z, M, N, K, kn = case
+    print(f"{name}: Z={Z} M={M} N={N} K={K} B {'(K, N)' if kn else '(N, K)'}", flush=True)
+    g = torch.Generator().manual_seed(sum(map(ord, name)) + M)
+    a8 = (torch.randn(Z, M, K, generator=g) * 30).to(torch.float8_e4m3fn)
+    bt8 = (torch.randn(Z, N, K, generator=g) * 30).to(torch.float8_e4m3fn)
+    if kind == "bias":
+        bias = (torch.randn(N, generator=g) * 50).to(torch.bfloat16)
+        sa, sb = 0.013, 0.0071
+        if kn:
+            got = ops.fp8_gemm(a8[0].to(gpu), bt8[0].t().contiguous().to(gpu), sa, sb,
+                               bias=bias.to(gpu))
+        else:
+            got = ops.fp8_gemm(a8[0].to(gpu), bt8[0].to(gpu), sa, sb, b_transposed=True,
+                               bias=bias.to(gpu))
+        torch.cuda.synchronize()
+        _assert_one_rounding_apart(got.float().cpu().numpy(), None,
+                                   a8[0].view(torch.uint8).numpy(),
+                                   bt8[0].view(torch.uint8).numpy(),
+                                   float(np.float32(sa) * np.float32(sb)),
+                                   bias.float().numpy().astype(np.float64))
+        return
+    rs = torch.rand(Z, M, generator=g) * 0.02 + 1e-3
+    cs = torch.rand(Z, N, generator=g) * 0.02 + 1e-3
+    got = ops.gemm_rowwise(a8.to(gpu), bt8.to(gpu), rs.to(gpu), cs.to(gpu)).float().cpu().numpy()
+    A = DECODE[a8.view(torch.uint8).numpy()].astype(np.float64)
+    B = DECODE[bt8.view(torch.uint8).numpy()].astype(np.float64)
+    sc = rs.numpy().astype(np.float64)[:, :, None] * cs.numpy().astype(np.float64)[:, None, :]
+    exact = np.matmul(A, B.transpose(0, 2, 1)) * sc
+    eps = (2.0 ** -14 * np.matmul(np.abs(A), np.abs(B).transpose(0, 2, 1)) * sc
+           + 2.0 ** -22 * np.abs(exact))
+    lo = torch.from_numpy(exact - eps).float().to(torch.bfloat16).float().numpy()
+    hi = torch.from_numpy(exact + eps).float().to(torch.bfloat16).float().numpy()
+    bad = (got < np.minimum(lo, hi)) | (got > np.maximum(lo, hi))
+    print(f"  outside the rounding interval: {int(bad.sum())}", flush=True)
+    assert not bad.any(), name
+
